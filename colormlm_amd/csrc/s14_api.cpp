@@ -1,0 +1,542 @@
+// C ABI of the S14 path: contexts, bind/cmd dispatch, fused expert entry
+// points, the pool's device arena and the hipEvent fences.
+//
+// Replaces scheduler/ssd_inference/src/s14_vulkan.rs:187-498 (pipelines,
+// bind_*, cmd_*) and the Vulkan substrate it sits on (device.rs, buffer.rs,
+// compute.rs): a context owns a compute stream, a copy stream and one device
+// workspace; "binding" is validation into a plain record; "recording" is a
+// kernel launch on a stream; fences are hipEvents.
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstring>
+#include <new>
+
+#include "s14_device.hpp"
+#include "s14_internal.hpp"
+
+using s14::fail;
+
+struct s14_ctx {
+  int device = 0;
+  hipStream_t compute = nullptr;
+  hipStream_t copy = nullptr;
+  void *ws_base = nullptr;
+  s14::Workspace ws{};
+  s14::PageOffsets mx{}, fp8{};
+};
+
+struct s14_fence {
+  hipEvent_t ev = nullptr;
+};
+
+namespace {
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(S14_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define S14_HIP(call, what)                       \
+  do {                                            \
+    hipError_t _e = (call);                       \
+    if (_e != hipSuccess) return hip_fail(_e, what); \
+  } while (0)
+
+hipStream_t pick(s14_ctx *ctx, void *stream) {
+  return stream ? reinterpret_cast<hipStream_t>(stream) : ctx->compute;
+}
+
+uint64_t storage_bytes(uint64_t logical) { return (logical + 3) / 4 * 4; }
+
+int require_capacity(const s14_buffer &b, uint64_t required, const char *label) {
+  if (!b.ptr) return fail(S14_ERR_INVALID, "%s buffer is NULL", label);
+  if (b.bytes < required)
+    return fail(S14_ERR_CAPACITY, "%s buffer is %llu B, requires at least %llu B", label,
+                (unsigned long long)b.bytes, (unsigned long long)required);
+  return S14_OK;
+}
+
+s14::PageOffsets offsets_of(const s14_page_layout &l) { return {l.w1, l.s1, l.w3, l.s3, l.w2, l.s2}; }
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+int check_ctx(s14_ctx *ctx) {
+  if (!ctx) return fail(S14_ERR_INVALID, "NULL context");
+  return S14_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------
+
+extern "C" int s14_ctx_create(int device, s14_ctx **out) {
+  if (!out) return fail(S14_ERR_INVALID, "NULL context output");
+  *out = nullptr;
+  int count = 0;
+  S14_HIP(hipGetDeviceCount(&count), "hipGetDeviceCount");
+  if (device < 0 || device >= count) return fail(S14_ERR_INVALID, "device %d not present (%d visible)", device, count);
+  S14_HIP(hipSetDevice(device), "hipSetDevice");
+  s14_ctx *ctx = new (std::nothrow) s14_ctx();
+  if (!ctx) return fail(S14_ERR_INVALID, "out of host memory");
+  ctx->device = device;
+  hipError_t e = hipStreamCreateWithFlags(&ctx->compute, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->copy, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    s14_ctx_destroy(ctx);
+    return hip_fail(e, "hipStreamCreate");
+  }
+  // workspace: table | h | down | scores | biased | ids | weights | counters
+  size_t off = 0;
+  const size_t o_table = off;
+  off = align_up(off + sizeof(s14::PairTable), 256);
+  const size_t o_h = off;
+  off = align_up(off + sizeof(float) * s14::kMaxPairs * s14::kInter, 256);
+  const size_t o_down = off;
+  off = align_up(off + sizeof(float) * s14::kMaxPairs * s14::kHidden, 256);
+  const size_t o_scores = off;
+  off = align_up(off + sizeof(float) * s14::kMaxTokens * s14::kMaxExperts, 256);
+  const size_t o_biased = off;
+  off = align_up(off + sizeof(float) * s14::kMaxTokens * s14::kMaxExperts, 256);
+  const size_t o_ids = off;
+  off = align_up(off + sizeof(uint16_t) * s14::kMaxTokens * s14::kTopK, 256);
+  const size_t o_w = off;
+  off = align_up(off + sizeof(float) * s14::kMaxTokens * s14::kTopK, 256);
+  const size_t o_cnt = off;
+  off = align_up(off + sizeof(uint32_t) * s14::kNumCounters, 256);
+  e = hipMalloc(&ctx->ws_base, off);
+  if (e != hipSuccess) {
+    s14_ctx_destroy(ctx);
+    return hip_fail(e, "hipMalloc(workspace)");
+  }
+  uint8_t *b = static_cast<uint8_t *>(ctx->ws_base);
+  ctx->ws.table = reinterpret_cast<s14::PairTable *>(b + o_table);
+  ctx->ws.h = reinterpret_cast<float *>(b + o_h);
+  ctx->ws.down = reinterpret_cast<float *>(b + o_down);
+  ctx->ws.scores = reinterpret_cast<float *>(b + o_scores);
+  ctx->ws.biased = reinterpret_cast<float *>(b + o_biased);
+  ctx->ws.ids = reinterpret_cast<uint16_t *>(b + o_ids);
+  ctx->ws.weights = reinterpret_cast<float *>(b + o_w);
+  ctx->ws.counters = reinterpret_cast<uint32_t *>(b + o_cnt);
+  ctx->ws.bytes = off;
+  // Completion counters start at zero and every launch leaves them at zero,
+  // so this is the only clear (no memset inside launch sequences).
+  e = hipMemset(ctx->ws_base, 0, off);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    s14_ctx_destroy(ctx);
+    return hip_fail(e, "hipMemset(workspace)");
+  }
+  s14_page_layout l;
+  s14_page_layout_get(S14_PAGE_MXFP4, S14_HIDDEN, S14_INTER, &l);
+  ctx->mx = offsets_of(l);
+  s14_page_layout_get(S14_PAGE_FP8, S14_HIDDEN, S14_INTER, &l);
+  ctx->fp8 = offsets_of(l);
+  *out = ctx;
+  s14::clear_error();
+  return S14_OK;
+}
+
+extern "C" void s14_ctx_destroy(s14_ctx *ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->compute) (void)hipStreamSynchronize(ctx->compute);
+  if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
+  if (ctx->ws_base) (void)hipFree(ctx->ws_base);
+  if (ctx->compute) (void)hipStreamDestroy(ctx->compute);
+  if (ctx->copy) (void)hipStreamDestroy(ctx->copy);
+  delete ctx;
+}
+
+extern "C" void *s14_ctx_compute_stream(s14_ctx *ctx) { return ctx ? ctx->compute : nullptr; }
+extern "C" void *s14_ctx_copy_stream(s14_ctx *ctx) { return ctx ? ctx->copy : nullptr; }
+
+extern "C" int s14_ctx_synchronize(s14_ctx *ctx) {
+  if (int rc = check_ctx(ctx)) return rc;
+  S14_HIP(hipStreamSynchronize(ctx->compute), "hipStreamSynchronize(compute)");
+  S14_HIP(hipStreamSynchronize(ctx->copy), "hipStreamSynchronize(copy)");
+  return S14_OK;
+}
+
+namespace s14 {
+int pool_alloc_arena(s14_ctx *ctx, uint64_t bytes, uint8_t **out) {
+  S14_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  void *p = nullptr;
+  S14_HIP(hipMalloc(&p, bytes), "hipMalloc(pool arena)");
+  *out = static_cast<uint8_t *>(p);
+  return S14_OK;
+}
+void pool_free_arena(s14_ctx *ctx, uint8_t *base) {
+  if (ctx) (void)hipSetDevice(ctx->device);
+  (void)hipFree(base);
+}
+}  // namespace s14
+
+// ---------------------------------------------------------------------------
+// bind (s14_vulkan.rs:206-334)
+// ---------------------------------------------------------------------------
+
+extern "C" int s14_bind_mxfp4(s14_shape shape, s14_buffer x, s14_buffer w, s14_buffer sc, s14_buffer y,
+                              int mode, s14_mxfp4_dispatch *out) {
+  if (!out) return fail(S14_ERR_INVALID, "NULL dispatch output");
+  s14_shape_bytes b;
+  if (int rc = s14_shape_validate_mxfp4(shape, &b)) return rc;
+  if (mode != S14_MODE_EXACT && mode != S14_MODE_FAST) return fail(S14_ERR_INVALID, "unknown mode %d", mode);
+  if (int rc = require_capacity(x, b.input_bytes, "S14 MXFP4 input")) return rc;
+  if (int rc = require_capacity(w, storage_bytes(b.weight_bytes), "S14 MXFP4 weight")) return rc;
+  if (int rc = require_capacity(sc, storage_bytes(b.scale_bytes), "S14 MXFP4 scale")) return rc;
+  if (int rc = require_capacity(y, b.output_bytes, "S14 MXFP4 output")) return rc;
+  if (reinterpret_cast<uintptr_t>(x.ptr) % 16 || reinterpret_cast<uintptr_t>(w.ptr) % 16 ||
+      reinterpret_cast<uintptr_t>(sc.ptr) % 4)
+    return fail(S14_ERR_INVALID, "S14 MXFP4 buffers need 16-byte x/weight and 4-byte scale alignment");
+  *out = s14_mxfp4_dispatch{shape, static_cast<const float *>(x.ptr), static_cast<const uint8_t *>(w.ptr),
+                            static_cast<const uint8_t *>(sc.ptr), static_cast<float *>(y.ptr), mode};
+  return S14_OK;
+}
+
+extern "C" int s14_bind_fp8(s14_shape shape, s14_buffer x, int x_dtype, s14_buffer w, s14_buffer sc,
+                            int scale_dtype, s14_buffer y, int mode, s14_fp8_dispatch *out) {
+  if (!out) return fail(S14_ERR_INVALID, "NULL dispatch output");
+  s14_shape_bytes b;
+  if (int rc = s14_shape_validate_fp8(shape, &b)) return rc;
+  if (mode != S14_MODE_EXACT && mode != S14_MODE_FAST) return fail(S14_ERR_INVALID, "unknown mode %d", mode);
+  if (x_dtype != S14_X_F32 && x_dtype != S14_X_BF16) return fail(S14_ERR_INVALID, "unknown x dtype %d", x_dtype);
+  if (scale_dtype != S14_SCALE_UE8M0 && scale_dtype != S14_SCALE_F32)
+    return fail(S14_ERR_INVALID, "unknown scale dtype %d", scale_dtype);
+  const uint64_t x_bytes = x_dtype == S14_X_BF16 ? uint64_t(shape.k) * 2 : b.input_bytes;
+  const uint64_t s_bytes = scale_dtype == S14_SCALE_F32 ? b.scale_bytes * 4 : storage_bytes(b.scale_bytes);
+  if (int rc = require_capacity(x, x_bytes, "S14 FP8 input")) return rc;
+  if (int rc = require_capacity(w, storage_bytes(b.weight_bytes), "S14 FP8 weight")) return rc;
+  if (int rc = require_capacity(sc, s_bytes, "S14 FP8 scale")) return rc;
+  if (int rc = require_capacity(y, b.output_bytes, "S14 FP8 output")) return rc;
+  *out = s14_fp8_dispatch{shape, x.ptr, static_cast<const uint8_t *>(w.ptr), sc.ptr,
+                          static_cast<float *>(y.ptr), x_dtype, scale_dtype, mode};
+  return S14_OK;
+}
+
+extern "C" int s14_bind_swiglu_limit(uint32_t n, s14_buffer gate, s14_buffer up, s14_buffer y,
+                                     s14_swiglu_dispatch *out) {
+  if (!out) return fail(S14_ERR_INVALID, "NULL dispatch output");
+  if (n == 0) return fail(S14_ERR_SHAPE, "S14 SwiGLU requires non-zero length");
+  const uint64_t bytes = uint64_t(n) * 4;
+  if (int rc = require_capacity(gate, bytes, "S14 SwiGLU gate")) return rc;
+  if (int rc = require_capacity(up, bytes, "S14 SwiGLU up")) return rc;
+  if (int rc = require_capacity(y, bytes, "S14 SwiGLU output")) return rc;
+  *out = s14_swiglu_dispatch{n, static_cast<const float *>(gate.ptr), static_cast<const float *>(up.ptr),
+                             static_cast<float *>(y.ptr)};
+  return S14_OK;
+}
+
+extern "C" int s14_bind_route_mix(uint32_t n, float w, s14_buffer expert, s14_buffer routed,
+                                  s14_scale_dispatch *out) {
+  if (!out) return fail(S14_ERR_INVALID, "NULL dispatch output");
+  if (n == 0 || !std::isfinite(w) || w < 0.0f)
+    return fail(S14_ERR_INVALID, "S14 route mix requires non-zero length and finite non-negative weight");
+  const uint64_t bytes = uint64_t(n) * 4;
+  if (int rc = require_capacity(expert, bytes, "S14 route mix expert")) return rc;
+  if (int rc = require_capacity(routed, bytes, "S14 route mix output")) return rc;
+  *out = s14_scale_dispatch{n, w, static_cast<const float *>(expert.ptr), static_cast<float *>(routed.ptr)};
+  return S14_OK;
+}
+
+extern "C" int s14_bind_moe_accumulate(uint32_t n, float w, s14_buffer expert, s14_buffer acc,
+                                       s14_scale_dispatch *out) {
+  if (!out) return fail(S14_ERR_INVALID, "NULL dispatch output");
+  if (n == 0 || !std::isfinite(w) || w < 0.0f)
+    return fail(S14_ERR_INVALID, "S14 MoE accumulate requires non-zero length and finite non-negative weight");
+  const uint64_t bytes = uint64_t(n) * 4;
+  if (int rc = require_capacity(expert, bytes, "S14 MoE accumulate expert")) return rc;
+  if (int rc = require_capacity(acc, bytes, "S14 MoE accumulator")) return rc;
+  *out = s14_scale_dispatch{n, w, static_cast<const float *>(expert.ptr), static_cast<float *>(acc.ptr)};
+  return S14_OK;
+}
+
+// ---------------------------------------------------------------------------
+// cmd (s14_vulkan.rs:338-416)
+// ---------------------------------------------------------------------------
+
+#define S14_LAUNCH(call, what)                      \
+  do {                                              \
+    hipError_t _e = (call);                         \
+    if (_e != hipSuccess) return hip_fail(_e, what); \
+    return S14_OK;                                  \
+  } while (0)
+
+extern "C" int s14_cmd_mxfp4_matvec(s14_ctx *ctx, void *stream, const s14_mxfp4_dispatch *d) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!d) return fail(S14_ERR_INVALID, "NULL dispatch");
+  S14_LAUNCH(s14::launch_mxfp4_matvec(pick(ctx, stream), *d), "mxfp4_matvec launch");
+}
+extern "C" int s14_cmd_fp8_matvec(s14_ctx *ctx, void *stream, const s14_fp8_dispatch *d) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!d) return fail(S14_ERR_INVALID, "NULL dispatch");
+  S14_LAUNCH(s14::launch_fp8_matvec(pick(ctx, stream), *d), "fp8_matvec launch");
+}
+extern "C" int s14_cmd_swiglu_limit(s14_ctx *ctx, void *stream, const s14_swiglu_dispatch *d) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!d) return fail(S14_ERR_INVALID, "NULL dispatch");
+  S14_LAUNCH(s14::launch_swiglu(pick(ctx, stream), *d), "swiglu launch");
+}
+extern "C" int s14_cmd_route_mix(s14_ctx *ctx, void *stream, const s14_scale_dispatch *d) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!d) return fail(S14_ERR_INVALID, "NULL dispatch");
+  S14_LAUNCH(s14::launch_route_mix(pick(ctx, stream), *d), "route_mix launch");
+}
+extern "C" int s14_cmd_moe_accumulate(s14_ctx *ctx, void *stream, const s14_scale_dispatch *d) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!d) return fail(S14_ERR_INVALID, "NULL dispatch");
+  S14_LAUNCH(s14::launch_moe_accumulate(pick(ctx, stream), *d), "moe_accumulate launch");
+}
+
+extern "C" int s14_dequant_mxfp4(s14_ctx *ctx, void *stream, s14_shape shape, const uint8_t *packed,
+                                 const uint8_t *scale, float *out) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = s14_shape_validate_mxfp4(shape, nullptr)) return rc;
+  if (!packed || !scale || !out) return fail(S14_ERR_INVALID, "NULL dequant buffer");
+  S14_LAUNCH(s14::launch_dequant_mxfp4(pick(ctx, stream), shape, packed, scale, out), "dequant launch");
+}
+
+extern "C" int s14_dequant_fp8(s14_ctx *ctx, void *stream, s14_shape shape, const uint8_t *weight,
+                               const void *scale, int scale_dtype, float *out) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = s14_shape_validate_fp8(shape, nullptr)) return rc;
+  if (!weight || !scale || !out) return fail(S14_ERR_INVALID, "NULL dequant buffer");
+  S14_LAUNCH(s14::launch_dequant_fp8(pick(ctx, stream), shape, weight, scale, scale_dtype, out),
+             "dequant launch");
+}
+
+extern "C" int s14_fill_mxfp4_page(s14_ctx *ctx, void *stream, uint8_t *page, uint64_t seed, uint32_t layer,
+                                   uint32_t expert, uint32_t hidden, uint32_t inter, int lo_exp, int hi_exp) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!page) return fail(S14_ERR_INVALID, "NULL page");
+  if (hi_exp < lo_exp || 127 + lo_exp < 0 || 127 + hi_exp > 254)
+    return fail(S14_ERR_INVALID, "scale exponent range [%d, %d] invalid", lo_exp, hi_exp);
+  s14_page_layout l;
+  if (int rc = s14_page_layout_get(S14_PAGE_MXFP4, hidden, inter, &l)) return rc;
+  if (reinterpret_cast<uintptr_t>(page) % 8) return fail(S14_ERR_INVALID, "page must be 8-byte aligned");
+  S14_LAUNCH(s14::launch_fill_mxfp4_page(pick(ctx, stream), page, seed, layer, expert, hidden, inter, lo_exp,
+                                         hi_exp, offsets_of(l)),
+             "fill launch");
+}
+
+// ---------------------------------------------------------------------------
+// fused expert entry points
+// ---------------------------------------------------------------------------
+
+namespace {
+
+int check_mode(int mode) {
+  if (mode != S14_MODE_EXACT && mode != S14_MODE_FAST) return fail(S14_ERR_INVALID, "unknown mode %d", mode);
+  return S14_OK;
+}
+
+int check_router(const s14_router *r) {
+  if (!r || !r->weight || !r->bias) return fail(S14_ERR_INVALID, "router weight/bias missing");
+  if (r->n_experts == 0 || r->n_experts > uint32_t(s14::kMaxExperts))
+    return fail(S14_ERR_SHAPE, "router n_experts=%u outside 1..%d", r->n_experts, s14::kMaxExperts);
+  if (r->topk == 0 || r->topk > uint32_t(s14::kTopK) || r->topk > r->n_experts)
+    return fail(S14_ERR_SHAPE, "router topk=%u outside 1..%d", r->topk, s14::kTopK);
+  if (r->score_fn != S14_SCORE_SIGMOID && r->score_fn != S14_SCORE_SQRT_SOFTPLUS)
+    return fail(S14_ERR_INVALID, "unknown score function %d", r->score_fn);
+  if (!std::isfinite(r->route_scale) || r->route_scale <= 0.0f)
+    return fail(S14_ERR_INVALID, "route_scale must be finite and positive");
+  return S14_OK;
+}
+
+s14::RouterArgs router_args(const s14_router *r) {
+  return s14::RouterArgs{r->weight, r->bias, r->n_experts, r->topk, r->score_fn, r->route_scale};
+}
+
+int run_phases(s14_ctx *ctx, hipStream_t st, uint32_t n_pairs, uint32_t tokens, const float *x, float *y,
+               int mode) {
+  S14_LAUNCH(s14::launch_layer_phases(st, ctx->ws, n_pairs, tokens, ctx->mx, ctx->fp8, x, y, mode),
+             "layer phase launch");
+}
+
+}  // namespace
+
+extern "C" int s14_expert_chain(s14_ctx *ctx, void *stream, const uint8_t *page, const float *x, float route_w,
+                                float *y, int mode) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_mode(mode)) return rc;
+  if (!page || !x || !y) return fail(S14_ERR_INVALID, "NULL chain buffer");
+  if (!std::isfinite(route_w) || route_w < 0.0f)
+    return fail(S14_ERR_INVALID, "S14 route mix requires a finite non-negative weight");
+  s14::PairTable t{};
+  t.n_pairs = 1;
+  t.n_tokens = 1;
+  t.n_distinct = 1;
+  t.chain = 1;
+  t.page[0] = reinterpret_cast<uint64_t>(page);
+  t.fmt[0] = S14_PAGE_MXFP4;
+  t.weight[0] = route_w;
+  t.token_pairs[0][0] = 0;
+  t.token_npairs[0] = 1;
+  hipStream_t st = pick(ctx, stream);
+  hipError_t e = s14::launch_plan_from_host(st, ctx->ws, t);
+  if (e != hipSuccess) return hip_fail(e, "plan launch");
+  return run_phases(ctx, st, 1, 1, x, y, mode);
+}
+
+extern "C" int s14_moe_layer(s14_ctx *ctx, void *stream, uint32_t topk, const uint8_t *const *routed_pages,
+                             const float *route_weights, const uint8_t *shared_page, int shared_format,
+                             const float *x, float *y, int mode) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_mode(mode)) return rc;
+  if (topk > uint32_t(s14::kTopK)) return fail(S14_ERR_SHAPE, "topk=%u exceeds %d", topk, s14::kTopK);
+  if (topk == 0 && !shared_page) return fail(S14_ERR_SHAPE, "layer needs at least one expert");
+  if (!x || !y || (topk && (!routed_pages || !route_weights))) return fail(S14_ERR_INVALID, "NULL layer buffer");
+  if (shared_page && shared_format != S14_PAGE_MXFP4 && shared_format != S14_PAGE_FP8)
+    return fail(S14_ERR_INVALID, "unknown shared page format %d", shared_format);
+  s14::PairTable t{};
+  for (uint32_t i = 0; i < topk; ++i) {
+    if (!routed_pages[i]) return fail(S14_ERR_INVALID, "routed page %u is NULL", i);
+    const float w = route_weights[i];
+    if (!std::isfinite(w) || w < 0.0f)
+      return fail(S14_ERR_INVALID, "S14 MoE accumulate requires finite non-negative weight (route %u)", i);
+    t.page[i] = reinterpret_cast<uint64_t>(routed_pages[i]);
+    t.fmt[i] = S14_PAGE_MXFP4;
+    t.weight[i] = w;
+    t.token_pairs[0][i] = i;
+  }
+  uint32_t n = topk;
+  if (shared_page) {
+    t.page[n] = reinterpret_cast<uint64_t>(shared_page);
+    t.fmt[n] = uint32_t(shared_format);
+    t.weight[n] = 1.0f;
+    t.is_shared[n] = 1;
+    t.token_pairs[0][n] = n;
+    ++n;
+  }
+  t.n_pairs = n;
+  t.n_tokens = 1;
+  t.n_distinct = topk;
+  t.token_npairs[0] = n;
+  hipStream_t st = pick(ctx, stream);
+  hipError_t e = s14::launch_plan_from_host(st, ctx->ws, t);
+  if (e != hipSuccess) return hip_fail(e, "plan launch");
+  return run_phases(ctx, st, n, 1, x, y, mode);
+}
+
+extern "C" int s14_moe_block_route(s14_ctx *ctx, void *stream, uint32_t tokens, const s14_router *router,
+                                   const uint64_t *expert_pages_dev, const uint8_t *shared_page,
+                                   int shared_format, const float *x, float *y, uint16_t *ids_out,
+                                   float *weights_out, int mode) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_mode(mode)) return rc;
+  if (int rc = check_router(router)) return rc;
+  if (router->topk != uint32_t(s14::kTopK))
+    return fail(S14_ERR_SHAPE, "routed layer requires topk=%d", s14::kTopK);
+  if (tokens == 0 || tokens > uint32_t(s14::kMaxTokens))
+    return fail(S14_ERR_SHAPE, "block size %u outside 1..%d", tokens, s14::kMaxTokens);
+  if (!expert_pages_dev || !shared_page || !x || !y) return fail(S14_ERR_INVALID, "NULL layer buffer");
+  if (shared_format != S14_PAGE_MXFP4 && shared_format != S14_PAGE_FP8)
+    return fail(S14_ERR_INVALID, "unknown shared page format %d", shared_format);
+  hipStream_t st = pick(ctx, stream);
+  hipError_t e = s14::launch_router_plan(st, ctx->ws, router_args(router), tokens, x, expert_pages_dev,
+                                         shared_page, shared_format, ids_out, weights_out, 1);
+  if (e != hipSuccess) return hip_fail(e, "router launch");
+  return run_phases(ctx, st, tokens * (s14::kTopK + 1), tokens, x, y, mode);
+}
+
+extern "C" int s14_moe_layer_route(s14_ctx *ctx, void *stream, const s14_router *router,
+                                   const uint64_t *expert_pages_dev, const uint8_t *shared_page,
+                                   int shared_format, const float *x, float *y, uint16_t *ids_out,
+                                   float *weights_out, int mode) {
+  return s14_moe_block_route(ctx, stream, 1, router, expert_pages_dev, shared_page, shared_format, x, y,
+                             ids_out, weights_out, mode);
+}
+
+extern "C" int s14_last_block_distinct(s14_ctx *ctx, uint32_t *n_distinct) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!n_distinct) return fail(S14_ERR_INVALID, "NULL output");
+  // the launch may have gone to any stream of the device
+  S14_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  S14_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  S14_HIP(hipMemcpy(n_distinct, &ctx->ws.table->n_distinct, sizeof(uint32_t), hipMemcpyDeviceToHost),
+          "hipMemcpy(n_distinct)");
+  return S14_OK;
+}
+
+extern "C" int s14_route(s14_ctx *ctx, void *stream, const s14_router *router, uint32_t tokens,
+                         const float *x, float *scores_out, uint16_t *ids_out, float *weights_out) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_router(router)) return rc;
+  if (tokens == 0 || tokens > uint32_t(s14::kMaxTokens))
+    return fail(S14_ERR_SHAPE, "token count %u outside 1..%d", tokens, s14::kMaxTokens);
+  if (!x) return fail(S14_ERR_INVALID, "NULL router input");
+  hipStream_t st = pick(ctx, stream);
+  hipError_t e = s14::launch_router_plan(st, ctx->ws, router_args(router), tokens, x, nullptr, nullptr, 0,
+                                         ids_out, weights_out, 0);
+  if (e != hipSuccess) return hip_fail(e, "router launch");
+  if (scores_out) {
+    for (uint32_t t = 0; t < tokens; ++t) {
+      e = hipMemcpyAsync(scores_out + size_t(t) * router->n_experts, ctx->ws.scores + size_t(t) * s14::kMaxExperts,
+                         sizeof(float) * router->n_experts, hipMemcpyDeviceToDevice, st);
+      if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(scores)");
+    }
+  }
+  return S14_OK;
+}
+
+// ---------------------------------------------------------------------------
+// uploads and fences (replacing the Vulkan transfer/compute fences)
+// ---------------------------------------------------------------------------
+
+extern "C" int s14_pool_upload(s14_ctx *ctx, s14_pool *pool, const s14_loading_reservation *r,
+                               const void *host, uint64_t bytes, s14_fence **fence_out) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!pool || !r || !host || !fence_out) return fail(S14_ERR_INVALID, "NULL upload argument");
+  *fence_out = nullptr;
+  if (!pool->base) return fail(S14_ERR_INVALID, "pool has no device arena");
+  if (r->slot >= pool->n_slots) return fail(S14_ERR_INVALID, "invalid VRAM slot %u", r->slot);
+  if (pool->states[r->slot] != SlotState::Loading || !s14::key_eq(pool->state_keys[r->slot], r->key) ||
+      pool->generations[r->slot] != r->generation)
+    return fail(S14_ERR_STALE, "upload target slot %u is not the reservation's Loading generation", r->slot);
+  if (bytes > pool->slot_bytes)
+    return fail(S14_ERR_CAPACITY, "upload of %llu B exceeds slot of %llu B", (unsigned long long)bytes,
+                (unsigned long long)pool->slot_bytes);
+  S14_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  S14_HIP(hipMemcpyAsync(pool->base + uint64_t(r->slot) * pool->slot_bytes, host, bytes, hipMemcpyHostToDevice,
+                         ctx->copy),
+          "hipMemcpyAsync(upload)");
+  return s14_fence_record(ctx, ctx->copy, fence_out);
+}
+
+extern "C" int s14_fence_record(s14_ctx *ctx, void *stream, s14_fence **fence_out) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!fence_out) return fail(S14_ERR_INVALID, "NULL fence output");
+  *fence_out = nullptr;
+  s14_fence *f = new (std::nothrow) s14_fence();
+  if (!f) return fail(S14_ERR_INVALID, "out of host memory");
+  hipError_t e = hipEventCreateWithFlags(&f->ev, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(f->ev, pick(ctx, stream));
+  if (e != hipSuccess) {
+    if (f->ev) (void)hipEventDestroy(f->ev);
+    delete f;
+    return hip_fail(e, "hipEventRecord");
+  }
+  *fence_out = f;
+  return S14_OK;
+}
+
+extern "C" int s14_fence_query(s14_fence *fence) {
+  if (!fence) return fail(S14_ERR_INVALID, "NULL fence");
+  hipError_t e = hipEventQuery(fence->ev);
+  if (e == hipSuccess) return S14_OK;
+  if (e == hipErrorNotReady) return fail(S14_ERR_NOT_READY, "fence not yet signalled");
+  return hip_fail(e, "hipEventQuery");
+}
+
+extern "C" int s14_fence_wait(s14_fence *fence) {
+  if (!fence) return fail(S14_ERR_INVALID, "NULL fence");
+  S14_HIP(hipEventSynchronize(fence->ev), "hipEventSynchronize");
+  return S14_OK;
+}
+
+extern "C" void s14_fence_destroy(s14_fence *fence) {
+  if (!fence) return;
+  if (fence->ev) (void)hipEventDestroy(fence->ev);
+  delete fence;
+}

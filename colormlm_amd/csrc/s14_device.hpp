@@ -1,0 +1,108 @@
+// Launchers of the gfx950 kernels in s14_device.hip, called by the C ABI in
+// s14_api.cpp.  All pointers are device pointers; every launcher enqueues on
+// `stream` and returns the hipError_t of the launch.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#include "s14_hip.h"
+
+namespace s14 {
+
+constexpr int kMaxTokens = 8;
+constexpr int kTopK = 6;
+constexpr int kMaxPairs = kMaxTokens * (kTopK + 1);  // (token, expert) pairs incl. shared
+constexpr int kHidden = 4096;
+constexpr int kInter = 2048;
+constexpr int kMaxExperts = 256;
+
+// Exact-mode tiles: phase 1 = 32 rows of w1 + the same 32 rows of w3 per
+// wavefront; phase 2 = 64 rows of w2 per wavefront.
+constexpr int kP1ExactRows = 32;
+constexpr int kP2ExactRows = 64;
+// Fast-mode tiles.
+constexpr int kP1FastRowsPerWave = 4;
+constexpr int kP2FastRowsPerWave = 8;
+constexpr int kFastWaves = 4;
+constexpr int kP1FastRows = kP1FastRowsPerWave * kFastWaves;  // rows per block
+constexpr int kP2FastRows = kP2FastRowsPerWave * kFastWaves;
+constexpr int kMaxTiles = kHidden / 32;  // upper bound on phase-2 tiles of any mode
+
+// One (token, expert) unit of work of a layer or block launch.  Routed pairs
+// come first, sorted by expert id so that all tokens of one expert page are
+// consecutive in the grid; the shared expert's pairs follow.
+struct PairTable {
+  uint32_t n_pairs;
+  uint32_t n_tokens;
+  uint32_t n_distinct;  // distinct routed pages
+  uint32_t chain;       // 1: output = weight * down (the single-expert chain)
+  uint64_t page[kMaxPairs];
+  uint32_t fmt[kMaxPairs];
+  uint32_t token[kMaxPairs];
+  float weight[kMaxPairs];
+  uint32_t is_shared[kMaxPairs];
+  // accumulation order per token: routed pairs in route order, shared last
+  uint32_t token_pairs[kMaxTokens][kTopK + 1];
+  uint32_t token_npairs[kMaxTokens];
+};
+
+// Device workspace of a context (one allocation, carved by s14_api.cpp).
+struct Workspace {
+  PairTable *table;
+  float *h;           // [kMaxPairs][kInter]
+  float *down;        // [kMaxPairs][kHidden]
+  float *scores;      // [kMaxTokens][kMaxExperts]
+  float *biased;      // [kMaxTokens][kMaxExperts]
+  uint16_t *ids;      // [kMaxTokens][kTopK]
+  float *weights;     // [kMaxTokens][kTopK]
+  uint32_t *counters; // self-resetting completion counters (zero at rest)
+  size_t bytes;
+};
+// counters layout: [0, kMaxTokens) router per token; [kMaxTokens] plan;
+// [kCntAcc, kCntAcc + kMaxTokens*kMaxTiles) accumulate per (token, tile).
+constexpr int kCntPlan = kMaxTokens;
+constexpr int kCntAcc = 16;
+constexpr int kNumCounters = kCntAcc + kMaxTokens * kMaxTiles;
+
+struct PageOffsets {
+  uint64_t w1, s1, w3, s3, w2, s2;
+};
+
+struct RouterArgs {
+  const float *weight;
+  const float *bias;
+  uint32_t n_experts;
+  uint32_t topk;
+  int score_fn;
+  float route_scale;
+};
+
+// --- standalone dispatches (bind/cmd API) ---
+hipError_t launch_mxfp4_matvec(hipStream_t s, const s14_mxfp4_dispatch &d);
+hipError_t launch_fp8_matvec(hipStream_t s, const s14_fp8_dispatch &d);
+hipError_t launch_swiglu(hipStream_t s, const s14_swiglu_dispatch &d);
+hipError_t launch_route_mix(hipStream_t s, const s14_scale_dispatch &d);
+hipError_t launch_moe_accumulate(hipStream_t s, const s14_scale_dispatch &d);
+hipError_t launch_dequant_mxfp4(hipStream_t s, s14_shape shape, const uint8_t *w,
+                                const uint8_t *sc, float *out);
+hipError_t launch_dequant_fp8(hipStream_t s, s14_shape shape, const uint8_t *w, const void *sc,
+                              int scale_dtype, float *out);
+hipError_t launch_fill_mxfp4_page(hipStream_t s, uint8_t *page, uint64_t seed, uint32_t layer,
+                                  uint32_t expert, uint32_t hidden, uint32_t inter, int lo, int hi,
+                                  const PageOffsets &off);
+
+// --- fused layer / block path ---
+// Writes a PairTable for a host-known route (expert chain, route-given layer).
+hipError_t launch_plan_from_host(hipStream_t s, const Workspace &ws, const PairTable &plan);
+// Router for `tokens` tokens; the last block of each token selects the top-k,
+// and the last token to finish builds the PairTable (expert-major).
+hipError_t launch_router_plan(hipStream_t s, const Workspace &ws, const RouterArgs &r,
+                              uint32_t tokens, const float *x, const uint64_t *expert_pages,
+                              const uint8_t *shared_page, int shared_fmt, uint16_t *ids_out,
+                              float *weights_out, int build_plan);
+hipError_t launch_layer_phases(hipStream_t s, const Workspace &ws, uint32_t n_pairs,
+                               uint32_t tokens, const PageOffsets &mx, const PageOffsets &fp8,
+                               const float *x, float *y, int mode);
+
+}  // namespace s14

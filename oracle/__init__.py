@@ -1,0 +1,288 @@
+"""CPU oracle (test infrastructure only) — ctypes wrapper of libs14oracle.so.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this package, and only as the checker.  The C source (s14_oracle.c) restates
+the reference CPU F32 oracle of scheduler/ssd_inference/examples/
+s14_vulkan_numeric.rs:1543-1784 in its exact operation order; see the header
+of s14_oracle.h for what pins each function.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "libs14oracle.so"
+
+HIDDEN = 4096
+INTER = 2048
+SCORE_SIGMOID = 0
+SCORE_SQRT_SOFTPLUS = 1
+
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        _lib = C.CDLL(str(LIB))
+        _declare(_lib)
+    return _lib
+
+
+P = C.c_void_p
+U32, U64, I, F, D = C.c_uint32, C.c_uint64, C.c_int, C.c_float, C.c_double
+
+
+class _Expert(C.Structure):
+    _fields_ = [(n, P) for n in ("w1", "s1", "w3", "s3", "w2", "s2")]
+
+
+class ErrorStats(C.Structure):
+    _fields_ = [
+        ("max_abs", C.c_float),
+        ("mean_abs", C.c_double),
+        ("rmse", C.c_double),
+        ("max_rel_abs_ref_gt_1e_5", C.c_float),
+        ("finite", C.c_int),
+    ]
+
+    def as_dict(self):
+        return {
+            "max_abs": float(self.max_abs),
+            "mean_abs": float(self.mean_abs),
+            "rmse": float(self.rmse),
+            "max_rel_abs_ref_gt_1e_5": float(self.max_rel_abs_ref_gt_1e_5),
+            "finite": bool(self.finite),
+        }
+
+
+def _declare(L):
+    sig = {
+        "s14o_e2m1": (F, [C.c_uint8]),
+        "s14o_ue8m0": (F, [C.c_uint8]),
+        "s14o_e4m3fn": (F, [C.c_uint8]),
+        "s14o_bf16_to_f32": (F, [C.c_uint16]),
+        "s14o_f32_to_e4m3fn_rne_sat": (C.c_uint8, [F]),
+        "s14o_f32_to_bf16_rne": (C.c_uint16, [F]),
+        "s14o_dequant_mxfp4": (None, [U32, U32, P, P, P]),
+        "s14o_dequant_fp8_ue8m0": (None, [U32, U32, P, P, P]),
+        "s14o_mxfp4_matvec": (None, [U32, U32, P, P, P, P]),
+        "s14o_fp8_matvec_ue8m0": (None, [U32, U32, P, P, P, P]),
+        "s14o_fp8_matvec_f32scale_bf16x": (None, [U32, U32, P, P, P, P]),
+        "s14o_swiglu_limit": (None, [U32, P, P, P]),
+        "s14o_mxfp4_expert_down": (None, [U32, U32, P, C.POINTER(_Expert), P]),
+        "s14o_fp8_expert_down": (None, [U32, U32, P, C.POINTER(_Expert), P]),
+        "s14o_expert_chain": (None, [U32, U32, P, C.POINTER(_Expert), F, P]),
+        "s14o_moe_layer": (None, [U32, U32, P, U32, P, P, P, P, P]),
+        "s14o_router_logits": (None, [U32, U32, P, P, P]),
+        "s14o_route": (None, [U32, U32, P, P, P, I, U32, F, P, P, P]),
+        "s14o_error_stats_compute": (None, [C.c_size_t, P, P, C.POINTER(ErrorStats)]),
+        "s14o_requant_e4m3": (None, [U32, U32, U32, P, P, P]),
+        "s14o_num_threads": (I, []),
+        "s14o_set_num_threads": (None, [I]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be contiguous"
+    return a.ctypes.data
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _u8(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.uint8)
+
+
+# ---------------------------------------------------------------------------
+# decoders / encoders
+# ---------------------------------------------------------------------------
+
+
+def e2m1(code: int) -> float:
+    return float(np.float32(lib().s14o_e2m1(code)))
+
+
+def ue8m0(code: int) -> np.float32:
+    return np.float32(lib().s14o_ue8m0(code))
+
+
+def e4m3fn(code: int) -> np.float32:
+    return np.float32(lib().s14o_e4m3fn(code))
+
+
+def e4m3fn_encode(v: float) -> int:
+    return int(lib().s14o_f32_to_e4m3fn_rne_sat(float(np.float32(v))))
+
+
+def bf16_encode(v: float) -> int:
+    return int(lib().s14o_f32_to_bf16_rne(float(np.float32(v))))
+
+
+def dequant_mxfp4(packed: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    packed, scale = _u8(packed), _u8(scale)
+    n, pk = packed.shape
+    out = np.empty((n, pk * 2), dtype=np.float32)
+    lib().s14o_dequant_mxfp4(n, pk * 2, _p(packed), _p(scale), _p(out))
+    return out
+
+
+def dequant_fp8_ue8m0(w: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    w, scale = _u8(w), _u8(scale)
+    n, k = w.shape
+    out = np.empty((n, k), dtype=np.float32)
+    lib().s14o_dequant_fp8_ue8m0(n, k, _p(w), _p(scale), _p(out))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# matvecs, swiglu, experts, layer
+# ---------------------------------------------------------------------------
+
+
+def mxfp4_matvec(x, packed, scale) -> np.ndarray:
+    x, packed, scale = _f32(x), _u8(packed), _u8(scale)
+    n = packed.shape[0]
+    k = x.shape[0]
+    y = np.empty(n, dtype=np.float32)
+    lib().s14o_mxfp4_matvec(n, k, _p(x), _p(packed), _p(scale), _p(y))
+    return y
+
+
+def fp8_matvec_ue8m0(x, w, scale) -> np.ndarray:
+    x, w, scale = _f32(x), _u8(w), _u8(scale)
+    n, k = w.shape
+    y = np.empty(n, dtype=np.float32)
+    lib().s14o_fp8_matvec_ue8m0(n, k, _p(x), _p(w), _p(scale), _p(y))
+    return y
+
+
+def fp8_matvec_f32scale_bf16x(x_bf16, w, scale) -> np.ndarray:
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    w, scale = _u8(w), _f32(scale)
+    n, k = w.shape
+    y = np.empty(n, dtype=np.float32)
+    lib().s14o_fp8_matvec_f32scale_bf16x(n, k, _p(x), _p(w), _p(scale), _p(y))
+    return y
+
+
+def swiglu_limit(gate, up) -> np.ndarray:
+    gate, up = _f32(gate), _f32(up)
+    h = np.empty_like(gate)
+    lib().s14o_swiglu_limit(gate.size, _p(gate), _p(up), _p(h))
+    return h
+
+
+def page_offsets(fmt: str = "mxfp4", hidden: int = HIDDEN, inter: int = INTER):
+    """[w1|s1|w3|s3|w2|s2] byte offsets of an expert page."""
+    if fmt == "mxfp4":
+        up_w, up_s = inter * hidden // 2, inter * hidden // 32
+        dn_w, dn_s = hidden * inter // 2, hidden * inter // 32
+    else:
+        up_w, up_s = inter * hidden, -(-inter // 128) * -(-hidden // 128)
+        dn_w, dn_s = hidden * inter, -(-hidden // 128) * -(-inter // 128)
+    o = {"w1": 0}
+    o["s1"] = up_w
+    o["w3"] = o["s1"] + up_s
+    o["s3"] = o["w3"] + up_w
+    o["w2"] = o["s3"] + up_s
+    o["s2"] = o["w2"] + dn_w
+    o["total"] = o["s2"] + dn_s
+    return o
+
+
+def _expert(page: np.ndarray, fmt: str, hidden: int, inter: int) -> _Expert:
+    o = page_offsets(fmt, hidden, inter)
+    assert page.dtype == np.uint8 and page.size >= o["total"] and page.flags["C_CONTIGUOUS"]
+    base = page.ctypes.data
+    return _Expert(*[base + o[k] for k in ("w1", "s1", "w3", "s3", "w2", "s2")])
+
+
+def expert_down(x, page, fmt="mxfp4", hidden=HIDDEN, inter=INTER) -> np.ndarray:
+    x = _f32(x)
+    e = _expert(page, fmt, hidden, inter)
+    out = np.empty(hidden, dtype=np.float32)
+    fn = lib().s14o_mxfp4_expert_down if fmt == "mxfp4" else lib().s14o_fp8_expert_down
+    fn(hidden, inter, _p(x), C.byref(e), _p(out))
+    return out
+
+
+def expert_chain(x, page, route_w: float, hidden=HIDDEN, inter=INTER) -> np.ndarray:
+    x = _f32(x)
+    e = _expert(page, "mxfp4", hidden, inter)
+    y = np.empty(hidden, dtype=np.float32)
+    lib().s14o_expert_chain(hidden, inter, _p(x), C.byref(e), float(route_w), _p(y))
+    return y
+
+
+def moe_layer(x, routed_pages, weights, shared_page, shared_fmt="mxfp4", hidden=HIDDEN, inter=INTER) -> np.ndarray:
+    x = _f32(x)
+    k = len(routed_pages)
+    arr = (_Expert * max(1, k))(*[_expert(p, "mxfp4", hidden, inter) for p in routed_pages])
+    w = _f32(weights)
+    y = np.empty(hidden, dtype=np.float32)
+    sh = _expert(shared_page, shared_fmt, hidden, inter)
+    sh_mx = C.byref(sh) if shared_fmt == "mxfp4" else None
+    sh_f8 = C.byref(sh) if shared_fmt != "mxfp4" else None
+    lib().s14o_moe_layer(hidden, inter, _p(x), k, C.cast(arr, P), _p(w), sh_mx, sh_f8, _p(y))
+    return y
+
+
+def router_logits(wr, x) -> np.ndarray:
+    wr, x = _f32(wr), _f32(x)
+    z = np.empty(wr.shape[0], dtype=np.float32)
+    lib().s14o_router_logits(wr.shape[0], wr.shape[1], _p(wr), _p(x), _p(z))
+    return z
+
+
+def route(wr, bias, x, score_fn=SCORE_SIGMOID, topk=6, route_scale=1.0):
+    wr, bias, x = _f32(wr), _f32(bias), _f32(x)
+    n = wr.shape[0]
+    scores = np.empty(n, dtype=np.float32)
+    ids = np.empty(topk, dtype=np.uint16)
+    w = np.empty(topk, dtype=np.float32)
+    lib().s14o_route(n, wr.shape[1], _p(wr), _p(bias), _p(x), score_fn, topk, float(route_scale), _p(scores), _p(ids), _p(w))
+    return scores, ids, w
+
+
+def error_stats(actual, expected) -> dict:
+    a, e = _f32(actual).reshape(-1), _f32(expected).reshape(-1)
+    assert a.size == e.size and a.size > 0
+    st = ErrorStats()
+    lib().s14o_error_stats_compute(a.size, _p(a), _p(e), C.byref(st))
+    return st.as_dict()
+
+
+def requant_e4m3(x, group: int = 32):
+    x = _f32(np.atleast_2d(x))
+    rows, k = x.shape
+    q = np.empty((rows, k), dtype=np.uint8)
+    s = np.empty((rows, k // group), dtype=np.uint8)
+    lib().s14o_requant_e4m3(rows, k, group, _p(x), _p(q), _p(s))
+    return q, s
+
+
+def set_num_threads(n: int) -> None:
+    lib().s14o_set_num_threads(n)
+
+
+def num_threads() -> int:
+    return int(lib().s14o_num_threads())

@@ -1,0 +1,392 @@
+"""GPU parity: the HIP path through its C ABI against the CPU oracle on the
+same seeded inputs.  EXACT mode must be bit-identical (integer/decode work
+and the oracle-order f32 reductions); FAST mode is checked against the
+north-star tolerance where it applies (FP8: max-abs 2e-5, RMSE 2e-6) and
+otherwise against the reference's own Vulkan gates
+(s14_vulkan_numeric.rs:1039 layer 1e-3/1.5e-4, :1347 chain 2e-4/2.5e-5)."""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+from colormlm_amd import _native as N  # noqa: E402
+from colormlm_amd import s14, synth  # noqa: E402
+
+HIDDEN, INTER = N.HIDDEN, N.INTER
+
+
+def say(msg: str) -> None:
+    print(f"[gpu-test] {msg}", file=sys.stderr, flush=True)
+
+
+def dev(a: np.ndarray) -> "torch.Tensor":
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda()
+    return torch.from_numpy(a).cuda()
+
+
+def host(t) -> np.ndarray:
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def bits(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def assert_bit_exact(got, want, what):
+    g, w = bits(got), bits(want)
+    bad = np.flatnonzero(g != w)
+    assert bad.size == 0, f"{what}: {bad.size} of {g.size} differ; first {bad[:5]} got {np.asarray(got).reshape(-1)[bad[:3]]} want {np.asarray(want).reshape(-1)[bad[:3]]}"
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    say("context on cuda:0")
+    c = s14.Context(0)
+    yield c
+    torch.cuda.synchronize()
+    c.destroy()
+
+
+@pytest.fixture(scope="module")
+def pipes(ctx):
+    return s14.S14NumericPipelines(ctx)
+
+
+def mx_parts(page: np.ndarray):
+    o = synth.page_offsets("mxfp4")
+    return {
+        "w1": page[o["w1"]:o["s1"]].reshape(INTER, HIDDEN // 2),
+        "s1": page[o["s1"]:o["w3"]].reshape(INTER, HIDDEN // 32),
+        "w3": page[o["w3"]:o["s3"]].reshape(INTER, HIDDEN // 2),
+        "s3": page[o["s3"]:o["w2"]].reshape(INTER, HIDDEN // 32),
+        "w2": page[o["w2"]:o["s2"]].reshape(HIDDEN, INTER // 2),
+        "s2": page[o["s2"]:o["total"]].reshape(HIDDEN, INTER // 32),
+    }
+
+
+# --------------------------------------------------------------------------
+# synthetic page fill and decoders
+# --------------------------------------------------------------------------
+
+
+def test_device_fill_matches_host_generator(ctx):
+    say("fill page seed=3 layer=1 expert=5")
+    page = torch.empty(N.EXPERT_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+    s14.fill_mxfp4_page(ctx, page, 3, 1, 5)
+    assert np.array_equal(host(page), synth.gen_mxfp4_page(3, 1, 5))
+
+
+def test_dequant_mxfp4_bit_exact_every_byte_and_scale(pipes, oracle):
+    say("dequant mxfp4 all codes x all scales")
+    n, k = 256, 128
+    packed = ((np.arange(n)[:, None] * 7 + np.arange(k // 2)[None, :]) % 256).astype(np.uint8)
+    scale = (np.arange(n * 4).reshape(n, 4) % 255).astype(np.uint8)  # every code 0..254
+    out = torch.empty((n, k), dtype=torch.float32, device="cuda")
+    pipes.dequant_mxfp4(s14.S14MatvecShape(n, k), dev(packed), dev(scale), out)
+    assert_bit_exact(host(out), oracle.dequant_mxfp4(packed, scale), "dequant mxfp4")
+
+
+def test_dequant_fp8_bit_exact_every_code(pipes, oracle):
+    say("dequant fp8 all codes")
+    n, k = 256, 256
+    w = ((np.arange(n)[:, None] + np.arange(k)[None, :]) % 256).astype(np.uint8)
+    w[(w & 0x7F) == 0x7F] = 0x7E
+    s = np.array([[0, 127], [130, 254]], dtype=np.uint8)
+    out = torch.empty((n, k), dtype=torch.float32, device="cuda")
+    pipes.dequant_fp8(s14.S14MatvecShape(n, k), dev(w), dev(s), out)
+    assert_bit_exact(host(out), oracle.dequant_fp8_ue8m0(w, s), "dequant fp8")
+
+
+# --------------------------------------------------------------------------
+# standalone dispatches (bind / cmd)
+# --------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("n,k", [(2048, 4096), (4096, 2048), (64, 128), (100, 384), (7, 8192)])
+def test_mxfp4_matvec_exact_bit_exact(pipes, oracle, n, k):
+    say(f"mxfp4 exact n={n} k={k}")
+    packed = synth.gen_bytes(11, 1 + n, n * k // 2).reshape(n, k // 2)
+    scale = synth.gen_ue8m0(11, 2 + n, n * k // 32).reshape(n, k // 32)
+    x = synth.gen_normal(11, 3 + n, k)
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    shape = s14.S14MatvecShape.new(n, k)
+    d = pipes.bind_mxfp4(shape, dev(x), dev(packed), dev(scale), y, mode=s14.EXACT)
+    pipes.cmd_mxfp4_matvec(d)
+    assert_bit_exact(host(y), oracle.mxfp4_matvec(x, packed, scale), f"mxfp4 exact {n}x{k}")
+
+
+def test_mxfp4_matvec_exact_slow_decode_paths(pipes, oracle):
+    """Scale codes outside the scaled-decode window (tiny and huge), tiny and
+    subnormal activations, zeros and infinities in x."""
+    say("mxfp4 exact edge codes")
+    n, k = 64, 256
+    packed = synth.gen_bytes(12, 1, n * k // 2).reshape(n, k // 2)
+    scale = synth.gen_ue8m0(12, 2, n * k // 32, -127, 127).reshape(n, k // 32)
+    scale[0, :] = 0
+    scale[1, :] = 254
+    x = synth.gen_normal(12, 3, k)
+    x[5] = 0.0
+    x[6] = -0.0
+    x[7] = np.float32(1e-40)  # subnormal
+    x[8] = np.float32(3e-38)
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    d = pipes.bind_mxfp4(s14.S14MatvecShape(n, k), dev(x), dev(packed), dev(scale), y, mode=s14.EXACT)
+    pipes.cmd_mxfp4_matvec(d)
+    assert_bit_exact(host(y), oracle.mxfp4_matvec(x, packed, scale), "mxfp4 exact edge")
+
+
+@pytest.mark.parametrize("n,k", [(2048, 4096), (4096, 2048), (100, 384)])
+def test_mxfp4_matvec_fast_close(pipes, oracle, n, k):
+    say(f"mxfp4 fast n={n} k={k}")
+    packed = synth.gen_bytes(13, 1, n * k // 2).reshape(n, k // 2)
+    scale = synth.gen_ue8m0(13, 2, n * k // 32).reshape(n, k // 32)
+    x = synth.gen_normal(13, 3, k)
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    d = pipes.bind_mxfp4(s14.S14MatvecShape(n, k), dev(x), dev(packed), dev(scale), y, mode=s14.FAST)
+    pipes.cmd_mxfp4_matvec(d)
+    got, want = host(y), oracle.mxfp4_matvec(x, packed, scale)
+    st = oracle.error_stats(got, want)
+    say(f"  fast vs oracle {st}")
+    # order-changed f32 sums over k terms: bounded by k * eps * sum|terms|
+    assert st["max_abs"] < 2e-4 and st["rmse"] < 5e-5
+
+
+def test_fp8_wq_a_config(pipes, oracle):
+    """Config 1: W e4m3 [1024, 4096], f32 128x128 tile scales, bf16 x."""
+    say("fp8 wq_a config: exact and fast")
+    cfg = synth.config1(seed=0)
+    want = oracle.fp8_matvec_f32scale_bf16x(cfg["x_bf16"], cfg["w"], cfg["scale"])
+    x = dev(cfg["x_bf16"]).view(torch.bfloat16)
+    shape = s14.S14MatvecShape.new(1024, 4096).validate_fp8()
+    for mode in (s14.EXACT, s14.FAST):
+        y = torch.empty(1024, dtype=torch.float32, device="cuda")
+        d = pipes.bind_fp8(shape, x, dev(cfg["w"]), dev(cfg["scale"]), y, mode=mode)
+        pipes.cmd_fp8_matvec(d)
+        got = host(y)
+        if mode == s14.EXACT:
+            assert_bit_exact(got, want, "fp8 exact")
+        else:
+            st = oracle.error_stats(got, want)
+            say(f"  fp8 fast vs oracle {st}")
+            assert st["max_abs"] <= 2e-5 and st["rmse"] <= 2e-6
+
+
+@pytest.mark.parametrize("n,k", [(2048, 4096), (4096, 2048), (129, 130)])
+def test_fp8_ue8m0_reference_variant_exact(pipes, oracle, n, k):
+    say(f"fp8 ue8m0 f32-x exact n={n} k={k}")
+    w = synth.e4m3fn_encode(synth.gen_normal(14, 1, n * k)).reshape(n, k)
+    s = synth.gen_ue8m0(14, 2, (-(-n // 128)) * (-(-k // 128)), -7, -5).reshape(-(-n // 128), -(-k // 128))
+    x = synth.gen_normal(14, 3, k)
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    d = pipes.bind_fp8(s14.S14MatvecShape(n, k), dev(x), dev(w), dev(s), y, mode=s14.EXACT)
+    pipes.cmd_fp8_matvec(d)
+    assert_bit_exact(host(y), oracle.fp8_matvec_ue8m0(x, w, s), "fp8 ue8m0 exact")
+
+
+def test_swiglu_route_mix_accumulate_bit_exact(pipes, oracle):
+    say("swiglu / route_mix / moe_accumulate")
+    n = 1 << 20
+    g = synth.gen_normal(15, 1, n, 0.0, 8.0)
+    u = synth.gen_normal(15, 2, n, 0.0, 8.0)
+    g[:6] = [0.0, -0.0, 10.0, 1e30, -200.0, np.nan]
+    u[6:8] = [np.nan, 1e20]
+    gt, ut, yt = dev(g), dev(u), torch.empty(n, dtype=torch.float32, device="cuda")
+    pipes.cmd_swiglu_limit(pipes.bind_swiglu_limit(n, gt, ut, yt))
+    assert_bit_exact(host(yt), oracle.swiglu_limit(g, u), "swiglu")
+    e = synth.gen_normal(15, 3, 4096)
+    acc0 = synth.gen_normal(15, 4, 4096)
+    et, rt = dev(e), torch.empty(4096, dtype=torch.float32, device="cuda")
+    pipes.cmd_route_mix(pipes.bind_route_mix(4096, 0.17, et, rt))
+    assert_bit_exact(host(rt), (np.float32(0.17) * e).astype(np.float32), "route_mix")
+    at = dev(acc0)
+    pipes.cmd_moe_accumulate(pipes.bind_moe_accumulate(4096, 0.3, et, at))
+    assert_bit_exact(host(at), (acc0 + (np.float32(0.3) * e).astype(np.float32)).astype(np.float32), "accumulate")
+
+
+# --------------------------------------------------------------------------
+# fused expert paths
+# --------------------------------------------------------------------------
+
+
+def test_expert_chain_config0(ctx, oracle):
+    say("config 0 expert chain exact + fast")
+    cfg = synth.config0(seed=0)
+    want = oracle.expert_chain(cfg["x"], cfg["page"], float(cfg["route_w"]))
+    page, x = dev(cfg["page"]), dev(cfg["x"])
+    y = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    s14.expert_chain(ctx, page, x, float(cfg["route_w"]), y, mode=s14.EXACT)
+    assert_bit_exact(host(y), want, "chain exact")
+    s14.expert_chain(ctx, page, x, float(cfg["route_w"]), y, mode=s14.FAST)
+    st = oracle.error_stats(host(y), want)
+    say(f"  chain fast vs oracle {st}")
+    assert st["max_abs"] <= 2e-4 and st["rmse"] <= 2.5e-5
+
+
+@pytest.fixture(scope="module")
+def bank(ctx):
+    """256 routed MXFP4 pages + 1 MXFP4 shared page of layer 0, on device."""
+    say("filling 257-page bank (3.4 GB)")
+    pages = torch.empty((257, N.EXPERT_PAGE_BYTES), dtype=torch.uint8, device="cuda")
+    for e in range(256):
+        s14.fill_mxfp4_page(ctx, pages[e], 0, 0, e)
+    s14.fill_mxfp4_page(ctx, pages[256], 0, 0, synth.SHARED_EXPERT)
+    table = torch.tensor([pages[e].data_ptr() for e in range(256)], dtype=torch.int64, device="cuda")
+    wr, bias = synth.router(seed=0, layer=0)
+    torch.cuda.synchronize()
+    return {"pages": pages, "table": table, "wr": wr, "bias": bias, "wr_d": dev(wr), "bias_d": dev(bias)}
+
+
+def page_host(bank, e) -> np.ndarray:
+    return host(bank["pages"][e])
+
+
+def test_moe_layer_route_given(ctx, oracle, bank):
+    say("moe layer, route given, mxfp4 shared, exact + fast")
+    ids = [126, 12, 205, 149, 227, 174]
+    w = np.array([0.3, 0.2, 0.15, 0.15, 0.1, 0.1], dtype=np.float32)
+    x = synth.token(seed=1)
+    want = oracle.moe_layer(x, [page_host(bank, e) for e in ids], w, page_host(bank, 256))
+    y = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    routed = [bank["pages"][e] for e in ids]
+    s14.moe_layer(ctx, routed, w.tolist(), bank["pages"][256], dev(x), y, mode=s14.EXACT)
+    assert_bit_exact(host(y), want, "layer exact")
+    s14.moe_layer(ctx, routed, w.tolist(), bank["pages"][256], dev(x), y, mode=s14.FAST)
+    st = oracle.error_stats(host(y), want)
+    say(f"  layer fast vs oracle {st}")
+    assert st["max_abs"] <= 1e-3 and st["rmse"] <= 1.5e-4
+
+
+def test_moe_layer_fp8_shared_reference_variant(ctx, oracle, bank):
+    say("moe layer with the reference's FP8 shared page, exact")
+    sh = synth.gen_fp8_page(0, 0)
+    ids = [1, 2, 3, 4, 5, 6]
+    w = np.full(6, 0.25, dtype=np.float32)  # reference route_scale 1.5
+    x = synth.token(seed=2)
+    want = oracle.moe_layer(x, [page_host(bank, e) for e in ids], w, sh, shared_fmt="fp8")
+    y = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    s14.moe_layer(ctx, [bank["pages"][e] for e in ids], w.tolist(), dev(sh), dev(x), y,
+                  shared_format=N.S14_PAGE_FP8, mode=s14.EXACT)
+    assert_bit_exact(host(y), want, "layer fp8-shared exact")
+    s14.moe_layer(ctx, [bank["pages"][e] for e in ids], w.tolist(), dev(sh), dev(x), y,
+                  shared_format=N.S14_PAGE_FP8, mode=s14.FAST)
+    st = oracle.error_stats(host(y), want)
+    say(f"  layer fp8-shared fast vs oracle {st}")
+    assert st["max_abs"] <= 1e-3 and st["rmse"] <= 1.5e-4
+
+
+def test_router_matches_oracle(ctx, oracle, bank):
+    say("router sigmoid + sqrt-softplus")
+    xs = synth.block_tokens(seed=3, tokens=8)
+    router = s14.Router(bank["wr_d"], bank["bias_d"])
+    scores = torch.empty((8, 256), dtype=torch.float32, device="cuda")
+    ids = torch.empty((8, 6), dtype=torch.int16, device="cuda")
+    wts = torch.empty((8, 6), dtype=torch.float32, device="cuda")
+    s14.route(ctx, router, 8, dev(xs), scores, ids, wts)
+    sc_h, ids_h, w_h = host(scores), host(ids).astype(np.uint16), host(wts)
+    for t in range(8):
+        s_o, i_o, w_o = oracle.route(bank["wr"], bank["bias"], xs[t])
+        assert_bit_exact(sc_h[t], s_o, f"scores t={t}")
+        assert ids_h[t].tolist() == i_o.tolist()
+        assert_bit_exact(w_h[t], w_o, f"weights t={t}")
+    ref = s14.Router(bank["wr_d"], bank["bias_d"], score_fn=N.S14_SCORE_SQRT_SOFTPLUS, route_scale=1.5)
+    s14.route(ctx, ref, 1, dev(xs[0]), scores, ids, wts)
+    s_o, i_o, w_o = oracle.route(bank["wr"], bank["bias"], xs[0], score_fn=oracle.SCORE_SQRT_SOFTPLUS, route_scale=1.5)
+    np.testing.assert_allclose(host(scores)[0], s_o, rtol=2e-7, atol=0)
+    assert host(ids).astype(np.uint16)[0].tolist() == i_o.tolist()
+    np.testing.assert_allclose(host(wts)[0], w_o, rtol=1e-6)
+
+
+def test_moe_layer_route_config2(ctx, oracle, bank):
+    say("config 2 layer with device router, exact + fast")
+    x = synth.token(seed=0)
+    _, i_o, w_o = oracle.route(bank["wr"], bank["bias"], x)
+    want = oracle.moe_layer(x, [page_host(bank, int(e)) for e in i_o], w_o, page_host(bank, 256))
+    router = s14.Router(bank["wr_d"], bank["bias_d"])
+    y = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    ids = torch.empty(6, dtype=torch.int16, device="cuda")
+    wts = torch.empty(6, dtype=torch.float32, device="cuda")
+    s14.moe_layer_route(ctx, router, bank["table"], bank["pages"][256], dev(x), y, ids, wts, mode=s14.EXACT)
+    assert host(ids).astype(np.uint16).tolist() == i_o.tolist()
+    assert_bit_exact(host(wts), w_o, "route weights")
+    assert_bit_exact(host(y), want, "config2 exact")
+    s14.moe_layer_route(ctx, router, bank["table"], bank["pages"][256], dev(x), y, ids, wts, mode=s14.FAST)
+    st = oracle.error_stats(host(y), want)
+    say(f"  config2 fast vs oracle {st}")
+    assert st["max_abs"] <= 1e-3 and st["rmse"] <= 1.5e-4
+
+
+@pytest.mark.parametrize("tokens", [8, 3])
+def test_moe_block_route_config3(ctx, oracle, bank, tokens):
+    say(f"config 3 verify block T={tokens}, exact + fast")
+    xs = synth.block_tokens(seed=4, tokens=tokens)
+    router = s14.Router(bank["wr_d"], bank["bias_d"])
+    y = torch.empty((tokens, HIDDEN), dtype=torch.float32, device="cuda")
+    ids = torch.empty((tokens, 6), dtype=torch.int16, device="cuda")
+    s14.moe_block_route(ctx, tokens, router, bank["table"], bank["pages"][256], dev(xs), y, ids, mode=s14.EXACT)
+    got = host(y)
+    distinct = s14.last_block_distinct(ctx)
+    ids_h = host(ids).astype(np.uint16)
+    cache = {}
+    shared = page_host(bank, 256)
+    for t in range(tokens):
+        _, i_o, w_o = oracle.route(bank["wr"], bank["bias"], xs[t])
+        assert ids_h[t].tolist() == i_o.tolist()
+        for e in i_o:
+            if int(e) not in cache:
+                cache[int(e)] = page_host(bank, int(e))
+        want = oracle.moe_layer(xs[t], [cache[int(e)] for e in i_o], w_o, shared)
+        assert_bit_exact(got[t], want, f"block token {t}")
+    assert distinct == len(cache)
+    say(f"  distinct routed pages D={distinct}")
+    s14.moe_block_route(ctx, tokens, router, bank["table"], bank["pages"][256], dev(xs), y, mode=s14.FAST)
+    fast = host(y)
+    for t in range(tokens):
+        assert np.max(np.abs(fast[t] - got[t])) <= 1e-3
+
+
+def test_pool_upload_publish_compute_release(ctx, oracle, bank):
+    """The page contract end to end on the device: reserve, upload on the copy
+    stream, wait the transfer fence, publish, compute from slot addresses,
+    release after the compute fence."""
+    say("pool upload -> fence -> publish -> layer -> release")
+    from colormlm_amd.pool import Fence, GraphProfile, RouteDecision, RouterKind, S14MoePages, VramPool
+
+    routed = VramPool(7, N.EXPERT_PAGE_BYTES, ctx)
+    shared = VramPool(1, N.EXPERT_PAGE_BYTES, ctx)
+    pages = S14MoePages(routed, shared, GraphProfile.S14_TOP6, shared_format=N.S14_PAGE_MXFP4, weight_sum=1.0)
+    ids = [126, 12, 205, 149, 227, 174]
+    w = [1 / 6] * 6
+    batch = pages.begin_after_official_route(RouteDecision(42, RouterKind.SCORE, ids, w))
+    fences = []
+    hosts = {}
+    for i, p in enumerate(batch.pages()):
+        e = ids[i] if i < 6 else 256
+        hosts[e] = page_host(bank, e)
+        fences.append((routed if i < 6 else shared).upload(ctx, p, hosts[e].tobytes()))
+    for f in fences:
+        f.wait()
+        assert f.is_complete()
+    lease = pages.publish_after_transfer_fence(batch)
+    slots = [b.slot for b in lease.routed_bindings()]
+    ptrs = [routed.slot_ptr(s) for s in slots]
+    x = synth.token(seed=5)
+    y = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    s14.moe_layer(ctx, ptrs, np.array(w, np.float32).tolist(), shared.slot_ptr(lease.shared_binding().slot), dev(x), y,
+                  mode=s14.EXACT, stream=ctx.compute_stream)
+    done = Fence.record(ctx, ctx.compute_stream)
+    done.wait()
+    pages.release_after_compute_fence(lease)
+    want = oracle.moe_layer(x, [hosts[e] for e in ids], np.array(w, np.float32), hosts[256])
+    assert_bit_exact(host(y), want, "layer from pool slots")

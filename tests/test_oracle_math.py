@@ -1,0 +1,280 @@
+"""Pin the oracle's arithmetic where no reference vector exists: float64
+brute force on small shapes, closed-form constructions whose sequential-f32
+value is known (so a changed summation order fails), IEEE identities, and
+library routines (numpy/torch) for the parts that reduce to them."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from colormlm_amd import synth
+
+E2M1 = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0.0, -.5, -1, -1.5, -2, -3, -4, -6], dtype=np.float64)
+
+
+def _codes(packed):
+    c = np.empty((packed.shape[0], packed.shape[1] * 2), dtype=np.int64)
+    c[:, 0::2] = packed & 0x0F
+    c[:, 1::2] = packed >> 4
+    return c
+
+
+def _pack(codes):
+    codes = np.asarray(codes, dtype=np.uint8)
+    return (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+
+
+def _f64_mxfp4(x, packed, scale):
+    w = E2M1[_codes(packed)] * np.exp2(np.repeat(scale.astype(np.float64) - 127, 32, axis=1))
+    return w @ x.astype(np.float64)
+
+
+@pytest.mark.parametrize("n,k", [(1, 128), (8, 128), (5, 256), (3, 384)])
+def test_mxfp4_matvec_vs_f64(oracle, n, k):
+    rng = np.random.default_rng(n * 1000 + k)
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scale = rng.integers(117, 124, (n, k // 32), dtype=np.uint8)
+    x = rng.normal(0, 1, k).astype(np.float32)
+    y = oracle.mxfp4_matvec(x, packed, scale)
+    ref = _f64_mxfp4(x, packed, scale)
+    # sequential f32 over k terms: |err| <= k * eps * sum|terms|
+    bound = k * 2.0**-23 * (np.abs(E2M1[_codes(packed)]) * np.exp2(np.repeat(scale - 127.0, 32, 1))) @ np.abs(x)
+    assert np.all(np.abs(y - ref) <= bound + 1e-30)
+
+
+def test_mxfp4_single_code_is_one_scaled_x(oracle):
+    k = 128
+    x = np.linspace(-3, 3, k).astype(np.float32)
+    for pos, code, sc in [(0, 2, 127), (77, 13, 120), (127, 7, 130), (64, 9, 125)]:
+        codes = np.zeros((1, k), dtype=np.uint8)
+        codes[0, pos] = code
+        scale = np.full((1, k // 32), 127, dtype=np.uint8)
+        scale[0, pos // 32] = sc
+        y = oracle.mxfp4_matvec(x, _pack(codes), scale)
+        expect = np.float32(np.float32(x[pos] * np.float32(E2M1[code])) * np.float32(2.0 ** (sc - 127)))
+        assert y[0] == expect
+    assert oracle.mxfp4_matvec(x, np.zeros((2, k // 2), np.uint8), np.full((2, 4), 127, np.uint8)).tolist() == [0.0, 0.0]
+
+
+def test_mxfp4_sequential_order_closed_form(oracle):
+    """Terms 2^24, then 63 ones (each absorbed: 2^24+1 rounds to even), then
+    -2^24, then 63 ones: strictly sequential f32 gives exactly 63 where the
+    exact sum is 126."""
+    k = 128
+    x = np.ones(k, dtype=np.float32)
+    x[0] = 2.0**24
+    x[64] = -(2.0**24)
+    codes = np.full((1, k), 2, dtype=np.uint8)  # e2m1 1.0
+    y = oracle.mxfp4_matvec(x, _pack(codes), np.full((1, 4), 127, np.uint8))
+    assert y[0] == 63.0
+
+
+def test_mxfp4_low_nibble_before_high_nibble(oracle):
+    """Pair 1 holds (+1 at even k, -2^24 at odd k) after a running 2^24:
+    low-then-high gives (2^24 + 1) - 2^24 = 0, the other order would give 1."""
+    k = 128
+    x = np.zeros(k, dtype=np.float32)
+    x[0], x[2], x[3] = 2.0**24, 1.0, -(2.0**24)
+    codes = np.zeros((1, k), dtype=np.uint8)
+    codes[0, [0, 2, 3]] = 2
+    y = oracle.mxfp4_matvec(x, _pack(codes), np.full((1, 4), 127, np.uint8))
+    assert y[0] == 0.0
+
+
+def test_mxfp4_sign_symmetry(oracle):
+    rng = np.random.default_rng(11)
+    packed = rng.integers(0, 256, (4, 128), dtype=np.uint8)
+    scale = rng.integers(110, 130, (4, 8), dtype=np.uint8)
+    x = rng.normal(0, 1, 256).astype(np.float32)
+    y = oracle.mxfp4_matvec(x, packed, scale)
+    flipped = packed ^ 0x88  # flip both sign bits: every weight negated
+    assert np.array_equal(oracle.mxfp4_matvec(x, flipped, scale), -y)
+    assert np.array_equal(oracle.mxfp4_matvec(-x, packed, scale), -y)
+
+
+def test_mxfp4_subnormal_products_round_twice(oracle):
+    """(x * e2m1) * scale rounds twice; with a tiny scale the second rounding
+    lands in the subnormal range.  numpy's IEEE float32 gives the expected."""
+    k = 128
+    x = np.full(k, np.float32(1.0000001), dtype=np.float32)
+    codes = np.zeros((1, k), dtype=np.uint8)
+    codes[0, 0] = 3  # 1.5
+    scale = np.full((1, 4), 1, dtype=np.uint8)  # 2^-126
+    y = oracle.mxfp4_matvec(x, _pack(codes), scale)
+    with np.errstate(under="ignore"):
+        expect = np.float32(np.float32(x[0] * np.float32(1.5)) * np.float32(2.0**-126))
+    assert y[0] == expect
+
+
+def test_fp8_matvec_vs_f64_and_order(oracle):
+    rng = np.random.default_rng(21)
+    n, k = 130, 260
+    w = rng.integers(0, 255, (n, k), dtype=np.uint8)
+    w[(w & 0x7F) == 0x7F] = 0x7E
+    s = rng.integers(118, 126, (-(-n // 128), -(-k // 128)), dtype=np.uint8)
+    x = rng.normal(0, 1, k).astype(np.float32)
+    y = oracle.fp8_matvec_ue8m0(x, w, s)
+    dec = torch.from_numpy(w).view(torch.float8_e4m3fn).double().numpy()
+    sc = np.exp2(s.astype(np.float64) - 127).repeat(128, 0).repeat(128, 1)[:n, :k]
+    ref = (dec * sc) @ x.astype(np.float64)
+    bound = k * 2.0**-23 * (np.abs(dec * sc) @ np.abs(x.astype(np.float64)))
+    assert np.all(np.abs(y - ref) <= bound)
+    # closed form: 2^24 then ones absorbed, k ascending (e4m3 0x38 = 1.0)
+    wk = np.full((1, 128), 0x38, dtype=np.uint8)
+    xk = np.ones(128, dtype=np.float32)
+    xk[0] = 2.0**24
+    xk[100] = -(2.0**24)
+    assert oracle.fp8_matvec_ue8m0(xk, wk, np.full((1, 1), 127, np.uint8))[0] == 27.0
+
+
+def test_fp8_f32scale_bf16x(oracle):
+    rng = np.random.default_rng(22)
+    n, k = 256, 512
+    cfg = synth.config1(seed=3, n=n, k=k)
+    y = oracle.fp8_matvec_f32scale_bf16x(cfg["x_bf16"], cfg["w"], cfg["scale"])
+    dec = torch.from_numpy(cfg["w"]).view(torch.float8_e4m3fn).double().numpy()
+    sc = cfg["scale"].astype(np.float64).repeat(128, 0).repeat(128, 1)[:n, :k]
+    xf = synth.bf16_decode(cfg["x_bf16"]).astype(np.float64)
+    ref = (dec * sc) @ xf
+    bound = k * 2.0**-22 * (np.abs(dec * sc) @ np.abs(xf))
+    assert np.all(np.abs(y - ref) <= bound)
+    del rng
+
+
+def test_swiglu_limit_semantics(oracle):
+    g = np.array([0.0, -0.0, 1.0, -3.0, 10.0, 25.0, 1e30, -200.0, np.nan, 2.0], dtype=np.float32)
+    u = np.array([1.0, 1.0, 2.0, 5.0, -1.0, 3.0, 1.0, 1.0, 1.0, np.nan], dtype=np.float32)
+    h = oracle.swiglu_limit(g, u)
+    assert h[0] == 0.0 and h[1] == 0.0
+    assert h[5] == oracle.swiglu_limit(np.float32([10.0]), np.float32([3.0]))[0]  # gate clamped at 10
+    assert h[6] == oracle.swiglu_limit(np.float32([10.0]), np.float32([1.0]))[0]
+    assert h[7] == 0.0 or abs(h[7]) < 1e-80  # exp overflow: g / inf
+    assert h[8] == oracle.swiglu_limit(np.float32([10.0]), np.float32([1.0]))[0]  # Rust min(NaN, 10) = 10
+    assert np.isnan(h[9])  # clamp passes NaN
+    rng = np.random.default_rng(2)
+    g = rng.normal(0, 5, 20000).astype(np.float32)
+    u = rng.normal(0, 5, 20000).astype(np.float32)
+    h = oracle.swiglu_limit(g, u)
+    gd = np.minimum(g.astype(np.float64), 10.0)
+    ud = np.clip(u.astype(np.float64), -10.0, 10.0)
+    ref = gd / (1.0 + np.exp(-gd)) * ud
+    assert np.all(np.abs(h - ref) <= 4 * np.spacing(np.abs(ref).astype(np.float32)) + 1e-30)
+    # up clamp is exact
+    assert oracle.swiglu_limit(np.float32([1.0]), np.float32([50.0]))[0] == \
+        oracle.swiglu_limit(np.float32([1.0]), np.float32([10.0]))[0]
+
+
+def test_router_logit_order_closed_form(oracle):
+    """Lane 0 holds 2^24, lane 1 holds 1 + 1 = 2; the butterfly adds them
+    once: 2^24 + 2 (representable).  Strictly sequential k would absorb
+    each 1 and give 2^24."""
+    wr = np.zeros((1, 256), dtype=np.float32)
+    wr[0, 0], wr[0, 4], wr[0, 5] = 2.0**24, 1.0, 1.0
+    x = np.ones(256, dtype=np.float32)
+    assert oracle.router_logits(wr, x)[0] == 2.0**24 + 2
+
+
+def test_router_vs_f64_topk_and_ties(oracle):
+    wr, bias = synth.router(seed=7)
+    x = synth.token(seed=7)
+    z = oracle.router_logits(wr, x)
+    zd = wr.astype(np.float64) @ x.astype(np.float64)
+    assert np.all(np.abs(z - zd) <= 4096 * 2.0**-23 * (np.abs(wr) @ np.abs(x)))
+    scores, ids, w = oracle.route(wr, bias, x)
+    sd = 1.0 / (1.0 + np.exp(-z.astype(np.float64)))
+    np.testing.assert_allclose(scores, sd, rtol=3e-7, atol=0)
+    biased = (scores + bias).astype(np.float32)
+    order = np.argsort(-biased.astype(np.float64), kind="stable")[:6]
+    assert ids.tolist() == order.tolist()
+    total = np.float32(0)
+    for i in ids:
+        total = np.float32(total + scores[i])
+    assert np.array_equal(w, (scores[ids] / total).astype(np.float32))
+    # reference scaling: (w / sum) * 1.5, and sqrt(softplus) scores
+    s2, ids2, w2 = oracle.route(wr, bias, x, score_fn=oracle.SCORE_SQRT_SOFTPLUS, route_scale=1.5)
+    np.testing.assert_allclose(s2, np.sqrt(np.log1p(np.exp(z.astype(np.float64)))), rtol=3e-7)
+    assert abs(float(np.sum(w2, dtype=np.float64)) - 1.5) < 1e-5
+    # ties go to the lower index
+    wr_t = wr.copy()
+    wr_t[9] = wr_t[5]
+    b_t = bias.copy()
+    b_t[9] = b_t[5] = 1.0  # both certainly selected, equal biased score
+    _, ids_t, _ = oracle.route(wr_t, b_t, x)
+    assert ids_t[0] == 5 and ids_t[1] == 9
+
+
+def test_chain_and_layer_composition(oracle):
+    hidden, inter = 256, 128
+    rng = np.random.default_rng(4)
+    pages = [synth.gen_mxfp4_page(5, 1, e, hidden=hidden, inter=inter) for e in range(4)]
+    shared = synth.gen_mxfp4_page(5, 1, synth.SHARED_EXPERT, hidden=hidden, inter=inter)
+    x = rng.normal(0, 1, hidden).astype(np.float32)
+    downs = [oracle.expert_down(x, p, hidden=hidden, inter=inter) for p in pages]
+    # chain = route_w * down
+    y = oracle.expert_chain(x, pages[0], 0.17, hidden=hidden, inter=inter)
+    assert np.array_equal(y, (np.float32(0.17) * downs[0]).astype(np.float32))
+    # expert down = w2 . swiglu(w1 x, w3 x) through the pinned matvec/swiglu
+    o = synth.page_offsets("mxfp4", hidden, inter)
+    g = oracle.mxfp4_matvec(x, pages[1][o["w1"]:o["s1"]].reshape(inter, hidden // 2), pages[1][o["s1"]:o["w3"]].reshape(inter, hidden // 32))
+    u = oracle.mxfp4_matvec(x, pages[1][o["w3"]:o["s3"]].reshape(inter, hidden // 2), pages[1][o["s3"]:o["w2"]].reshape(inter, hidden // 32))
+    h = oracle.swiglu_limit(g, u)
+    d = oracle.mxfp4_matvec(h, pages[1][o["w2"]:o["s2"]].reshape(hidden, inter // 2), pages[1][o["s2"]:o["total"]].reshape(hidden, inter // 32))
+    assert np.array_equal(d, downs[1])
+    # layer: acc = 0; acc += w_i * d_i in route order; acc += shared
+    w = np.array([0.4, 0.3, 0.2, 0.1], dtype=np.float32)
+    y = oracle.moe_layer(x, pages, w, shared, hidden=hidden, inter=inter)
+    acc = np.zeros(hidden, dtype=np.float32)
+    for wi, di in zip(w, downs):
+        acc = (acc + (wi * di).astype(np.float32)).astype(np.float32)
+    acc = (acc + oracle.expert_down(x, shared, hidden=hidden, inter=inter)).astype(np.float32)
+    assert np.array_equal(y, acc)
+
+
+def test_layer_fp8_shared(oracle):
+    hidden, inter = 256, 128
+    x = np.random.default_rng(6).normal(0, 1, hidden).astype(np.float32)
+    pages = [synth.gen_mxfp4_page(8, 2, e, hidden=hidden, inter=inter) for e in range(2)]
+    sh = synth.gen_fp8_page(8, 2, hidden=hidden, inter=inter)
+    y = oracle.moe_layer(x, pages, [0.5, 0.5], sh, shared_fmt="fp8", hidden=hidden, inter=inter)
+    d_sh = oracle.expert_down(x, sh, fmt="fp8", hidden=hidden, inter=inter)
+    acc = np.zeros(hidden, dtype=np.float32)
+    for p in pages:
+        acc = (acc + np.float32(0.5) * oracle.expert_down(x, p, hidden=hidden, inter=inter)).astype(np.float32)
+    assert np.array_equal(y, (acc + d_sh).astype(np.float32))
+
+
+def test_error_stats_definition(oracle):
+    rng = np.random.default_rng(1)
+    e = rng.normal(0, 1, 1000).astype(np.float32)
+    e[:5] = 0.0
+    a = (e + rng.normal(0, 1e-5, 1000)).astype(np.float32)
+    st = oracle.error_stats(a, e)
+    d = np.abs(a - e).astype(np.float32)
+    assert st["max_abs"] == np.max(d)
+    assert abs(st["mean_abs"] - np.mean(d.astype(np.float64))) < 1e-15
+    assert abs(st["rmse"] - np.sqrt(np.mean(d.astype(np.float64) ** 2))) < 1e-15
+    m = np.abs(e) > 1e-5
+    assert st["max_rel_abs_ref_gt_1e_5"] == np.max(d[m] / np.abs(e[m]))
+    bad = a.copy()
+    bad[3] = np.nan
+    assert not oracle.error_stats(bad, e)["finite"]
+
+
+def test_requant_e4m3_against_torch(oracle):
+    rng = np.random.default_rng(12)
+    x = rng.normal(0, 1, (4, 256)).astype(np.float32)
+    x[1, :32] *= 1e-6  # amax floor of 1e-4 applies
+    q, s = oracle.requant_e4m3(x, group=32)
+    for r in range(4):
+        for g in range(8):
+            blk = x[r, g * 32:(g + 1) * 32]
+            amax = max(float(np.abs(blk).max()), float(np.float32(1e-4)))
+            ratio = np.float32(np.float32(amax) / np.float32(448))
+            m, e = np.frexp(np.float64(ratio))
+            want = e - 1 if m == 0.5 else e
+            assert int(s[r, g]) - 127 == want
+            scaled = np.clip(blk / np.float32(2.0**want), -448, 448).astype(np.float32)
+            ref = torch.from_numpy(scaled).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+            assert np.array_equal(q[r, g * 32:(g + 1) * 32], ref)
