@@ -190,7 +190,12 @@ def test_fp8_ue8m0_reference_variant_exact(pipes, oracle, n, k):
     s = synth.gen_ue8m0(14, 2, (-(-n // 128)) * (-(-k // 128)), -7, -5).reshape(-(-n // 128), -(-k // 128))
     x = synth.gen_normal(14, 3, k)
     y = torch.empty(n, dtype=torch.float32, device="cuda")
-    d = pipes.bind_fp8(s14.S14MatvecShape(n, k), dev(x), dev(w), dev(s), y, mode=s14.EXACT)
+    # buffers hold whole 4-byte words, as storage_bytes requires (s14_vulkan.rs:124-126)
+    w_words = np.zeros(-(-w.size // 4) * 4, dtype=np.uint8)
+    w_words[: w.size] = w.reshape(-1)
+    s_words = np.zeros(-(-s.size // 4) * 4, dtype=np.uint8)
+    s_words[: s.size] = s.reshape(-1)
+    d = pipes.bind_fp8(s14.S14MatvecShape(n, k), dev(x), dev(w_words), dev(s_words), y, mode=s14.EXACT)
     pipes.cmd_fp8_matvec(d)
     assert_bit_exact(host(y), oracle.fp8_matvec_ue8m0(x, w, s), "fp8 ue8m0 exact")
 
