@@ -192,6 +192,8 @@ SIGNATURES = {
     "s14_ctx_compute_stream": (P, [P]),
     "s14_ctx_copy_stream": (P, [P]),
     "s14_ctx_synchronize": (I, [P]),
+    "s14_ctx_enable_stage_timing": (I, [P, I]),
+    "s14_ctx_stage_times": (I, [P, C.POINTER(F), U32, C.POINTER(U32)]),
     "s14_bind_mxfp4": (I, [Shape, Buffer, Buffer, Buffer, Buffer, I, C.POINTER(Mxfp4Dispatch)]),
     "s14_bind_fp8": (I, [Shape, Buffer, I, Buffer, Buffer, I, Buffer, I, C.POINTER(Fp8Dispatch)]),
     "s14_bind_swiglu_limit": (I, [U32, Buffer, Buffer, Buffer, C.POINTER(SwigluDispatch)]),

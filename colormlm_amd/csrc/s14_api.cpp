@@ -24,6 +24,11 @@ struct s14_ctx {
   void *ws_base = nullptr;
   s14::Workspace ws{};
   s14::PageOffsets mx{}, fp8{};
+  // optional per-stage timestamps of the fused entry points (the role of
+  // the reference's Vulkan timestamp queries): plan/router, phase 1, phase 2
+  bool stage_timing = false;
+  hipEvent_t stage_ev[4] = {nullptr, nullptr, nullptr, nullptr};
+  bool stage_valid = false;
 };
 
 struct s14_fence {
@@ -42,8 +47,11 @@ int hip_fail(hipError_t e, const char *what) {
     if (_e != hipSuccess) return hip_fail(_e, what); \
   } while (0)
 
+// Streams follow HIP's convention: NULL is the device's null (default)
+// stream; the context's own streams are passed explicitly.
 hipStream_t pick(s14_ctx *ctx, void *stream) {
-  return stream ? reinterpret_cast<hipStream_t>(stream) : ctx->compute;
+  (void)ctx;
+  return reinterpret_cast<hipStream_t>(stream);
 }
 
 uint64_t storage_bytes(uint64_t logical) { return (logical + 3) / 4 * 4; }
@@ -87,24 +95,16 @@ extern "C" int s14_ctx_create(int device, s14_ctx **out) {
     s14_ctx_destroy(ctx);
     return hip_fail(e, "hipStreamCreate");
   }
-  // workspace: table | h | down | scores | biased | ids | weights | counters
+  // workspace: table | h | scores | biased
   size_t off = 0;
   const size_t o_table = off;
   off = align_up(off + sizeof(s14::PairTable), 256);
   const size_t o_h = off;
   off = align_up(off + sizeof(float) * s14::kMaxPairs * s14::kInter, 256);
-  const size_t o_down = off;
-  off = align_up(off + sizeof(float) * s14::kMaxPairs * s14::kHidden, 256);
   const size_t o_scores = off;
   off = align_up(off + sizeof(float) * s14::kMaxTokens * s14::kMaxExperts, 256);
   const size_t o_biased = off;
   off = align_up(off + sizeof(float) * s14::kMaxTokens * s14::kMaxExperts, 256);
-  const size_t o_ids = off;
-  off = align_up(off + sizeof(uint16_t) * s14::kMaxTokens * s14::kTopK, 256);
-  const size_t o_w = off;
-  off = align_up(off + sizeof(float) * s14::kMaxTokens * s14::kTopK, 256);
-  const size_t o_cnt = off;
-  off = align_up(off + sizeof(uint32_t) * s14::kNumCounters, 256);
   e = hipMalloc(&ctx->ws_base, off);
   if (e != hipSuccess) {
     s14_ctx_destroy(ctx);
@@ -113,15 +113,10 @@ extern "C" int s14_ctx_create(int device, s14_ctx **out) {
   uint8_t *b = static_cast<uint8_t *>(ctx->ws_base);
   ctx->ws.table = reinterpret_cast<s14::PairTable *>(b + o_table);
   ctx->ws.h = reinterpret_cast<float *>(b + o_h);
-  ctx->ws.down = reinterpret_cast<float *>(b + o_down);
   ctx->ws.scores = reinterpret_cast<float *>(b + o_scores);
   ctx->ws.biased = reinterpret_cast<float *>(b + o_biased);
-  ctx->ws.ids = reinterpret_cast<uint16_t *>(b + o_ids);
-  ctx->ws.weights = reinterpret_cast<float *>(b + o_w);
-  ctx->ws.counters = reinterpret_cast<uint32_t *>(b + o_cnt);
   ctx->ws.bytes = off;
-  // Completion counters start at zero and every launch leaves them at zero,
-  // so this is the only clear (no memset inside launch sequences).
+  // one clear at creation, outside any launch sequence
   e = hipMemset(ctx->ws_base, 0, off);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
@@ -146,6 +141,8 @@ extern "C" void s14_ctx_destroy(s14_ctx *ctx) {
   if (ctx->ws_base) (void)hipFree(ctx->ws_base);
   if (ctx->compute) (void)hipStreamDestroy(ctx->compute);
   if (ctx->copy) (void)hipStreamDestroy(ctx->copy);
+  for (auto ev : ctx->stage_ev)
+    if (ev) (void)hipEventDestroy(ev);
   delete ctx;
 }
 
@@ -348,10 +345,26 @@ s14::RouterArgs router_args(const s14_router *r) {
   return s14::RouterArgs{r->weight, r->bias, r->n_experts, r->topk, r->score_fn, r->route_scale};
 }
 
-int run_phases(s14_ctx *ctx, hipStream_t st, uint32_t n_pairs, uint32_t tokens, const float *x, float *y,
-               int mode) {
-  S14_LAUNCH(s14::launch_layer_phases(st, ctx->ws, n_pairs, tokens, ctx->mx, ctx->fp8, x, y, mode),
-             "layer phase launch");
+// Records stage timestamp i on `st` when stage timing is on.
+int stage_mark(s14_ctx *ctx, hipStream_t st, int i) {
+  if (!ctx->stage_timing) return S14_OK;
+  if (i == 0) ctx->stage_valid = false;
+  S14_HIP(hipEventRecord(ctx->stage_ev[i], st), "hipEventRecord(stage)");
+  if (i == 3) ctx->stage_valid = true;
+  return S14_OK;
+}
+
+// phase 1 -> phase 2 with stage marks 1..3 (mark 0 precedes the router and
+// the plan).
+int run_layer(s14_ctx *ctx, hipStream_t st, const s14::PairTable *host_plan, uint32_t n_pairs, uint32_t tokens,
+              const float *x, float *y, int mode) {
+  if (int rc = stage_mark(ctx, st, 1)) return rc;
+  hipError_t e = s14::launch_phase1(st, ctx->ws, host_plan, n_pairs, ctx->mx, ctx->fp8, x, mode);
+  if (e != hipSuccess) return hip_fail(e, "phase 1 launch");
+  if (int rc = stage_mark(ctx, st, 2)) return rc;
+  e = s14::launch_phase2(st, ctx->ws, tokens, ctx->mx, ctx->fp8, y, mode);
+  if (e != hipSuccess) return hip_fail(e, "phase 2 launch");
+  return stage_mark(ctx, st, 3);
 }
 
 }  // namespace
@@ -374,9 +387,8 @@ extern "C" int s14_expert_chain(s14_ctx *ctx, void *stream, const uint8_t *page,
   t.token_pairs[0][0] = 0;
   t.token_npairs[0] = 1;
   hipStream_t st = pick(ctx, stream);
-  hipError_t e = s14::launch_plan_from_host(st, ctx->ws, t);
-  if (e != hipSuccess) return hip_fail(e, "plan launch");
-  return run_phases(ctx, st, 1, 1, x, y, mode);
+  if (int rc = stage_mark(ctx, st, 0)) return rc;
+  return run_layer(ctx, st, &t, 1, 1, x, y, mode);
 }
 
 extern "C" int s14_moe_layer(s14_ctx *ctx, void *stream, uint32_t topk, const uint8_t *const *routed_pages,
@@ -414,9 +426,8 @@ extern "C" int s14_moe_layer(s14_ctx *ctx, void *stream, uint32_t topk, const ui
   t.n_distinct = topk;
   t.token_npairs[0] = n;
   hipStream_t st = pick(ctx, stream);
-  hipError_t e = s14::launch_plan_from_host(st, ctx->ws, t);
-  if (e != hipSuccess) return hip_fail(e, "plan launch");
-  return run_phases(ctx, st, n, 1, x, y, mode);
+  if (int rc = stage_mark(ctx, st, 0)) return rc;
+  return run_layer(ctx, st, &t, n, 1, x, y, mode);
 }
 
 extern "C" int s14_moe_block_route(s14_ctx *ctx, void *stream, uint32_t tokens, const s14_router *router,
@@ -434,10 +445,13 @@ extern "C" int s14_moe_block_route(s14_ctx *ctx, void *stream, uint32_t tokens, 
   if (shared_format != S14_PAGE_MXFP4 && shared_format != S14_PAGE_FP8)
     return fail(S14_ERR_INVALID, "unknown shared page format %d", shared_format);
   hipStream_t st = pick(ctx, stream);
-  hipError_t e = s14::launch_router_plan(st, ctx->ws, router_args(router), tokens, x, expert_pages_dev,
-                                         shared_page, shared_format, ids_out, weights_out, 1);
+  const s14::RouteSpec rs{router_args(router), tokens, shared_format, expert_pages_dev, shared_page, ids_out,
+                          weights_out};
+  if (int rc = stage_mark(ctx, st, 0)) return rc;
+  hipError_t e = s14::launch_router_scores(st, ctx->ws, rs.r, tokens, x);
+  if (e == hipSuccess) e = s14::launch_plan(st, ctx->ws, rs);
   if (e != hipSuccess) return hip_fail(e, "router launch");
-  return run_phases(ctx, st, tokens * (s14::kTopK + 1), tokens, x, y, mode);
+  return run_layer(ctx, st, nullptr, tokens * (s14::kTopK + 1), tokens, x, y, mode);
 }
 
 extern "C" int s14_moe_layer_route(s14_ctx *ctx, void *stream, const s14_router *router,
@@ -467,8 +481,9 @@ extern "C" int s14_route(s14_ctx *ctx, void *stream, const s14_router *router, u
     return fail(S14_ERR_SHAPE, "token count %u outside 1..%d", tokens, s14::kMaxTokens);
   if (!x) return fail(S14_ERR_INVALID, "NULL router input");
   hipStream_t st = pick(ctx, stream);
-  hipError_t e = s14::launch_router_plan(st, ctx->ws, router_args(router), tokens, x, nullptr, nullptr, 0,
-                                         ids_out, weights_out, 0);
+  const s14::RouteSpec rs{router_args(router), tokens, S14_PAGE_MXFP4, nullptr, nullptr, ids_out, weights_out};
+  hipError_t e = s14::launch_router_scores(st, ctx->ws, rs.r, tokens, x);
+  if (e == hipSuccess) e = s14::launch_plan(st, ctx->ws, rs);
   if (e != hipSuccess) return hip_fail(e, "router launch");
   if (scores_out) {
     for (uint32_t t = 0; t < tokens; ++t) {
@@ -539,4 +554,30 @@ extern "C" void s14_fence_destroy(s14_fence *fence) {
   if (!fence) return;
   if (fence->ev) (void)hipEventDestroy(fence->ev);
   delete fence;
+}
+
+// ---------------------------------------------------------------------------
+// stage timestamps
+// ---------------------------------------------------------------------------
+
+extern "C" int s14_ctx_enable_stage_timing(s14_ctx *ctx, int enable) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (enable && !ctx->stage_ev[0]) {
+    for (auto &ev : ctx->stage_ev) S14_HIP(hipEventCreate(&ev), "hipEventCreate(stage)");
+  }
+  ctx->stage_timing = enable != 0;
+  ctx->stage_valid = false;
+  return S14_OK;
+}
+
+extern "C" int s14_ctx_stage_times(s14_ctx *ctx, float *ms, uint32_t cap, uint32_t *n_stages) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!ms || !n_stages) return fail(S14_ERR_INVALID, "NULL stage-time output");
+  if (!ctx->stage_valid) return fail(S14_ERR_NOT_READY, "no timed launch recorded");
+  S14_HIP(hipEventSynchronize(ctx->stage_ev[3]), "hipEventSynchronize(stage)");
+  const uint32_t n = cap < 3 ? cap : 3;
+  for (uint32_t i = 0; i < n; ++i)
+    S14_HIP(hipEventElapsedTime(&ms[i], ctx->stage_ev[i], ctx->stage_ev[i + 1]), "hipEventElapsedTime");
+  *n_stages = 3;
+  return S14_OK;
 }

@@ -1,13 +1,17 @@
 // gfx950 (CDNA4) kernels of the S14 quantized expert path.
 //
 // Two reduction orders:
-//   EXACT  one output row per lane, k strictly ascending, multiply then add
-//          (no FMA) — the operation order of the reference CPU oracle
+//   EXACT  k strictly ascending, multiply then add (no FMA): the operation
+//          order of the reference CPU oracle
 //          (scheduler/ssd_inference/examples/s14_vulkan_numeric.rs:1669-1714),
-//          so outputs are bit-identical to it.  At batch 1 this is bound by
-//          the per-lane dependent-add chain, not by HBM.
+//          so outputs are bit-identical to it.  Each row is owned by a lane
+//          pair: in every group of 32 k the even lane forms the products of
+//          k 0..15 and the odd lane those of k 16..31; the even lane then adds
+//          its own 16 products and the odd lane's 16 (read through a DPP
+//          quad_perm operand of v_add) in k order.  The per-row dependent add
+//          chain, not HBM, bounds this order at batch 1.
 //   FAST   K split across the 64 lanes of a wavefront, products fused
-//          (v_fma), cross-lane tree reduction; HBM-bound.
+//          (v_fma), DPP cross-lane reduction; HBM-bound.
 // The reference's five shaders (shaders/s14_*.comp) are one workgroup per
 // row with a 128-way LDS tree; neither order here follows them.
 //
@@ -22,6 +26,7 @@ namespace s14 {
 namespace {
 
 typedef float v2f __attribute__((ext_vector_type(2)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 
@@ -41,6 +46,10 @@ __device__ __forceinline__ uint4 ld16(Rsrc r, uint32_t off) {
   const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ uint2 ld8(Rsrc r, uint32_t off) {
+  const v2u v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  return make_uint2(v.x, v.y);
+}
 __device__ __forceinline__ uint32_t ld4(Rsrc r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
@@ -48,6 +57,17 @@ __device__ __forceinline__ uint32_t ld1(Rsrc r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
 }
 __device__ __forceinline__ float ldf(Rsrc r, uint32_t off) { return __uint_as_float(ld4(r, off)); }
+
+// Where a row's bytes come from: one matrix (codes and scales may be
+// separate buffers), or two pages split by lane half (lanes 32-63 read page
+// b), each page holding its codes and scales.
+struct Src1 {
+  Rsrc w, s;
+};
+struct Src2 {
+  Rsrc a, b;
+  bool hi;
+};
 
 // ---------------------------------------------------------------------------
 // decoders (bit patterns; equal to s14_vulkan_numeric.rs:1716-1743)
@@ -89,14 +109,9 @@ __device__ __forceinline__ float swiglu_exact(float gate, float up) {
 }
 
 // ---------------------------------------------------------------------------
-// wavefront reductions
+// wavefront reductions and lane movement
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-  return v;
-}
 __device__ __forceinline__ int wave_min_i(int v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = min(v, __shfl_xor(v, m));
@@ -106,6 +121,53 @@ __device__ __forceinline__ int wave_max_i(int v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m));
   return v;
+}
+
+// DPP row operations.  dpp_f/dpp_i read the source lane given by CTRL; lanes
+// without a source (or in rows outside ROW_MASK) get `old`.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int dpp_i(int old, int v) {
+  return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xf, false);
+}
+
+// Value of the odd lane of each lane pair (quad_perm [1,1,3,3]); every lane
+// has a source, so the move folds into the consuming VALU op as a DPP operand.
+__device__ __forceinline__ float from_odd(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xF5, 0xf, 0xf, true));
+}
+
+// Full-wavefront sum (order-changing; FAST mode only), returned to every lane.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f<0xb1>(0.0f, v);        // quad_perm [1,0,3,2]
+  v += dpp_f<0x4e>(0.0f, v);        // quad_perm [2,3,0,1]
+  v += dpp_f<0x114>(0.0f, v);       // row_shr:4
+  v += dpp_f<0x118>(0.0f, v);       // row_shr:8
+  v += dpp_f<0x142, 0xa>(0.0f, v);  // row_bcast:15
+  v += dpp_f<0x143, 0xc>(0.0f, v);  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Arg-max over the wavefront of (v, i) with ties to the lower index; i < 0
+// marks an empty candidate.  The order is total on non-NaN values, so the
+// DPP tree's shape does not matter.  Result returned to every lane.
+__device__ __forceinline__ void argmax_step(float &v, int &i, float ov, int oi) {
+  const bool take = oi >= 0 && (i < 0 || ov > v || (ov == v && oi < i));
+  v = take ? ov : v;
+  i = take ? oi : i;
+}
+__device__ __forceinline__ int wave_argmax(float v, int i) {
+  argmax_step(v, i, dpp_f<0xb1>(v, v), dpp_i<0xb1>(i, i));
+  argmax_step(v, i, dpp_f<0x4e>(v, v), dpp_i<0x4e>(i, i));
+  argmax_step(v, i, dpp_f<0x114>(v, v), dpp_i<0x114>(i, i));
+  argmax_step(v, i, dpp_f<0x118>(v, v), dpp_i<0x118>(i, i));
+  argmax_step(v, i, dpp_f<0x142, 0xa>(v, v), dpp_i<0x142, 0xa>(i, i));
+  argmax_step(v, i, dpp_f<0x143, 0xc>(v, v), dpp_i<0x143, 0xc>(i, i));
+  return __builtin_amdgcn_readlane(i, 63);
 }
 
 // Biased-exponent range of the nonzero finite values seen by this lane.
@@ -122,7 +184,8 @@ __device__ __forceinline__ void exp_range_acc(float v, int &lo, int &hi) {
 // oracle's (x * e2m1) * 2^(c-127): both products stay normal and the scaled
 // decode is exact.  With every nonzero finite x in [2^(emin-127),
 // 2^(emax-126)): requires emin >= 2 (x*0.5 normal), emax <= 251 (x*6
-// finite); then c in [max(2, 129 - emin), 252].  Other groups take the
+// finite); then c in [max(2, 129 - emin), 252].  (Infinite or NaN x give
+// the same inf/NaN either way.)  Batches holding other codes take the
 // literal two-multiply path.
 struct CodeWindow {
   int cmin, cmax;
@@ -132,208 +195,398 @@ __device__ __forceinline__ CodeWindow mx_window(int emin, int emax) {
   return {max(2, 129 - emin), 252};
 }
 
+// Stage S vectors of N f32 (N % 256 == 0) from global memory into LDS with
+// the calling wavefront (lane-strided float4), returning each vector's
+// exponent window.  Every global load is issued before the first LDS store:
+// a generic source pointer may alias LDS, so the compiler would otherwise
+// wait for each load in turn.  The caller synchronises before reading the
+// LDS copies.
+template <int N, int S>
+__device__ __forceinline__ void stage_x_wave(float *const (&dst)[S], const float *const (&src)[S],
+                                             CodeWindow (&win)[S]) {
+  static_assert(N % 256 == 0, "whole float4 sweeps");
+  constexpr int IT = N / 256;
+  const int lane = int(threadIdx.x & 63);
+  float4 v[S][IT];
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int it = 0; it < IT; ++it) v[s][it] = *reinterpret_cast<const float4 *>(src[s] + it * 256 + lane * 4);
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    int lo = 255, hi = 0;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      *reinterpret_cast<float4 *>(dst[s] + it * 256 + lane * 4) = v[s][it];
+      exp_range_acc(v[s][it].x, lo, hi);
+      exp_range_acc(v[s][it].y, lo, hi);
+      exp_range_acc(v[s][it].z, lo, hi);
+      exp_range_acc(v[s][it].w, lo, hi);
+    }
+    win[s] = mx_window(wave_min_i(lo), wave_max_i(hi));
+  }
+}
+
+// Copy n f32 (n % 4 == 0) into LDS with the calling wavefront, eight float4
+// loads in flight per lane.
+__device__ __forceinline__ void stage_chunk_wave(float *dst, const float *__restrict__ src, uint32_t n) {
+  const uint32_t lane = threadIdx.x & 63;
+  uint32_t i = lane * 4;
+  for (; i + 7 * 256 < n; i += 8 * 256) {
+    float4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4 *>(src + i + j * 256);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *reinterpret_cast<float4 *>(dst + i + j * 256) = v[j];
+  }
+  for (; i < n; i += 256) *reinterpret_cast<float4 *>(dst + i) = *reinterpret_cast<const float4 *>(src + i);
+}
+
 // ---------------------------------------------------------------------------
-// EXACT row kernels
+// EXACT row engine (lane pairs)
 // ---------------------------------------------------------------------------
 
-// One group of 32 k values (16 code bytes, one scale code) of an MXFP4 row,
-// in the oracle's order: pair by pair, low nibble (even k) then high nibble.
-__device__ __forceinline__ float mx_group_exact(float acc, const uint4 w, uint32_t c,
-                                                const float *__restrict__ xs, CodeWindow win) {
-  const float4 *x4 = reinterpret_cast<const float4 *>(xs);
-  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-  if (c >= uint32_t(win.cmin) && c <= uint32_t(win.cmax)) {
-    const float sc = __uint_as_float(c << 23);
+// The 16 x values of a lane's half-group, from LDS (two distinct addresses
+// per wavefront: even and odd lanes).
+struct X16 {
+  float v[16];
+};
+__device__ __forceinline__ void load_x16(X16 &x, const float *__restrict__ xs) {
+  const float4 *p = reinterpret_cast<const float4 *>(xs);
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const float4 xa = x4[2 * d], xb = x4[2 * d + 1];
-      const v2f p0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[d], sc, 0);
-      const v2f p1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[d], sc, 1);
-      const v2f p2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[d], sc, 2);
-      const v2f p3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[d], sc, 3);
-      acc = __fadd_rn(acc, __fmul_rn(xa.x, p0.x));
-      acc = __fadd_rn(acc, __fmul_rn(xa.y, p0.y));
-      acc = __fadd_rn(acc, __fmul_rn(xa.z, p1.x));
-      acc = __fadd_rn(acc, __fmul_rn(xa.w, p1.y));
-      acc = __fadd_rn(acc, __fmul_rn(xb.x, p2.x));
-      acc = __fadd_rn(acc, __fmul_rn(xb.y, p2.y));
-      acc = __fadd_rn(acc, __fmul_rn(xb.z, p3.x));
-      acc = __fadd_rn(acc, __fmul_rn(xb.w, p3.y));
-    }
-  } else {
-    const float s = ue8m0_f32(c);
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const float4 xa = x4[2 * d], xb = x4[2 * d + 1];
-      const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float e = e2m1_f32((words[d] >> (4 * j)) & 15u);
-        acc = __fadd_rn(acc, __fmul_rn(__fmul_rn(xv[j], e), s));
-      }
-    }
+  for (int d = 0; d < 4; ++d) {
+    const float4 q = p[d];
+    x.v[4 * d + 0] = q.x;
+    x.v[4 * d + 1] = q.y;
+    x.v[4 * d + 2] = q.z;
+    x.v[4 * d + 3] = q.w;
   }
+}
+
+// acc = acc + p for the even lane's 16 products, then for the odd lane's 16,
+// in k order (the odd lane's result is not used).
+__device__ __forceinline__ float pair_chain16(float acc, const float (&p)[16]) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc = __fadd_rn(acc, p[j]);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc = __fadd_rn(acc, from_odd(p[j]));
   return acc;
 }
 
-// Dot of one MXFP4 row (G groups of 32) with x staged in LDS, k ascending.
-// Code bytes live at r[woff + 16 g], scale codes at rs[soff + g]; they are
-// prefetched PF groups ahead (PF * 16 B per lane in flight).
+// MXFP4 products of the lane's 8 code bytes (16 k, low nibble first).
+// Scaled: p = x * (e2m1 * 2^(c-127)) via the gfx950 scaled converter — equal
+// to the oracle's (x * e2m1) * 2^(c-127) for codes inside the window.
+__device__ __forceinline__ void mx_products_scaled(float (&p)[16], uint2 w, uint32_t c, const X16 &x) {
+  const float sc = __uint_as_float(c << 23);
+  const uint32_t words[2] = {w.x, w.y};
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const v2f q[4] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[d], sc, 0),
+                      __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[d], sc, 1),
+                      __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[d], sc, 2),
+                      __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[d], sc, 3)};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      p[8 * d + 2 * s] = __fmul_rn(x.v[8 * d + 2 * s], q[s].x);
+      p[8 * d + 2 * s + 1] = __fmul_rn(x.v[8 * d + 2 * s + 1], q[s].y);
+    }
+  }
+}
+// Literal: p = (x * e2m1) * ue8m0(c), any code.
+__device__ __forceinline__ void mx_products_literal(float (&p)[16], uint2 w, uint32_t c, const X16 &x) {
+  const float s = ue8m0_f32(c);
+  const uint32_t words[2] = {w.x, w.y};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float e = e2m1_f32((words[j >> 3] >> (4 * (j & 7))) & 15u);
+    p[j] = __fmul_rn(__fmul_rn(x.v[j], e), s);
+  }
+}
+
 template <int PF>
-__device__ __forceinline__ float mx_row_exact(float acc, Rsrc r, uint32_t woff, Rsrc rs, uint32_t soff,
-                                              int G, const float *__restrict__ xs, CodeWindow win) {
-  static_assert(PF % 4 == 0, "scale words hold 4 codes");
-  uint4 cur[PF];
-  uint32_t cs[PF / 4];
+struct MxBatch {
+  uint2 w[PF];
+  uint32_t c[PF / 4];
+};
+
+// Codes of groups [g0, g0+PF): the lane's 8 bytes at woff + 16 g (woff
+// includes the lane's half-group offset), scale codes at soff + g.  Loads
+// past a row's end read neighbouring bytes or, past num_records, zeros;
+// such values are never consumed.
+template <int PF>
+__device__ __forceinline__ void mx_load(MxBatch<PF> &b, const Src1 &src, uint32_t woff, uint32_t soff, int g0) {
 #pragma unroll
-  for (int i = 0; i < PF; ++i) cur[i] = ld16(r, woff + 16u * i);
+  for (int i = 0; i < PF; ++i) b.w[i] = ld8(src.w, woff + 16u * uint32_t(g0 + i));
 #pragma unroll
-  for (int j = 0; j < PF / 4; ++j) cs[j] = ld4(rs, soff + 4u * j);
-  for (int g0 = 0; g0 < G; g0 += PF) {
-    uint4 nxt[PF];
-    uint32_t ns[PF / 4];
-    const bool more = (g0 + PF) < G;
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < PF; ++i) nxt[i] = ld16(r, woff + 16u * (g0 + PF + i));
-#pragma unroll
-      for (int j = 0; j < PF / 4; ++j) ns[j] = ld4(rs, soff + uint32_t(g0 + PF) + 4u * j);
-    }
-#pragma unroll
-    for (int i = 0; i < PF; ++i)
-      acc = mx_group_exact(acc, cur[i], (cs[i >> 2] >> (8 * (i & 3))) & 255u, xs + (g0 + i) * 32, win);
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < PF; ++i) cur[i] = nxt[i];
-#pragma unroll
-      for (int j = 0; j < PF / 4; ++j) cs[j] = ns[j];
-    }
-  }
-  return acc;
+  for (int j = 0; j < PF / 4; ++j) b.c[j] = ld4(src.s, soff + uint32_t(g0) + 4u * j);
+}
+template <int PF>
+__device__ __forceinline__ void mx_load(MxBatch<PF> &b, const Src2 &src, uint32_t woff, uint32_t soff, int g0) {
+  if (src.hi)
+    mx_load<PF>(b, Src1{src.b, src.b}, woff, soff, g0);
+  else
+    mx_load<PF>(b, Src1{src.a, src.a}, woff, soff, g0);
 }
 
-// Dot of one FP8 row with x in LDS: sum += (x * e4m3) * scale, k ascending
-// (s14_vulkan_numeric.rs:1698-1714).  Codes at rw[woff + k]; the row's tile
-// scales (ceil(K/128) of them, ue8m0 bytes or f32) at rs[soff + ...].
-// K16: K % 16 == 0 and woff % 16 == 0.
-template <bool K16>
-__device__ __forceinline__ float fp8_row_exact(float acc, Rsrc rw, uint32_t woff, Rsrc rs, uint32_t soff,
-                                               int scale_f32, int K, const float *__restrict__ xs) {
-  if (K16) {
-    uint4 cur = ld16(rw, woff);
-    for (int k0 = 0; k0 < K; k0 += 16) {
-      uint4 nxt = cur;
-      if (k0 + 16 < K) nxt = ld16(rw, woff + uint32_t(k0) + 16u);
-      const uint32_t t = uint32_t(k0 >> 7);
-      const float s = scale_f32 ? ldf(rs, soff + 4u * t) : ue8m0_f32(ld1(rs, soff + t));
-      const uint32_t words[4] = {cur.x, cur.y, cur.z, cur.w};
-      const float4 *x4 = reinterpret_cast<const float4 *>(xs + k0);
+__device__ __forceinline__ bool codes_in(uint32_t word, CodeWindow win) {
+  bool ok = true;
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const float4 xv = x4[d];
-        const v2f lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, false);
-        const v2f hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, true);
-        acc = __fadd_rn(acc, __fmul_rn(__fmul_rn(xv.x, lo.x), s));
-        acc = __fadd_rn(acc, __fmul_rn(__fmul_rn(xv.y, lo.y), s));
-        acc = __fadd_rn(acc, __fmul_rn(__fmul_rn(xv.z, hi.x), s));
-        acc = __fadd_rn(acc, __fmul_rn(__fmul_rn(xv.w, hi.y), s));
-      }
-      cur = nxt;
+  for (int i = 0; i < 4; ++i) {
+    const int c = int((word >> (8 * i)) & 255u);
+    ok = ok && c >= win.cmin && c <= win.cmax;
+  }
+  return ok;
+}
+
+template <int PF>
+__device__ __forceinline__ uint32_t batch_code(const MxBatch<PF> &b, int i) {
+  return (b.c[i >> 2] >> (8 * (i & 3))) & 255u;
+}
+
+// One batch: if every lane's codes are inside its window the batch runs the
+// scaled decode as straight-line code, software-pipelined: group i+1's x
+// reads and products are issued ahead of group i's add chain, so LDS latency
+// and the chain's DPP read-after-write waits overlap independent work.
+// Otherwise the batch takes the literal decode.
+template <int PF>
+__device__ __forceinline__ float mx_consume(float acc, const MxBatch<PF> &b, const float *__restrict__ xh, int g0,
+                                            CodeWindow win) {
+  bool ok = true;
+#pragma unroll
+  for (int j = 0; j < PF / 4; ++j) ok = ok && codes_in(b.c[j], win);
+  if (__builtin_amdgcn_ballot_w64(!ok) == 0) {
+    X16 xa, xb;
+    float p[16], q[16];
+    load_x16(xa, xh + g0 * 32);
+    load_x16(xb, xh + (g0 + 1) * 32);
+    mx_products_scaled(p, b.w[0], batch_code(b, 0), xa);
+#pragma unroll
+    for (int i = 0; i < PF; i += 2) {
+      // p holds group i's products; xb holds group i+1's x
+      if (i + 2 < PF) load_x16(xa, xh + (g0 + i + 2) * 32);
+      mx_products_scaled(q, b.w[i + 1], batch_code(b, i + 1), xb);
+      acc = pair_chain16(acc, p);
+      if (i + 3 < PF) load_x16(xb, xh + (g0 + i + 3) * 32);
+      if (i + 2 < PF) mx_products_scaled(p, b.w[i + 2], batch_code(b, i + 2), xa);
+      acc = pair_chain16(acc, q);
     }
   } else {
-    for (int k = 0; k < K; ++k) {
-      const uint32_t t = uint32_t(k >> 7);
-      const float s = scale_f32 ? ldf(rs, soff + 4u * t) : ue8m0_f32(ld1(rs, soff + t));
-      acc = __fadd_rn(acc, __fmul_rn(__fmul_rn(xs[k], e4m3_f32(ld1(rw, woff + uint32_t(k)))), s));
+    float p[16];
+    X16 x;
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      load_x16(x, xh + (g0 + i) * 32);
+      mx_products_literal(p, b.w[i], batch_code(b, i), x);
+      acc = pair_chain16(acc, p);
     }
   }
   return acc;
 }
 
-// Stage n f32 (n % 4 == 0) from global to LDS with the whole block, and
-// return the block-uniform exponent range (1-wave blocks only).
-__device__ __forceinline__ void stage_f32_range(float *dst, const float *__restrict__ src, int n,
-                                                int &emin, int &emax) {
-  int lo = 255, hi = 0;
-  for (int i = int(threadIdx.x) * 4; i < n; i += int(blockDim.x) * 4) {
-    const float4 v = *reinterpret_cast<const float4 *>(src + i);
-    *reinterpret_cast<float4 *>(dst + i) = v;
-    exp_range_acc(v.x, lo, hi);
-    exp_range_acc(v.y, lo, hi);
-    exp_range_acc(v.z, lo, hi);
-    exp_range_acc(v.w, lo, hi);
+// Dot of one MXFP4 row of G groups (G % PF == 0) with x in LDS (xh = x +
+// 16 * (lane & 1)); result in the even lane.  `ba` arrives holding groups
+// [0, PF) (loaded by the caller with mx_load, ahead of its own set-up work);
+// two register batches of PF groups then ping-pong so that batch b+1 is in
+// flight while batch b is consumed.
+template <int PF, class Src>
+__device__ __forceinline__ float mx_row_pair(float acc, MxBatch<PF> &ba, const Src &src, uint32_t woff,
+                                             uint32_t soff, int G, const float *__restrict__ xh, CodeWindow win) {
+  static_assert(PF % 4 == 0, "scale words hold 4 codes");
+  MxBatch<PF> bb;
+  int g0 = 0;
+  for (; g0 + 2 * PF <= G; g0 += 2 * PF) {
+    mx_load<PF>(bb, src, woff, soff, g0 + PF);
+    acc = mx_consume<PF>(acc, ba, xh, g0, win);
+    mx_load<PF>(ba, src, woff, soff, g0 + 2 * PF);
+    acc = mx_consume<PF>(acc, bb, xh, g0 + PF, win);
   }
-  emin = wave_min_i(lo);
-  emax = wave_max_i(hi);
-  __syncthreads();
+  if (g0 < G) acc = mx_consume<PF>(acc, ba, xh, g0, win);  // one batch left
+  return acc;
 }
 
-constexpr int kExactChunk = 4096;  // x staged in LDS in chunks of this many k
+// FP8 products of the lane's 16 code bytes: p = (x * e4m3) * s
+// (s14_vulkan_numeric.rs:1698-1714).
+__device__ __forceinline__ void fp8_products(float (&p)[16], uint4 w, float s, const X16 &x) {
+  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const v2f lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, false);
+    const v2f hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, true);
+    p[4 * d + 0] = __fmul_rn(__fmul_rn(x.v[4 * d + 0], lo.x), s);
+    p[4 * d + 1] = __fmul_rn(__fmul_rn(x.v[4 * d + 1], lo.y), s);
+    p[4 * d + 2] = __fmul_rn(__fmul_rn(x.v[4 * d + 2], hi.x), s);
+    p[4 * d + 3] = __fmul_rn(__fmul_rn(x.v[4 * d + 3], hi.y), s);
+  }
+}
 
-// Standalone EXACT MXFP4 matvec: one wavefront per 64 rows.
+// FP8 batch: 4 groups of 32 k (one 128-wide scale tile when g0 % 4 == 0).
+struct Fp8Batch {
+  uint4 w[4];
+  float s;
+};
+__device__ __forceinline__ float fp8_scale(Rsrc r, uint32_t soff, uint32_t tile, int scale_f32) {
+  return scale_f32 ? ldf(r, soff + 4u * tile) : ue8m0_f32(ld1(r, soff + tile));
+}
+__device__ __forceinline__ void fp8_load(Fp8Batch &b, const Src1 &src, uint32_t woff, uint32_t soff, int scale_f32,
+                                         int g0) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b.w[i] = ld16(src.w, woff + 32u * uint32_t(g0 + i));
+  b.s = fp8_scale(src.s, soff, uint32_t(g0) / 4u, scale_f32);
+}
+__device__ __forceinline__ void fp8_load(Fp8Batch &b, const Src2 &src, uint32_t woff, uint32_t soff, int scale_f32,
+                                         int g0) {
+  if (src.hi)
+    fp8_load(b, Src1{src.b, src.b}, woff, soff, scale_f32, g0);
+  else
+    fp8_load(b, Src1{src.a, src.a}, woff, soff, scale_f32, g0);
+}
+// Four groups, pipelined like mx_consume.
+__device__ __forceinline__ float fp8_consume(float acc, const Fp8Batch &b, const float *__restrict__ xh, int g0) {
+  X16 xa, xb;
+  float p[16], q[16];
+  load_x16(xa, xh + g0 * 32);
+  load_x16(xb, xh + (g0 + 1) * 32);
+  fp8_products(p, b.w[0], b.s, xa);
+#pragma unroll
+  for (int i = 0; i < 4; i += 2) {
+    if (i + 2 < 4) load_x16(xa, xh + (g0 + i + 2) * 32);
+    fp8_products(q, b.w[i + 1], b.s, xb);
+    acc = pair_chain16(acc, p);
+    if (i + 3 < 4) load_x16(xb, xh + (g0 + i + 3) * 32);
+    if (i + 2 < 4) fp8_products(p, b.w[i + 2], b.s, xa);
+    acc = pair_chain16(acc, q);
+  }
+  return acc;
+}
+
+// Dot of one FP8 row of G groups of 32 k with x in LDS (woff includes the
+// lane's 16-byte half-group offset; soff is the byte offset of the row's
+// first tile scale); result in the even lane.
+template <class Src>
+__device__ __forceinline__ float fp8_row_pair(float acc, const Src &src, uint32_t woff, uint32_t soff,
+                                              int scale_f32, int G, const float *__restrict__ xh) {
+  const int G4 = G & ~3;
+  Fp8Batch ba, bb;
+  fp8_load(ba, src, woff, soff, scale_f32, 0);
+  int g0 = 0;
+  for (; g0 + 8 <= G4; g0 += 8) {
+    fp8_load(bb, src, woff, soff, scale_f32, g0 + 4);
+    acc = fp8_consume(acc, ba, xh, g0);
+    fp8_load(ba, src, woff, soff, scale_f32, g0 + 8);
+    acc = fp8_consume(acc, bb, xh, g0 + 4);
+  }
+  if (g0 < G4) {
+    acc = fp8_consume(acc, ba, xh, g0);
+    g0 += 4;
+  }
+  for (; g0 < G; ++g0) {  // groups of a last partial tile
+    Fp8Batch t;
+    fp8_load(t, src, woff, soff, scale_f32, g0);  // loads 4 groups, uses one
+    float p[16];
+    X16 x;
+    load_x16(x, xh + g0 * 32);
+    fp8_products(p, t.w[0], t.s, x);
+    acc = pair_chain16(acc, p);
+  }
+  return acc;
+}
+
+// ---------------------------------------------------------------------------
+// standalone EXACT matvecs: 32 rows per wavefront (one row per lane pair),
+// x staged in LDS in chunks of kExactChunk
+// ---------------------------------------------------------------------------
+
+constexpr int kExactChunk = 4096;
+
 __global__ __launch_bounds__(64) void k_mxfp4_matvec_exact(uint32_t N, uint32_t K,
                                                            const float *__restrict__ x,
                                                            const uint8_t *__restrict__ w,
                                                            const uint8_t *__restrict__ sc,
                                                            float *__restrict__ y) {
   __shared__ float xs[kExactChunk];
+  const uint32_t lane = threadIdx.x, h = lane & 1u;
   int lo = 255, hi = 0;
-  for (uint32_t i = threadIdx.x; i < K; i += 64) exp_range_acc(x[i], lo, hi);
+  for (uint32_t i = lane; i < K; i += 64) exp_range_acc(x[i], lo, hi);
   const CodeWindow win = mx_window(wave_min_i(lo), wave_max_i(hi));
-  const Rsrc rw = make_rsrc(w, N * (K / 2));
-  const Rsrc rs = make_rsrc(sc, N * (K / 32));
-  const uint32_t row = blockIdx.x * 64u + threadIdx.x;
+  const Src1 src{make_rsrc(w, N * (K / 2)), make_rsrc(sc, N * (K / 32))};
+  const uint32_t row = blockIdx.x * 32u + (lane >> 1);
   const bool active = row < N;
   const uint32_t rr = active ? row : 0u;
   float acc = 0.0f;
   for (uint32_t c0 = 0; c0 < K; c0 += kExactChunk) {
     const uint32_t n = min(uint32_t(kExactChunk), K - c0);
+    const uint32_t woff = rr * (K / 2) + c0 / 2 + 8u * h, soff = rr * (K / 32) + c0 / 32;
+    const int G = int(n / 32);
     __syncthreads();
-    for (uint32_t i = threadIdx.x * 4; i < n; i += 256)
-      *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(x + c0 + i);
-    __syncthreads();
-    // one resource per matrix; only the row offsets differ between lanes
-    const uint32_t woff = rr * (K / 2) + c0 / 2, soff = rr * (K / 32) + c0 / 32;
-    acc = (((n / 32) & 15) == 0) ? mx_row_exact<16>(acc, rw, woff, rs, soff, int(n / 32), xs, win)
-                                 : mx_row_exact<4>(acc, rw, woff, rs, soff, int(n / 32), xs, win);
+    if (G % 16 == 0) {
+      MxBatch<16> ba;
+      mx_load<16>(ba, src, woff, soff, 0);
+      stage_chunk_wave(xs, x + c0, n);
+      __syncthreads();
+      acc = mx_row_pair<16>(acc, ba, src, woff, soff, G, xs + 16 * h, win);
+    } else {
+      MxBatch<4> ba;
+      mx_load<4>(ba, src, woff, soff, 0);
+      stage_chunk_wave(xs, x + c0, n);
+      __syncthreads();
+      acc = mx_row_pair<4>(acc, ba, src, woff, soff, G, xs + 16 * h, win);
+    }
   }
-  if (active) y[row] = acc;
+  if (active && h == 0) y[row] = acc;
 }
 
-// Standalone EXACT FP8 matvec: one wavefront per 64 rows.
-template <bool K16>
+// K % 32 == 0: lane pairs as above.  Otherwise every lane computes its pair's
+// whole row itself, element by element.
+template <bool K32>
 __global__ __launch_bounds__(64) void k_fp8_matvec_exact(uint32_t N, uint32_t K, const void *x,
                                                          int x_bf16, const uint8_t *__restrict__ w,
                                                          const void *__restrict__ sc, int scale_f32,
                                                          float *__restrict__ y) {
   __shared__ float xs[kExactChunk];
-  const uint32_t row = blockIdx.x * 64u + threadIdx.x;
+  const uint32_t lane = threadIdx.x, h = lane & 1u;
+  const uint32_t row = blockIdx.x * 32u + (lane >> 1);
   const bool active = row < N;
   const uint32_t rr = active ? row : 0u;
   const uint32_t kg = (K + 127) / 128;
   const uint32_t ntile = ((N + 127) / 128) * kg;
-  const Rsrc rw = make_rsrc(w, N * K);
-  const Rsrc rs = make_rsrc(sc, scale_f32 ? 4u * ntile : ntile);
+  const Src1 src{make_rsrc(w, N * K), make_rsrc(sc, scale_f32 ? 4u * ntile : ntile)};
   const uint32_t tile_row = (rr / 128) * kg;
   float acc = 0.0f;
   for (uint32_t c0 = 0; c0 < K; c0 += kExactChunk) {
     const uint32_t n = min(uint32_t(kExactChunk), K - c0);
     __syncthreads();
-    if (x_bf16)
-      for (uint32_t i = threadIdx.x; i < n; i += 64) xs[i] = bf16_f32(reinterpret_cast<const uint16_t *>(x)[c0 + i]);
-    else
-      for (uint32_t i = threadIdx.x; i < n; i += 64) xs[i] = reinterpret_cast<const float *>(x)[c0 + i];
+    // element-wise (x may be unaligned), eight loads in flight per lane
+    for (uint32_t i0 = lane; i0 < n; i0 += 64 * 8) {
+      float t[8];
+#pragma unroll
+      for (uint32_t j = 0; j < 8; ++j) {
+        const uint32_t i = i0 + 64 * j;
+        t[j] = i >= n ? 0.0f
+                      : (x_bf16 ? bf16_f32(reinterpret_cast<const uint16_t *>(x)[c0 + i])
+                                : reinterpret_cast<const float *>(x)[c0 + i]);
+      }
+#pragma unroll
+      for (uint32_t j = 0; j < 8; ++j)
+        if (i0 + 64 * j < n) xs[i0 + 64 * j] = t[j];
+    }
     __syncthreads();
     const uint32_t soff = (scale_f32 ? 4u : 1u) * (tile_row + c0 / 128);
-    acc = fp8_row_exact<K16>(acc, rw, rr * K + c0, rs, soff, scale_f32, int(n), xs);
+    if (K32) {
+      acc = fp8_row_pair(acc, src, rr * K + c0 + 16u * h, soff, scale_f32, int(n / 32), xs + 16 * h);
+    } else {
+      for (uint32_t k = 0; k < n; ++k) {
+        const float s = fp8_scale(src.s, soff, k / 128, scale_f32);
+        acc = __fadd_rn(acc, __fmul_rn(__fmul_rn(xs[k], e4m3_f32(ld1(src.w, rr * K + c0 + k))), s));
+      }
+    }
   }
-  if (active) y[row] = acc;
+  if (active && h == 0) y[row] = acc;
 }
 
 // ---------------------------------------------------------------------------
-// FAST row kernels: lane l owns k in [2048 s + 32 l, +32) for each 2048-wide
+// FAST row engine: lane l owns k in [2048 s + 32 l, +32) for each 2048-wide
 // segment s (MXFP4), x held in registers; rows streamed with coalesced
-// 16-byte loads; one cross-lane reduction per row.
+// 16-byte loads; one DPP reduction per row.
 // ---------------------------------------------------------------------------
 
 template <int NSEG>
@@ -411,6 +664,35 @@ __device__ __forceinline__ float mx_row_fast_partial(const MxRowFrag (&f)[NSEG],
   return acc;
 }
 
+// FP8 pages, same lane ownership: two 16-byte loads and one ue8m0 tile
+// scale per segment.
+template <int NSEG>
+__device__ __forceinline__ float fp8_row_fast_partial(Rsrc r, uint32_t woff, uint32_t soff_tiles,
+                                                      const XReg<NSEG> &xr) {
+  const int lane = threadIdx.x & 63;
+  float acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < NSEG; ++s) {
+    const uint32_t k0 = uint32_t(s * 2048 + lane * 32);
+    const uint4 a = ld16(r, woff + k0);
+    const uint4 b = ld16(r, woff + k0 + 16u);
+    const float sc = ue8m0_f32(ld1(r, soff_tiles + k0 / 128));
+    const uint32_t words[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float part = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const v2f lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, false);
+      const v2f hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, true);
+      part = fmaf(xr.v[s * 32 + 4 * d + 0], lo.x, part);
+      part = fmaf(xr.v[s * 32 + 4 * d + 1], lo.y, part);
+      part = fmaf(xr.v[s * 32 + 4 * d + 2], hi.x, part);
+      part = fmaf(xr.v[s * 32 + 4 * d + 3], hi.y, part);
+    }
+    acc = fmaf(part, sc, acc);
+  }
+  return acc;
+}
+
 // Standalone FAST MXFP4 matvec: 4 wavefronts per block, R rows per wavefront.
 template <int NSEG, int R>
 __global__ __launch_bounds__(256) void k_mxfp4_matvec_fast(uint32_t N, uint32_t K,
@@ -432,7 +714,7 @@ __global__ __launch_bounds__(256) void k_mxfp4_matvec_fast(uint32_t N, uint32_t 
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float v = wave_sum(mx_row_fast_partial<NSEG>(f[r], xr));
+    const float v = wave_sum_dpp(mx_row_fast_partial<NSEG>(f[r], xr));
     if ((threadIdx.x & 63) == 0 && row0 + r < N) y[row0 + r] = v;
   }
 }
@@ -488,8 +770,7 @@ __global__ __launch_bounds__(256) void k_fp8_matvec_fast(uint32_t N, uint32_t K,
     const int k0 = s * 1024 + lane * 16;
     if (k0 < int(K)) {
       wf[s] = ld16(rw, row * K + uint32_t(k0));
-      const uint32_t t = srow + uint32_t(k0 / 128);
-      sv[s] = scale_f32 ? ldf(rs, 4u * t) : ue8m0_f32(ld1(rs, t));
+      sv[s] = fp8_scale(rs, 0u, srow + uint32_t(k0 / 128), scale_f32);
     } else {
       wf[s] = make_uint4(0u, 0u, 0u, 0u);
       sv[s] = 0.0f;
@@ -511,7 +792,7 @@ __global__ __launch_bounds__(256) void k_fp8_matvec_fast(uint32_t N, uint32_t K,
     }
     acc = fmaf(part, sv[s], acc);
   }
-  acc = wave_sum(acc);
+  acc = wave_sum_dpp(acc);
   if (lane == 0) y[row] = acc;
 }
 
@@ -573,7 +854,7 @@ __global__ void k_dequant_fp8(uint32_t N, uint32_t K, const uint8_t *__restrict_
 }
 
 // ---------------------------------------------------------------------------
-// synthetic page fill: the oracle generator's integer hash, on the device
+// synthetic page fill: the host generator's integer hash, on the device
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ uint64_t mix64(uint64_t z) {
@@ -611,165 +892,170 @@ __global__ void k_fill_page(uint8_t *__restrict__ page, uint64_t seed, uint32_t 
 }
 
 // ---------------------------------------------------------------------------
-// fused layer / block path
+// fused layer / block path: router -> plan -> phase 1 -> phase 2
+//
+// No workgroup waits on another inside a kernel (an agent-scope release on
+// gfx950 writes back the L2, and one per workgroup serialised an earlier
+// design); each hand-off is a kernel boundary:
+//   router   scores and biased scores of every (token, expert)
+//   plan     one workgroup: top-k of every token, the renormalised weights,
+//            and the pair table sorted expert-major (each distinct routed
+//            page's tokens are adjacent in the grid)
+//   phase 1  h = swiglu(w1 x, w3 x) for every (token, expert) pair
+//   phase 2  one workgroup per (row tile, token) computes the token's routed
+//            and shared w2 rows and accumulates them in route order, shared
+//            last, in LDS (s14_vulkan_numeric.rs:929-946)
 // ---------------------------------------------------------------------------
-
-// Agent-scope acquire-release counter increment; returns the old value.
-__device__ __forceinline__ uint32_t counter_arrive(uint32_t *c) {
-  return __hip_atomic_fetch_add(c, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void counter_reset(uint32_t *c) {
-  __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <typename T>
-__device__ __forceinline__ T load_agent(const T *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__global__ void k_plan_from_host(PairTable plan, PairTable *__restrict__ out) {
-  const uint32_t *src = reinterpret_cast<const uint32_t *>(&plan);
-  uint32_t *dst = reinterpret_cast<uint32_t *>(out);
-  for (uint32_t i = threadIdx.x; i < sizeof(PairTable) / 4; i += blockDim.x) dst[i] = src[i];
-}
 
 // Router: one wavefront per (expert, token).  Logit order (fixed here; the
 // reference uses torch F.linear, executor.py:641, whose order is the
 // BLAS's): lane l sums k = 256c + 4l + j (c ascending, j = 0..3), then the
-// xor butterfly over lanes.  The last block of a token picks the top-k of
-// score + bias (ties to the lower index) and the renormalised weights; the
-// last token to finish writes the expert-major PairTable.
-__global__ __launch_bounds__(256) void k_router_plan(RouterArgs r, uint32_t T, const float *__restrict__ X,
-                                                     Workspace ws, const uint64_t *__restrict__ expert_pages,
-                                                     const uint8_t *shared_page, int shared_fmt,
-                                                     uint16_t *ids_out, float *weights_out, int build_plan) {
+// xor butterfly over lanes.  Score: sigmoid (north-star config) or
+// sqrt(softplus) with torch's threshold 20 (executor.py:642).
+__global__ __launch_bounds__(256) void k_router_scores(RouterArgs r, const float *__restrict__ X,
+                                                       float *__restrict__ scores, float *__restrict__ biased) {
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t t = blockIdx.y;
   const uint32_t e = blockIdx.x * 4u + wave;
+  if (e >= r.n_experts) return;
   const uint32_t K = kHidden;
   const float *x = X + size_t(t) * K;
-  if (e < r.n_experts) {
-    const float *row = r.weight + size_t(e) * K;
-    float acc = 0.0f;
-    for (uint32_t c = 0; c < K / 256; ++c) {
-      const uint32_t k = c * 256 + lane * 4;
-      const float4 wv = *reinterpret_cast<const float4 *>(row + k);
-      const float4 xv = *reinterpret_cast<const float4 *>(x + k);
-      acc = __fadd_rn(acc, __fmul_rn(wv.x, xv.x));
-      acc = __fadd_rn(acc, __fmul_rn(wv.y, xv.y));
-      acc = __fadd_rn(acc, __fmul_rn(wv.z, xv.z));
-      acc = __fadd_rn(acc, __fmul_rn(wv.w, xv.w));
-    }
+  const float *row = r.weight + size_t(e) * K;
+  float4 wv[K / 256], xv[K / 256];
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, m));
-    if (lane == 0) {
-      float s;
-      if (r.score_fn == S14_SCORE_SIGMOID) {
-        s = __fdiv_rn(1.0f, __fadd_rn(1.0f, s14x::expf_glibc(-acc)));
-      } else {
-        const float sp = acc > 20.0f ? acc : log1pf(s14x::expf_glibc(acc));
-        s = __fsqrt_rn(sp);
-      }
-      ws.scores[t * kMaxExperts + e] = s;
-      ws.biased[t * kMaxExperts + e] = __fadd_rn(s, r.bias[e]);
-    }
+  for (uint32_t c = 0; c < K / 256; ++c) {
+    wv[c] = *reinterpret_cast<const float4 *>(row + c * 256 + lane * 4);
+    xv[c] = *reinterpret_cast<const float4 *>(x + c * 256 + lane * 4);
   }
-  __threadfence();
-  __syncthreads();
-  __shared__ uint32_t s_old;
-  if (threadIdx.x == 0) s_old = counter_arrive(&ws.counters[t]);
-  __syncthreads();
-  if (s_old != gridDim.x - 1u || wave != 0) return;
-  // ---- last block of token t: top-k on wavefront 0 ----
-  if (lane == 0) counter_reset(&ws.counters[t]);
-  float v[4];
-  bool taken[4];
+  float acc = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t ee = lane + 64u * j;
-    taken[j] = ee >= r.n_experts;
-    v[j] = taken[j] ? 0.0f : load_agent(&ws.biased[t * kMaxExperts + ee]);
+  for (uint32_t c = 0; c < K / 256; ++c) {
+    acc = __fadd_rn(acc, __fmul_rn(wv[c].x, xv[c].x));
+    acc = __fadd_rn(acc, __fmul_rn(wv[c].y, xv[c].y));
+    acc = __fadd_rn(acc, __fmul_rn(wv[c].z, xv[c].z));
+    acc = __fadd_rn(acc, __fmul_rn(wv[c].w, xv[c].w));
   }
-  uint32_t sel[kTopK];
-  for (uint32_t i = 0; i < r.topk; ++i) {
-    float bv = 0.0f;
-    int bi = 0x7fffffff;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, m));
+  if (lane == 0) {
+    float s;
+    if (r.score_fn == S14_SCORE_SIGMOID) {
+      s = __fdiv_rn(1.0f, __fadd_rn(1.0f, s14x::expf_glibc(-acc)));
+    } else {
+      const float sp = acc > 20.0f ? acc : log1pf(s14x::expf_glibc(acc));
+      s = __fsqrt_rn(sp);
+    }
+    scores[t * kMaxExperts + e] = s;
+    biased[t * kMaxExperts + e] = __fadd_rn(s, r.bias[e]);
+  }
+}
+
+// Plan: wavefront t selects token t's top-k of score + bias (ties to the
+// lower index) and its weights s/sum (sum sequential in selection order)
+// times route_scale (executor.py:647-667); wavefront 0 then sorts the
+// (expert, token) pairs expert-major, appends the shared pairs and
+// publishes the pair table.  expert_pages == NULL: route only.
+__global__ __launch_bounds__(64 * kMaxTokens) void k_plan(RouteSpec rs, Workspace ws) {
+  __shared__ uint32_t ids[kMaxTokens][kTopK];
+  __shared__ float wts[kMaxTokens][kTopK];
+  __shared__ uint64_t pgs[kMaxTokens][kTopK];
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t t = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const RouterArgs &r = rs.r;
+  const uint32_t k = r.topk;
+  if (t < rs.tokens) {
+    // biased and unbiased scores and page addresses of experts lane + 64 j,
+    // all loaded up front (no memory access depends on a selection)
+    float v[4], sv[4];
+    uint64_t pv[4];
+    bool taken[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (!taken[j] && (bi == 0x7fffffff || v[j] > bv)) {
-        bv = v[j];
-        bi = int(lane + 64u * j);
+      const uint32_t ee = lane + 64u * j;
+      taken[j] = ee >= r.n_experts;
+      v[j] = taken[j] ? 0.0f : ws.biased[t * kMaxExperts + ee];
+      sv[j] = taken[j] ? 0.0f : ws.scores[t * kMaxExperts + ee];
+      pv[j] = (taken[j] || !rs.expert_pages) ? 0ull : rs.expert_pages[ee];
+    }
+    float sum = 0.0f, my_s = 0.0f;
+    uint32_t my_id = 0;
+    uint64_t my_pg = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < uint32_t(kTopK); ++i) {
+      if (i >= k) break;
+      float bv = 0.0f;
+      int bi = -1;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (!taken[j] && (bi < 0 || v[j] > bv)) {
+          bv = v[j];
+          bi = int(lane + 64u * j);
+        }
+      }
+      const int best = wave_argmax(bv, bi);
+      float cand = sv[0];
+      uint64_t cpg = pv[0];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (int(lane + 64u * j) == best) taken[j] = true;
+        if ((best >> 6) == j) {
+          cand = sv[j];
+          cpg = pv[j];
+        }
+      }
+      const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cand), best & 63));
+      const uint64_t pg = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(cpg >> 32), best & 63))) << 32) |
+                          uint32_t(__builtin_amdgcn_readlane(int(uint32_t(cpg)), best & 63));
+      sum = __fadd_rn(sum, s);
+      if (lane == i) {
+        my_id = uint32_t(best);
+        my_s = s;
+        my_pg = pg;
       }
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const float ov = __shfl_xor(bv, m);
-      const int oi = __shfl_xor(bi, m);
-      const bool better = (oi != 0x7fffffff) && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
-      if (better) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    sel[i] = uint32_t(bi);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (int(lane + 64u * j) == bi) taken[j] = true;
-  }
-  if (lane == 0) {
-    float sc[kTopK];
-    float sum = 0.0f;
-    for (uint32_t i = 0; i < r.topk; ++i) {
-      sc[i] = load_agent(&ws.scores[t * kMaxExperts + sel[i]]);
-      sum = __fadd_rn(sum, sc[i]);
-    }
-    for (uint32_t i = 0; i < r.topk; ++i) {
-      float wgt = __fdiv_rn(sc[i], sum);
+    if (lane < k) {
+      float wgt = __fdiv_rn(my_s, sum);
       if (r.route_scale != 1.0f) wgt = __fmul_rn(wgt, r.route_scale);
-      ws.ids[t * kTopK + i] = uint16_t(sel[i]);
-      ws.weights[t * kTopK + i] = wgt;
-      if (ids_out) ids_out[t * r.topk + i] = uint16_t(sel[i]);
-      if (weights_out) weights_out[t * r.topk + i] = wgt;
+      ids[t][lane] = my_id;
+      wts[t][lane] = wgt;
+      pgs[t][lane] = my_pg;
+      if (rs.ids_out) rs.ids_out[t * k + lane] = uint16_t(my_id);
+      if (rs.weights_out) rs.weights_out[t * k + lane] = wgt;
     }
   }
-  if (!build_plan) return;
-  __threadfence();
-  uint32_t old = 0;
-  if (lane == 0) old = counter_arrive(&ws.counters[kCntPlan]);
-  old = __shfl(old, 0);
-  if (old != T - 1u) return;
-  // ---- last token: expert-major PairTable ----
-  if (lane == 0) counter_reset(&ws.counters[kCntPlan]);
-  const uint32_t npr = T * kTopK;  // routed (token, expert) pairs, <= 48
+  if (!rs.expert_pages) return;  // route only (uniform: no barrier below is skipped by part of the group)
+  __syncthreads();
+  if (t != 0) return;
+  const uint32_t T = rs.tokens, npr = T * k;  // routed pairs, <= 48
   const bool mine = lane < npr;
-  const uint32_t mt = mine ? lane / kTopK : 0u, mr = mine ? lane % kTopK : 0u;
-  const uint32_t me = mine ? uint32_t(load_agent(&ws.ids[mt * kTopK + mr])) : 0u;
-  const float mw = mine ? load_agent(&ws.weights[mt * kTopK + mr]) : 0.0f;
-  const uint32_t key = mine ? me * 8u + mt : 0xffffffffu;
+  const uint32_t mt = mine ? lane / k : 0u, mr = mine ? lane % k : 0u;
+  const uint32_t me = mine ? ids[mt][mr] : 0u;
+  const uint32_t key = mine ? me * 8u + mt : 0xffffffffu;  // unique: an expert appears once per token
   uint32_t rank = 0, first = 1;
   for (uint32_t j = 0; j < npr; ++j) {
-    const uint32_t kj = __shfl(key, int(j));
+    const uint32_t kj = uint32_t(__builtin_amdgcn_readlane(int(key), int(j)));
     rank += kj < key ? 1u : 0u;
     if ((kj >> 3) == (key >> 3) && kj < key) first = 0;
   }
   PairTable *tab = ws.table;
   if (mine) {
-    tab->page[rank] = expert_pages[me];
+    tab->page[rank] = pgs[mt][mr];
     tab->fmt[rank] = S14_PAGE_MXFP4;
     tab->token[rank] = mt;
-    tab->weight[rank] = mw;
+    tab->weight[rank] = wts[mt][mr];
     tab->is_shared[rank] = 0u;
     tab->token_pairs[mt][mr] = rank;
   }
   const uint64_t firsts = __ballot(mine && first);
   if (lane < T) {
     const uint32_t sp = npr + lane;
-    tab->page[sp] = reinterpret_cast<uint64_t>(shared_page);
-    tab->fmt[sp] = uint32_t(shared_fmt);
+    tab->page[sp] = reinterpret_cast<uint64_t>(rs.shared_page);
+    tab->fmt[sp] = uint32_t(rs.shared_fmt);
     tab->token[sp] = lane;
     tab->weight[sp] = 1.0f;
     tab->is_shared[sp] = 1u;
-    tab->token_pairs[lane][kTopK] = sp;
-    tab->token_npairs[lane] = kTopK + 1;
+    tab->token_pairs[lane][k] = sp;
+    tab->token_npairs[lane] = k + 1;
   }
   if (lane == 0) {
     tab->n_pairs = npr + T;
@@ -779,145 +1065,83 @@ __global__ __launch_bounds__(256) void k_router_plan(RouterArgs r, uint32_t T, c
   }
 }
 
-// Final per-token accumulation of one row tile, run by the last block to
-// finish that (token, tile): acc = 0; acc += w * down in route order; acc +=
-// shared down (s14_vulkan_numeric.rs:929-946); or y = w * down for the chain
-// (:1300).
-__device__ __forceinline__ void accumulate_tail(const PairTable *__restrict__ tab, uint32_t p,
-                                                uint32_t tile, uint32_t rows_per_tile,
-                                                const float *down, float *__restrict__ Y,
-                                                uint32_t *counters) {
-  __threadfence();
-  __syncthreads();
-  __shared__ uint32_t s_old;
-  const uint32_t t = tab->token[p];
-  uint32_t *cnt = &counters[kCntAcc + t * kMaxTiles + tile];
-  if (threadIdx.x == 0) s_old = counter_arrive(cnt);
-  __syncthreads();
-  const uint32_t np = tab->token_npairs[t];
-  if (s_old != np - 1u) return;
-  if (threadIdx.x == 0) counter_reset(cnt);
-  for (uint32_t i = threadIdx.x; i < rows_per_tile; i += blockDim.x) {
-    const uint32_t row = tile * rows_per_tile + i;
-    float acc = 0.0f;
-    if (tab->chain) {
-      const uint32_t pr = tab->token_pairs[t][0];
-      acc = __fmul_rn(tab->weight[pr], load_agent(&down[size_t(pr) * kHidden + row]));
-    } else {
-      for (uint32_t j = 0; j < np; ++j) {
-        const uint32_t pr = tab->token_pairs[t][j];
-        const float d = load_agent(&down[size_t(pr) * kHidden + row]);
-        acc = tab->is_shared[pr] ? __fadd_rn(acc, d) : __fadd_rn(acc, __fmul_rn(tab->weight[pr], d));
-      }
+// Pair p of phase 1: from the host plan (by value; workgroup (0,0) also
+// publishes it for phase 2) or from the table the plan kernel wrote.
+struct PairRef {
+  const uint8_t *page;
+  uint32_t fmt;
+  uint32_t token;
+};
+
+template <bool kHostPlan>
+__device__ __forceinline__ PairRef phase1_pair(const PairTable &plan, PairTable *__restrict__ tab, uint32_t p) {
+  if (kHostPlan) {
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+      const uint32_t *src = reinterpret_cast<const uint32_t *>(&plan);
+      uint32_t *dst = reinterpret_cast<uint32_t *>(tab);
+      for (uint32_t i = threadIdx.x; i < sizeof(PairTable) / 4; i += blockDim.x) dst[i] = src[i];
     }
-    Y[size_t(t) * kHidden + row] = acc;
+    return PairRef{reinterpret_cast<const uint8_t *>(plan.page[p]), plan.fmt[p], plan.token[p]};
   }
+  return PairRef{reinterpret_cast<const uint8_t *>(tab->page[p]), tab->fmt[p], tab->token[p]};
 }
 
-// Phase 1 EXACT: one wavefront per (pair, 32-row tile); lanes 0-31 take rows
-// of w1, lanes 32-63 the same rows of w3; h = swiglu(g, u) after a lane swap.
-__global__ __launch_bounds__(64) void k_phase1_exact(const PairTable *__restrict__ tab,
-                                                     const float *__restrict__ X, float *__restrict__ H,
-                                                     PageOffsets mx, PageOffsets f8, uint32_t mx_bytes,
-                                                     uint32_t f8_bytes) {
+__device__ __forceinline__ uint32_t page_bytes(uint32_t fmt) {
+  return fmt == S14_PAGE_MXFP4 ? uint32_t(S14_EXPERT_PAGE_BYTES) : uint32_t(S14_SHARED_EXPERT_PAGE_BYTES);
+}
+
+// Phase 1 EXACT: one wavefront per (16-row tile, pair); lanes 0-31 take the
+// tile's rows of w1, lanes 32-63 the same rows of w3, one row per lane pair;
+// h = swiglu(g, u) after a half swap.
+template <bool kHostPlan>
+__global__ __launch_bounds__(64) void k_phase1_exact(PairTable plan, Workspace ws, const float *__restrict__ X,
+                                                     PageOffsets mx, PageOffsets f8) {
   __shared__ float xs[kHidden];
   const uint32_t p = blockIdx.y;
-  if (p >= tab->n_pairs) return;
-  const uint32_t lane = threadIdx.x;
-  int emin, emax;
-  stage_f32_range(xs, X + size_t(tab->token[p]) * kHidden, kHidden, emin, emax);
-  const uint8_t *page = reinterpret_cast<const uint8_t *>(tab->page[p]);
+  const PairRef pr = phase1_pair<kHostPlan>(plan, ws.table, p);
+  const uint32_t lane = threadIdx.x, h = lane & 1u;
   const bool upper = lane >= 32;
-  const uint32_t row = blockIdx.x * kP1ExactRows + (lane & 31u);
+  const uint32_t row = blockIdx.x * kP1ExactRows + ((lane & 31u) >> 1);
+  const Rsrc r = make_rsrc(pr.page, page_bytes(pr.fmt));
+  const Src1 src{r, r};
+  float *const dst[1] = {xs};
+  const float *const srcx[1] = {X + size_t(pr.token) * kHidden};
+  CodeWindow win[1];
   float acc;
-  if (tab->fmt[p] == S14_PAGE_MXFP4) {
-    const Rsrc r = make_rsrc(page, mx_bytes);
-    const uint32_t woff = uint32_t(upper ? mx.w3 : mx.w1) + row * (kHidden / 2);
+  if (pr.fmt == S14_PAGE_MXFP4) {
+    const uint32_t woff = uint32_t(upper ? mx.w3 : mx.w1) + row * (kHidden / 2) + 8u * h;
     const uint32_t soff = uint32_t(upper ? mx.s3 : mx.s1) + row * (kHidden / 32);
-    acc = mx_row_exact<16>(0.0f, r, woff, r, soff, kHidden / 32, xs, mx_window(emin, emax));
+    MxBatch<16> ba;
+    mx_load<16>(ba, src, woff, soff, 0);  // first weights in flight during the x copy
+    stage_x_wave<kHidden, 1>(dst, srcx, win);
+    __syncthreads();
+    acc = mx_row_pair<16>(0.0f, ba, src, woff, soff, kHidden / 32, xs + 16 * h, win[0]);
   } else {
-    const Rsrc r = make_rsrc(page, f8_bytes);
-    const uint32_t woff = uint32_t(upper ? f8.w3 : f8.w1) + row * kHidden;
+    const uint32_t woff = uint32_t(upper ? f8.w3 : f8.w1) + row * kHidden + 16u * h;
     const uint32_t soff = uint32_t(upper ? f8.s3 : f8.s1) + (row / 128) * (kHidden / 128);
-    acc = fp8_row_exact<true>(0.0f, r, woff, r, soff, 0, kHidden, xs);
+    stage_x_wave<kHidden, 1>(dst, srcx, win);
+    __syncthreads();
+    acc = fp8_row_pair(0.0f, src, woff, soff, 0, kHidden / 32, xs + 16 * h);
   }
   const float other = __shfl_xor(acc, 32);
-  if (!upper) H[size_t(p) * kInter + row] = swiglu_exact(acc, other);
+  if (!upper && h == 0) ws.h[size_t(p) * kInter + row] = swiglu_exact(acc, other);
 }
 
-// Phase 2 EXACT: one wavefront per (pair, 64-row tile) of w2.
-__global__ __launch_bounds__(64) void k_phase2_exact(const PairTable *__restrict__ tab,
-                                                     const float *__restrict__ H, float *D,
-                                                     float *__restrict__ Y, uint32_t *counters,
-                                                     PageOffsets mx, PageOffsets f8, uint32_t mx_bytes,
-                                                     uint32_t f8_bytes) {
-  __shared__ float hs[kInter];
-  const uint32_t p = blockIdx.y;
-  if (p >= tab->n_pairs) return;
-  int emin, emax;
-  stage_f32_range(hs, H + size_t(p) * kInter, kInter, emin, emax);
-  const uint8_t *page = reinterpret_cast<const uint8_t *>(tab->page[p]);
-  const uint32_t row = blockIdx.x * kP2ExactRows + threadIdx.x;
-  float acc;
-  if (tab->fmt[p] == S14_PAGE_MXFP4) {
-    const Rsrc r = make_rsrc(page, mx_bytes);
-    acc = mx_row_exact<16>(0.0f, r, uint32_t(mx.w2) + row * (kInter / 2), r,
-                           uint32_t(mx.s2) + row * (kInter / 32), kInter / 32, hs, mx_window(emin, emax));
-  } else {
-    const Rsrc r = make_rsrc(page, f8_bytes);
-    acc = fp8_row_exact<true>(0.0f, r, uint32_t(f8.w2) + row * kInter, r,
-                              uint32_t(f8.s2) + (row / 128) * (kInter / 128), 0, kInter, hs);
-  }
-  D[size_t(p) * kHidden + row] = acc;
-  accumulate_tail(tab, p, blockIdx.x, kP2ExactRows, D, Y, counters);
-}
-
-// FAST helpers for FP8 pages: lane l owns k in [2048 s + 32 l, +32) as for
-// MXFP4, i.e. two 16-byte loads per segment, one ue8m0 tile scale.
-template <int NSEG>
-__device__ __forceinline__ float fp8_row_fast_partial(Rsrc r, uint32_t woff, uint32_t soff_tiles,
-                                                      const XReg<NSEG> &xr) {
-  const int lane = threadIdx.x & 63;
-  float acc = 0.0f;
-#pragma unroll
-  for (int s = 0; s < NSEG; ++s) {
-    const uint32_t k0 = uint32_t(s * 2048 + lane * 32);
-    const uint4 a = ld16(r, woff + k0);
-    const uint4 b = ld16(r, woff + k0 + 16u);
-    const float sc = ue8m0_f32(ld1(r, soff_tiles + k0 / 128));
-    const uint32_t words[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    float part = 0.0f;
-#pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      const v2f lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, false);
-      const v2f hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, true);
-      part = fmaf(xr.v[s * 32 + 4 * d + 0], lo.x, part);
-      part = fmaf(xr.v[s * 32 + 4 * d + 1], lo.y, part);
-      part = fmaf(xr.v[s * 32 + 4 * d + 2], hi.x, part);
-      part = fmaf(xr.v[s * 32 + 4 * d + 3], hi.y, part);
-    }
-    acc = fmaf(part, sc, acc);
-  }
-  return acc;
-}
-
-// Phase 1 FAST: 4 wavefronts per block, each kP1FastRowsPerWave rows of w1
-// and w3 (x for the lane's k slices held in registers).
-__global__ __launch_bounds__(256) void k_phase1_fast(const PairTable *__restrict__ tab,
-                                                     const float *__restrict__ X, float *__restrict__ H,
-                                                     PageOffsets mx, PageOffsets f8, uint32_t mx_bytes,
-                                                     uint32_t f8_bytes) {
+// Phase 1 FAST: 4 wavefronts per workgroup, each kP1FastRowsPerWave rows of
+// w1 and w3 (x for the lane's k slices held in registers).
+template <bool kHostPlan>
+__global__ __launch_bounds__(256) void k_phase1_fast(PairTable plan, Workspace ws, const float *__restrict__ X,
+                                                     PageOffsets mx, PageOffsets f8) {
   constexpr int NSEG = kHidden / 2048;
   constexpr int R = kP1FastRowsPerWave;
   const uint32_t p = blockIdx.y;
-  if (p >= tab->n_pairs) return;
+  const PairRef pr = phase1_pair<kHostPlan>(plan, ws.table, p);
   XReg<NSEG> xr;
-  load_x_mx<NSEG>(xr, X + size_t(tab->token[p]) * kHidden, kHidden);
-  const uint8_t *page = reinterpret_cast<const uint8_t *>(tab->page[p]);
+  load_x_mx<NSEG>(xr, X + size_t(pr.token) * kHidden, kHidden);
   const uint32_t row0 = blockIdx.x * kP1FastRows + (threadIdx.x >> 6) * R;
+  const Rsrc r = make_rsrc(pr.page, page_bytes(pr.fmt));
   float g[R], u[R];
-  if (tab->fmt[p] == S14_PAGE_MXFP4) {
-    const Rsrc r = make_rsrc(page, mx_bytes);
+  if (pr.fmt == S14_PAGE_MXFP4) {
     MxRowFrag f1[R][NSEG], f3[R][NSEG];
 #pragma unroll
     for (int i = 0; i < R; ++i) {
@@ -929,18 +1153,17 @@ __global__ __launch_bounds__(256) void k_phase1_fast(const PairTable *__restrict
     }
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      g[i] = wave_sum(mx_row_fast_partial<NSEG>(f1[i], xr));
-      u[i] = wave_sum(mx_row_fast_partial<NSEG>(f3[i], xr));
+      g[i] = wave_sum_dpp(mx_row_fast_partial<NSEG>(f1[i], xr));
+      u[i] = wave_sum_dpp(mx_row_fast_partial<NSEG>(f3[i], xr));
     }
   } else {
-    const Rsrc r = make_rsrc(page, f8_bytes);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const uint32_t row = row0 + i;
-      g[i] = wave_sum(fp8_row_fast_partial<NSEG>(r, uint32_t(f8.w1) + row * kHidden,
-                                                 uint32_t(f8.s1) + (row / 128) * (kHidden / 128), xr));
-      u[i] = wave_sum(fp8_row_fast_partial<NSEG>(r, uint32_t(f8.w3) + row * kHidden,
-                                                 uint32_t(f8.s3) + (row / 128) * (kHidden / 128), xr));
+      g[i] = wave_sum_dpp(fp8_row_fast_partial<NSEG>(r, uint32_t(f8.w1) + row * kHidden,
+                                                     uint32_t(f8.s1) + (row / 128) * (kHidden / 128), xr));
+      u[i] = wave_sum_dpp(fp8_row_fast_partial<NSEG>(r, uint32_t(f8.w3) + row * kHidden,
+                                                     uint32_t(f8.s3) + (row / 128) * (kHidden / 128), xr));
     }
   }
   const int lane = threadIdx.x & 63;
@@ -952,54 +1175,145 @@ __global__ __launch_bounds__(256) void k_phase1_fast(const PairTable *__restrict
         gv = g[i];
         uv = u[i];
       }
-    H[size_t(p) * kInter + row0 + lane] = swiglu_exact(gv, uv);
+    ws.h[size_t(p) * kInter + row0 + lane] = swiglu_exact(gv, uv);
   }
 }
 
-// Phase 2 FAST: 4 wavefronts per block, kP2FastRowsPerWave rows of w2 each.
-__global__ __launch_bounds__(256) void k_phase2_fast(const PairTable *__restrict__ tab,
-                                                     const float *__restrict__ H, float *D,
-                                                     float *__restrict__ Y, uint32_t *counters,
-                                                     PageOffsets mx, PageOffsets f8, uint32_t mx_bytes,
-                                                     uint32_t f8_bytes) {
-  constexpr int NSEG = kInter / 2048;
-  constexpr int R = kP2FastRowsPerWave;
-  const uint32_t p = blockIdx.y;
-  if (p >= tab->n_pairs) return;
-  XReg<NSEG> xr;
-  load_x_mx<NSEG>(xr, H + size_t(p) * kInter, kInter);
-  const uint8_t *page = reinterpret_cast<const uint8_t *>(tab->page[p]);
-  const uint32_t row0 = blockIdx.x * kP2FastRows + (threadIdx.x >> 6) * R;
-  float d[R];
-  if (tab->fmt[p] == S14_PAGE_MXFP4) {
-    const Rsrc r = make_rsrc(page, mx_bytes);
-    MxRowFrag f[R][NSEG];
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      const uint32_t row = row0 + i;
-      load_mx_row_frag<NSEG>(f[i], r, uint32_t(mx.w2) + row * (kInter / 2), r,
-                             uint32_t(mx.s2) + row * (kInter / 32), kInter);
-    }
-#pragma unroll
-    for (int i = 0; i < R; ++i) d[i] = wave_sum(mx_row_fast_partial<NSEG>(f[i], xr));
+// Phase 2 accumulation of one row tile of token t from part[slot][row]:
+// acc = 0; acc += w * down (routed, route order); acc += down (shared) — or
+// y = w * down for the single-expert chain.
+template <int ROWS>
+__device__ __forceinline__ void phase2_accumulate(const PairTable *__restrict__ tab, uint32_t t, uint32_t np,
+                                                  const float (*part)[ROWS], uint32_t row0, float *__restrict__ Y) {
+  const uint32_t lane = threadIdx.x;
+  if (lane >= uint32_t(ROWS)) return;
+  float acc = 0.0f;
+  if (tab->chain) {
+    acc = __fmul_rn(tab->weight[tab->token_pairs[t][0]], part[0][lane]);
   } else {
-    const Rsrc r = make_rsrc(page, f8_bytes);
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      const uint32_t row = row0 + i;
-      d[i] = wave_sum(fp8_row_fast_partial<NSEG>(r, uint32_t(f8.w2) + row * kInter,
-                                                 uint32_t(f8.s2) + (row / 128) * (kInter / 128), xr));
+    for (uint32_t j = 0; j < np; ++j) {
+      const uint32_t p = tab->token_pairs[t][j];
+      const float d = part[j][lane];
+      acc = tab->is_shared[p] ? __fadd_rn(acc, d) : __fadd_rn(acc, __fmul_rn(tab->weight[p], d));
     }
   }
-  const int lane = threadIdx.x & 63;
-  if (lane < R) {
-    float v = d[0];
-#pragma unroll
-    for (int i = 1; i < R; ++i)
-      if (lane == i) v = d[i];
-    D[size_t(p) * kHidden + row0 + lane] = v;
+  Y[size_t(t) * kHidden + row0 + lane] = acc;
+}
+
+// Phase 2 EXACT: one workgroup of kP2ExactWaves wavefronts per (16-row tile,
+// token).  Wavefront w serves the token's pair slots 2w (lanes 0-31) and
+// 2w+1 (lanes 32-63), one row per lane pair, with each slot's h staged in
+// LDS (row stride padded so the two slots' reads fall in different banks).
+constexpr int kP2Slots = kTopK + 1;
+constexpr int kHStride = kInter + 8;
+
+__global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairTable *__restrict__ tab,
+                                                                     const float *__restrict__ H,
+                                                                     float *__restrict__ Y, PageOffsets mx,
+                                                                     PageOffsets f8) {
+  __shared__ float hs[kP2Slots][kHStride];
+  __shared__ float part[kP2Slots][kP2ExactRows];
+  const uint32_t t = blockIdx.y;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const uint32_t np = tab->token_npairs[t];
+  const uint32_t sa = 2 * wave, sb = 2 * wave + 1;
+  const bool has_a = sa < np, has_b = sb < np;
+  const bool hi = lane >= 32;
+  const uint32_t h = lane & 1u, r = (lane & 31u) >> 1;
+  const uint32_t row = blockIdx.x * kP2ExactRows + r;
+  const uint32_t slot = (hi && has_b) ? sb : sa;
+  // pair, page and format of both slots (b falls back to a when absent)
+  const uint32_t pa = has_a ? tab->token_pairs[t][sa] : 0u;
+  const uint32_t pb = has_b ? tab->token_pairs[t][sb] : pa;
+  const uint32_t fa = tab->fmt[pa], fb = tab->fmt[pb];
+  const Src2 src{make_rsrc(reinterpret_cast<const uint8_t *>(tab->page[pa]), page_bytes(fa)),
+                 make_rsrc(reinterpret_cast<const uint8_t *>(tab->page[pb]), page_bytes(fb)), hi};
+  const bool mine_mx = (hi ? fb : fa) == S14_PAGE_MXFP4;
+  const uint32_t mx_woff = uint32_t(mx.w2) + row * (kInter / 2) + 8u * h;
+  const uint32_t mx_soff = uint32_t(mx.s2) + row * (kInter / 32);
+  MxBatch<16> ba;
+  if (has_a && fa == S14_PAGE_MXFP4 && fb == S14_PAGE_MXFP4)
+    mx_load<16>(ba, src, mx_woff, mx_soff, 0);  // first weights in flight during the h copy
+  CodeWindow win[2] = {{256, 0}, {256, 0}};
+  if (has_b) {
+    float *const dst[2] = {hs[sa], hs[sb]};
+    const float *const srch[2] = {H + size_t(pa) * kInter, H + size_t(pb) * kInter};
+    stage_x_wave<kInter, 2>(dst, srch, win);
+  } else if (has_a) {
+    float *const dst[1] = {hs[sa]};
+    const float *const srch[1] = {H + size_t(pa) * kInter};
+    CodeWindow w1[1];
+    stage_x_wave<kInter, 1>(dst, srch, w1);
+    win[0] = win[1] = w1[0];
   }
-  accumulate_tail(tab, p, blockIdx.x, kP2FastRows, D, Y, counters);
+  __syncthreads();
+  if (has_a) {
+    const float *xh = hs[slot] + 16 * h;
+    float acc;
+    if (fa == S14_PAGE_MXFP4 && fb == S14_PAGE_MXFP4) {
+      acc = mx_row_pair<16>(0.0f, ba, src, mx_woff, mx_soff, kInter / 32, xh, (hi ? win[1] : win[0]));
+    } else if (mine_mx) {  // formats differ between the halves
+      MxBatch<16> bm;
+      mx_load<16>(bm, src, mx_woff, mx_soff, 0);
+      acc = mx_row_pair<16>(0.0f, bm, src, mx_woff, mx_soff, kInter / 32, xh, (hi ? win[1] : win[0]));
+    } else {
+      acc = fp8_row_pair(0.0f, src, uint32_t(f8.w2) + row * kInter + 16u * h,
+                         uint32_t(f8.s2) + (row / 128) * (kInter / 128), 0, kInter / 32, xh);
+    }
+    if (h == 0 && (!hi || has_b)) part[slot][r] = acc;
+  }
+  __syncthreads();
+  if (wave == 0) phase2_accumulate<kP2ExactRows>(tab, t, np, part, blockIdx.x * kP2ExactRows, Y);
+}
+
+// Phase 2 FAST: wavefront j computes kP2FastRows w2 rows of the token's j-th
+// pair.
+constexpr int kP2FastWaves = kTopK + 1;
+
+__global__ __launch_bounds__(64 * kP2FastWaves) void k_phase2_fast(const PairTable *__restrict__ tab,
+                                                                   const float *__restrict__ H,
+                                                                   float *__restrict__ Y, PageOffsets mx,
+                                                                   PageOffsets f8) {
+  constexpr int NSEG = kInter / 2048;
+  constexpr int R = kP2FastRows;
+  __shared__ float part[kP2FastWaves][R];
+  const uint32_t t = blockIdx.y;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const uint32_t np = tab->token_npairs[t];
+  const uint32_t row0 = blockIdx.x * R;
+  if (wave < np) {
+    const uint32_t p = tab->token_pairs[t][wave];
+    XReg<NSEG> xr;
+    load_x_mx<NSEG>(xr, H + size_t(p) * kInter, kInter);
+    const uint32_t fmt = tab->fmt[p];
+    const Rsrc r = make_rsrc(reinterpret_cast<const uint8_t *>(tab->page[p]), page_bytes(fmt));
+    float mine = 0.0f;
+    if (fmt == S14_PAGE_MXFP4) {
+      MxRowFrag f[R][NSEG];
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const uint32_t row = row0 + i;
+        load_mx_row_frag<NSEG>(f[i], r, uint32_t(mx.w2) + row * (kInter / 2), r,
+                               uint32_t(mx.s2) + row * (kInter / 32), kInter);
+      }
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const float v = wave_sum_dpp(mx_row_fast_partial<NSEG>(f[i], xr));
+        if (lane == uint32_t(i)) mine = v;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const uint32_t row = row0 + i;
+        const float v = wave_sum_dpp(fp8_row_fast_partial<NSEG>(r, uint32_t(f8.w2) + row * kInter,
+                                                                 uint32_t(f8.s2) + (row / 128) * (kInter / 128), xr));
+        if (lane == uint32_t(i)) mine = v;
+      }
+    }
+    if (lane < uint32_t(R)) part[wave][lane] = mine;
+  }
+  __syncthreads();
+  if (wave == 0) phase2_accumulate<kP2FastRows>(tab, t, np, part, row0, Y);
 }
 
 inline unsigned blocks_for(size_t n, unsigned threads) { return unsigned((n + threads - 1) / threads); }
@@ -1022,7 +1336,7 @@ hipError_t launch_mxfp4_matvec(hipStream_t s, const s14_mxfp4_dispatch &d) {
     else
       k_mxfp4_matvec_fast<4, 4><<<grid, 256, 0, s>>>(N, K, d.x, d.weight, d.scale, d.y);
   } else {
-    k_mxfp4_matvec_exact<<<blocks_for(N, 64), 64, 0, s>>>(N, K, d.x, d.weight, d.scale, d.y);
+    k_mxfp4_matvec_exact<<<blocks_for(N, 32), 64, 0, s>>>(N, K, d.x, d.weight, d.scale, d.y);
   }
   return hipGetLastError();
 }
@@ -1030,8 +1344,7 @@ hipError_t launch_mxfp4_matvec(hipStream_t s, const s14_mxfp4_dispatch &d) {
 hipError_t launch_fp8_matvec(hipStream_t s, const s14_fp8_dispatch &d) {
   const uint32_t N = d.shape.n, K = d.shape.k;
   const int xb = d.x_dtype == S14_X_BF16, sf = d.scale_dtype == S14_SCALE_F32;
-  const bool k16 = (K % 16) == 0;
-  if (d.mode == S14_MODE_FAST && k16 && K <= 8192) {
+  if (d.mode == S14_MODE_FAST && K % 16 == 0 && K <= 8192) {
     const unsigned grid = blocks_for(N, 4);
     if (K <= 1024)
       k_fp8_matvec_fast<1><<<grid, 256, 0, s>>>(N, K, d.x, xb, d.weight, d.scale, sf, d.y);
@@ -1041,10 +1354,10 @@ hipError_t launch_fp8_matvec(hipStream_t s, const s14_fp8_dispatch &d) {
       k_fp8_matvec_fast<4><<<grid, 256, 0, s>>>(N, K, d.x, xb, d.weight, d.scale, sf, d.y);
     else
       k_fp8_matvec_fast<8><<<grid, 256, 0, s>>>(N, K, d.x, xb, d.weight, d.scale, sf, d.y);
-  } else if (k16) {
-    k_fp8_matvec_exact<true><<<blocks_for(N, 64), 64, 0, s>>>(N, K, d.x, xb, d.weight, d.scale, sf, d.y);
+  } else if (K % 32 == 0) {
+    k_fp8_matvec_exact<true><<<blocks_for(N, 32), 64, 0, s>>>(N, K, d.x, xb, d.weight, d.scale, sf, d.y);
   } else {
-    k_fp8_matvec_exact<false><<<blocks_for(N, 64), 64, 0, s>>>(N, K, d.x, xb, d.weight, d.scale, sf, d.y);
+    k_fp8_matvec_exact<false><<<blocks_for(N, 32), 64, 0, s>>>(N, K, d.x, xb, d.weight, d.scale, sf, d.y);
   }
   return hipGetLastError();
 }
@@ -1088,39 +1401,44 @@ hipError_t launch_fill_mxfp4_page(hipStream_t s, uint8_t *page, uint64_t seed, u
   return hipGetLastError();
 }
 
-hipError_t launch_plan_from_host(hipStream_t s, const Workspace &ws, const PairTable &plan) {
-  k_plan_from_host<<<1, 256, 0, s>>>(plan, ws.table);
+hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const RouterArgs &r, uint32_t tokens,
+                                const float *x) {
+  k_router_scores<<<dim3((r.n_experts + 3) / 4, tokens), 256, 0, s>>>(r, x, ws.scores, ws.biased);
   return hipGetLastError();
 }
 
-hipError_t launch_router_plan(hipStream_t s, const Workspace &ws, const RouterArgs &r, uint32_t tokens,
-                              const float *x, const uint64_t *expert_pages, const uint8_t *shared_page,
-                              int shared_fmt, uint16_t *ids_out, float *weights_out, int build_plan) {
-  dim3 grid((r.n_experts + 3) / 4, tokens);
-  k_router_plan<<<grid, 256, 0, s>>>(r, tokens, x, ws, expert_pages, shared_page, shared_fmt, ids_out,
-                                     weights_out, build_plan);
+hipError_t launch_plan(hipStream_t s, const Workspace &ws, const RouteSpec &rs) {
+  k_plan<<<1, 64 * kMaxTokens, 0, s>>>(rs, ws);
   return hipGetLastError();
 }
 
-hipError_t launch_layer_phases(hipStream_t s, const Workspace &ws, uint32_t n_pairs, uint32_t tokens,
-                               const PageOffsets &mx, const PageOffsets &fp8, const float *x, float *y,
-                               int mode) {
-  (void)tokens;
-  const uint32_t mx_bytes = uint32_t(S14_EXPERT_PAGE_BYTES);
-  const uint32_t f8_bytes = uint32_t(S14_SHARED_EXPERT_PAGE_BYTES);
+hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *host_plan, uint32_t n_pairs,
+                         const PageOffsets &mx, const PageOffsets &fp8, const float *x, int mode) {
+  PairTable plan{};
+  if (host_plan) plan = *host_plan;
   if (mode == S14_MODE_FAST) {
-    k_phase1_fast<<<dim3(kInter / kP1FastRows, n_pairs), 256, 0, s>>>(ws.table, x, ws.h, mx, fp8, mx_bytes,
-                                                                      f8_bytes);
-    k_phase2_fast<<<dim3(kHidden / kP2FastRows, n_pairs), 256, 0, s>>>(ws.table, ws.h, ws.down, y,
-                                                                       ws.counters, mx, fp8, mx_bytes,
-                                                                       f8_bytes);
+    const dim3 grid(kInter / kP1FastRows, n_pairs);
+    if (host_plan)
+      k_phase1_fast<true><<<grid, 256, 0, s>>>(plan, ws, x, mx, fp8);
+    else
+      k_phase1_fast<false><<<grid, 256, 0, s>>>(plan, ws, x, mx, fp8);
   } else {
-    k_phase1_exact<<<dim3(kInter / kP1ExactRows, n_pairs), 64, 0, s>>>(ws.table, x, ws.h, mx, fp8, mx_bytes,
-                                                                       f8_bytes);
-    k_phase2_exact<<<dim3(kHidden / kP2ExactRows, n_pairs), 64, 0, s>>>(ws.table, ws.h, ws.down, y,
-                                                                        ws.counters, mx, fp8, mx_bytes,
-                                                                        f8_bytes);
+    const dim3 grid(kInter / kP1ExactRows, n_pairs);
+    if (host_plan)
+      k_phase1_exact<true><<<grid, 64, 0, s>>>(plan, ws, x, mx, fp8);
+    else
+      k_phase1_exact<false><<<grid, 64, 0, s>>>(plan, ws, x, mx, fp8);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_phase2(hipStream_t s, const Workspace &ws, uint32_t tokens, const PageOffsets &mx,
+                         const PageOffsets &fp8, float *y, int mode) {
+  if (mode == S14_MODE_FAST)
+    k_phase2_fast<<<dim3(kHidden / kP2FastRows, tokens), 64 * kP2FastWaves, 0, s>>>(ws.table, ws.h, y, mx, fp8);
+  else
+    k_phase2_exact<<<dim3(kHidden / kP2ExactRows, tokens), 64 * kP2ExactWaves, 0, s>>>(ws.table, ws.h, y, mx,
+                                                                                       fp8);
   return hipGetLastError();
 }
 

@@ -17,17 +17,18 @@ constexpr int kHidden = 4096;
 constexpr int kInter = 2048;
 constexpr int kMaxExperts = 256;
 
-// Exact-mode tiles: phase 1 = 32 rows of w1 + the same 32 rows of w3 per
-// wavefront; phase 2 = 64 rows of w2 per wavefront.
-constexpr int kP1ExactRows = 32;
-constexpr int kP2ExactRows = 64;
-// Fast-mode tiles.
+// Exact-mode tiles (one row per lane pair): phase 1 = 16 rows of w1 + the
+// same 16 rows of w3 per wavefront; phase 2 = 16 rows of w2 for each of the
+// token's pairs, two pairs per wavefront.
+constexpr int kP1ExactRows = 16;
+constexpr int kP2ExactRows = 16;
+constexpr int kP2ExactWaves = 4;
+// Fast-mode tiles: phase 1 = 4 wavefronts x 4 rows of w1 and w3; phase 2 =
+// 16 rows of w2 per wavefront (one wavefront per pair of the token).
 constexpr int kP1FastRowsPerWave = 4;
-constexpr int kP2FastRowsPerWave = 8;
 constexpr int kFastWaves = 4;
-constexpr int kP1FastRows = kP1FastRowsPerWave * kFastWaves;  // rows per block
-constexpr int kP2FastRows = kP2FastRowsPerWave * kFastWaves;
-constexpr int kMaxTiles = kHidden / 32;  // upper bound on phase-2 tiles of any mode
+constexpr int kP1FastRows = kP1FastRowsPerWave * kFastWaves;
+constexpr int kP2FastRows = 16;
 
 // One (token, expert) unit of work of a layer or block launch.  Routed pairs
 // come first, sorted by expert id so that all tokens of one expert page are
@@ -50,20 +51,11 @@ struct PairTable {
 // Device workspace of a context (one allocation, carved by s14_api.cpp).
 struct Workspace {
   PairTable *table;
-  float *h;           // [kMaxPairs][kInter]
-  float *down;        // [kMaxPairs][kHidden]
-  float *scores;      // [kMaxTokens][kMaxExperts]
-  float *biased;      // [kMaxTokens][kMaxExperts]
-  uint16_t *ids;      // [kMaxTokens][kTopK]
-  float *weights;     // [kMaxTokens][kTopK]
-  uint32_t *counters; // self-resetting completion counters (zero at rest)
+  float *h;       // [kMaxPairs][kInter]
+  float *scores;  // [kMaxTokens][kMaxExperts]
+  float *biased;  // [kMaxTokens][kMaxExperts]
   size_t bytes;
 };
-// counters layout: [0, kMaxTokens) router per token; [kMaxTokens] plan;
-// [kCntAcc, kCntAcc + kMaxTokens*kMaxTiles) accumulate per (token, tile).
-constexpr int kCntPlan = kMaxTokens;
-constexpr int kCntAcc = 16;
-constexpr int kNumCounters = kCntAcc + kMaxTokens * kMaxTiles;
 
 struct PageOffsets {
   uint64_t w1, s1, w3, s3, w2, s2;
@@ -76,6 +68,17 @@ struct RouterArgs {
   uint32_t topk;
   int score_fn;
   float route_scale;
+};
+
+// Where a device-routed launch finds its pages and reports its routes.
+struct RouteSpec {
+  RouterArgs r;
+  uint32_t tokens;
+  int shared_fmt;
+  const uint64_t *expert_pages;
+  const uint8_t *shared_page;
+  uint16_t *ids_out;
+  float *weights_out;
 };
 
 // --- standalone dispatches (bind/cmd API) ---
@@ -92,17 +95,22 @@ hipError_t launch_fill_mxfp4_page(hipStream_t s, uint8_t *page, uint64_t seed, u
                                   uint32_t expert, uint32_t hidden, uint32_t inter, int lo, int hi,
                                   const PageOffsets &off);
 
-// --- fused layer / block path ---
-// Writes a PairTable for a host-known route (expert chain, route-given layer).
-hipError_t launch_plan_from_host(hipStream_t s, const Workspace &ws, const PairTable &plan);
-// Router for `tokens` tokens; the last block of each token selects the top-k,
-// and the last token to finish builds the PairTable (expert-major).
-hipError_t launch_router_plan(hipStream_t s, const Workspace &ws, const RouterArgs &r,
-                              uint32_t tokens, const float *x, const uint64_t *expert_pages,
-                              const uint8_t *shared_page, int shared_fmt, uint16_t *ids_out,
-                              float *weights_out, int build_plan);
-hipError_t launch_layer_phases(hipStream_t s, const Workspace &ws, uint32_t n_pairs,
-                               uint32_t tokens, const PageOffsets &mx, const PageOffsets &fp8,
-                               const float *x, float *y, int mode);
+// --- fused layer / block path: router -> plan -> phase 1 -> phase 2 ---
+// Scores and biased scores of every (token, expert) into ws.scores/biased.
+hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const RouterArgs &r,
+                                uint32_t tokens, const float *x);
+// Top-k and weights of every token (after launch_router_scores) to
+// rs.ids_out/weights_out when given; with rs.expert_pages also the pair
+// table in ws.table.
+hipError_t launch_plan(hipStream_t s, const Workspace &ws, const RouteSpec &rs);
+// w1/w3 + SwiGLU of every pair.  host_plan != NULL: the pairs are given and
+// workgroup (0,0) publishes them for phase 2; otherwise they are read from
+// the table launch_plan wrote.
+hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *host_plan,
+                         uint32_t n_pairs, const PageOffsets &mx, const PageOffsets &fp8,
+                         const float *x, int mode);
+// w2 of every pair and the per-token accumulation into y [tokens][hidden].
+hipError_t launch_phase2(hipStream_t s, const Workspace &ws, uint32_t tokens,
+                         const PageOffsets &mx, const PageOffsets &fp8, float *y, int mode);
 
 }  // namespace s14

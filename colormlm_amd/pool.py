@@ -118,6 +118,15 @@ class VramPool:
         p = lib().s14_pool_slot_ptr(self._h, slot)
         return int(p) if p else None
 
+    def slot_tensor(self, slot: int):
+        """A torch uint8 view of one slot of the device arena (no copy)."""
+        import torch
+
+        ptr = self.slot_ptr(slot)
+        if ptr is None:
+            raise S14Error(N.S14_ERR_INVALID, "pool has no device arena")
+        return torch.as_tensor(_DeviceBytes(ptr, self.slot_bytes(), self), device="cuda")
+
     def lookup(self, key: ExpertKey) -> Optional[int]:
         slot = C.c_uint32()
         return int(slot.value) if lib().s14_pool_lookup(self._h, key.c(), C.byref(slot)) else None
@@ -174,6 +183,14 @@ class VramPool:
         r = reservation.c()
         check(lib().s14_pool_upload(ctx.handle, self._h, C.byref(r), buf.ctypes.data, buf.nbytes, C.byref(fence)))
         return Fence(fence, keepalive=buf)
+
+
+class _DeviceBytes:
+    """__cuda_array_interface__ of a byte range of device memory."""
+
+    def __init__(self, ptr: int, nbytes: int, owner):
+        self._owner = owner
+        self.__cuda_array_interface__ = {"shape": (nbytes,), "typestr": "|u1", "data": (ptr, False), "version": 3}
 
 
 class Fence:

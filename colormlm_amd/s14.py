@@ -87,6 +87,16 @@ class Context:
     def synchronize(self) -> None:
         check(lib().s14_ctx_synchronize(self._h))
 
+    def enable_stage_timing(self, enable: bool = True) -> None:
+        check(lib().s14_ctx_enable_stage_timing(self._h, 1 if enable else 0))
+
+    def stage_times(self):
+        """ms of {plan/router, phase 1, phase 2} of the last fused launch."""
+        ms = (C.c_float * 3)()
+        n = C.c_uint32()
+        check(lib().s14_ctx_stage_times(self._h, ms, 3, C.byref(n)))
+        return [float(ms[i]) for i in range(3)]
+
     def destroy(self) -> None:
         if self._h:
             lib().s14_ctx_destroy(self._h)

@@ -18,7 +18,9 @@
  *     bind_* (s14_vulkan.rs:206-334) and fill a plain dispatch record;
  *     s14_cmd_* only enqueue the kernel on the given stream (the reference's
  *     cmd_* "record only the dispatch", s14_vulkan.rs:336-416);
- *   - a stream argument of NULL means the context's compute stream;
+ *   - stream arguments are hipStream_t values passed as void*; NULL is the
+ *     device's null (default) stream, as everywhere in HIP; the context's own
+ *     streams come from s14_ctx_compute_stream / s14_ctx_copy_stream;
  *   - no internal locking: a pool or page set is used by one thread at a time
  *     (the reference's &mut discipline); contexts may be used from several
  *     threads only with distinct streams and workspaces.
@@ -92,6 +94,14 @@ void s14_ctx_destroy(s14_ctx *ctx);
 void *s14_ctx_compute_stream(s14_ctx *ctx);
 void *s14_ctx_copy_stream(s14_ctx *ctx);
 int s14_ctx_synchronize(s14_ctx *ctx);
+/* Stage timestamps (the role of the reference's Vulkan timestamp queries,
+ * s14_vulkan_numeric.rs:1088-1101): when enabled, each fused entry point
+ * (chain, layer, block) records a hipEvent before its plan/router kernel,
+ * between its two expert phases and after the last.  s14_ctx_stage_times
+ * waits for the last such launch and returns the elapsed ms of its three
+ * stages {plan/router, phase 1 (w1, w3, SwiGLU), phase 2 (w2, mix)}. */
+int s14_ctx_enable_stage_timing(s14_ctx *ctx, int enable);
+int s14_ctx_stage_times(s14_ctx *ctx, float *ms, uint32_t cap, uint32_t *n_stages);
 
 /* A device buffer view: the GpuBuffer of the reference (buffer.rs:21-70)
  * reduced to what the kernels need.  `bytes` is the capacity checked by the

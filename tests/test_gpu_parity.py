@@ -388,7 +388,9 @@ def test_pool_upload_publish_compute_release(ctx, oracle, bank):
     ptrs = [routed.slot_ptr(s) for s in slots]
     x = synth.token(seed=5)
     y = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
-    s14.moe_layer(ctx, ptrs, np.array(w, np.float32).tolist(), shared.slot_ptr(lease.shared_binding().slot), dev(x), y,
+    xd = dev(x)
+    torch.cuda.synchronize()  # torch's copies are on its stream; the layer runs on the context's
+    s14.moe_layer(ctx, ptrs, np.array(w, np.float32).tolist(), shared.slot_ptr(lease.shared_binding().slot), xd, y,
                   mode=s14.EXACT, stream=ctx.compute_stream)
     done = Fence.record(ctx, ctx.compute_stream)
     done.wait()
