@@ -381,11 +381,8 @@ extern "C" int s14_expert_chain(s14_ctx *ctx, void *stream, const uint8_t *page,
   t.n_tokens = 1;
   t.n_distinct = 1;
   t.chain = 1;
-  t.page[0] = reinterpret_cast<uint64_t>(page);
-  t.fmt[0] = S14_PAGE_MXFP4;
-  t.weight[0] = route_w;
-  t.token_pairs[0][0] = 0;
-  t.token_npairs[0] = 1;
+  s14::plan_pair(t, 0, page, S14_PAGE_MXFP4, 0, 0, route_w, false);
+  t.npairs[0] = 1;
   hipStream_t st = pick(ctx, stream);
   if (int rc = stage_mark(ctx, st, 0)) return rc;
   return run_layer(ctx, st, &t, 1, 1, x, y, mode);
@@ -407,24 +404,17 @@ extern "C" int s14_moe_layer(s14_ctx *ctx, void *stream, uint32_t topk, const ui
     const float w = route_weights[i];
     if (!std::isfinite(w) || w < 0.0f)
       return fail(S14_ERR_INVALID, "S14 MoE accumulate requires finite non-negative weight (route %u)", i);
-    t.page[i] = reinterpret_cast<uint64_t>(routed_pages[i]);
-    t.fmt[i] = S14_PAGE_MXFP4;
-    t.weight[i] = w;
-    t.token_pairs[0][i] = i;
+    s14::plan_pair(t, i, routed_pages[i], S14_PAGE_MXFP4, 0, i, w, false);
   }
   uint32_t n = topk;
   if (shared_page) {
-    t.page[n] = reinterpret_cast<uint64_t>(shared_page);
-    t.fmt[n] = uint32_t(shared_format);
-    t.weight[n] = 1.0f;
-    t.is_shared[n] = 1;
-    t.token_pairs[0][n] = n;
+    s14::plan_pair(t, n, shared_page, uint32_t(shared_format), 0, n, 1.0f, true);
     ++n;
   }
   t.n_pairs = n;
   t.n_tokens = 1;
   t.n_distinct = topk;
-  t.token_npairs[0] = n;
+  t.npairs[0] = n;
   hipStream_t st = pick(ctx, stream);
   if (int rc = stage_mark(ctx, st, 0)) return rc;
   return run_layer(ctx, st, &t, n, 1, x, y, mode);

@@ -152,22 +152,34 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// Arg-max over the wavefront of (v, i) with ties to the lower index; i < 0
-// marks an empty candidate.  The order is total on non-NaN values, so the
-// DPP tree's shape does not matter.  Result returned to every lane.
-__device__ __forceinline__ void argmax_step(float &v, int &i, float ov, int oi) {
-  const bool take = oi >= 0 && (i < 0 || ov > v || (ov == v && oi < i));
-  v = take ? ov : v;
-  i = take ? oi : i;
+// Wavefront max / min of a u32 (DPP row steps, then lane 63), returned to
+// every lane.  Lanes without a DPP source contribute the identity.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, uint32_t(dpp_i<0xb1>(0, int(v))));
+  v = max(v, uint32_t(dpp_i<0x4e>(0, int(v))));
+  v = max(v, uint32_t(dpp_i<0x114>(0, int(v))));
+  v = max(v, uint32_t(dpp_i<0x118>(0, int(v))));
+  v = max(v, uint32_t(dpp_i<0x142, 0xa>(0, int(v))));
+  v = max(v, uint32_t(dpp_i<0x143, 0xc>(0, int(v))));
+  return uint32_t(__builtin_amdgcn_readlane(int(v), 63));
 }
-__device__ __forceinline__ int wave_argmax(float v, int i) {
-  argmax_step(v, i, dpp_f<0xb1>(v, v), dpp_i<0xb1>(i, i));
-  argmax_step(v, i, dpp_f<0x4e>(v, v), dpp_i<0x4e>(i, i));
-  argmax_step(v, i, dpp_f<0x114>(v, v), dpp_i<0x114>(i, i));
-  argmax_step(v, i, dpp_f<0x118>(v, v), dpp_i<0x118>(i, i));
-  argmax_step(v, i, dpp_f<0x142, 0xa>(v, v), dpp_i<0x142, 0xa>(i, i));
-  argmax_step(v, i, dpp_f<0x143, 0xc>(v, v), dpp_i<0x143, 0xc>(i, i));
-  return __builtin_amdgcn_readlane(i, 63);
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, uint32_t(dpp_i<0xb1>(-1, int(v))));
+  v = min(v, uint32_t(dpp_i<0x4e>(-1, int(v))));
+  v = min(v, uint32_t(dpp_i<0x114>(-1, int(v))));
+  v = min(v, uint32_t(dpp_i<0x118>(-1, int(v))));
+  v = min(v, uint32_t(dpp_i<0x142, 0xa>(-1, int(v))));
+  v = min(v, uint32_t(dpp_i<0x143, 0xc>(-1, int(v))));
+  return uint32_t(__builtin_amdgcn_readlane(int(v), 63));
+}
+
+// Order-preserving key of a score for the top-k selection: larger float ->
+// larger key; -0 and +0 share a key (they compare equal); NaN gets key 0,
+// below every number (a NaN score is never preferred).
+__device__ __forceinline__ uint32_t score_key(float f) {
+  if (f != f) return 0u;
+  const uint32_t u = __float_as_uint(f + 0.0f);  // -0 + 0 = +0
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
 // Biased-exponent range of the nonzero finite values seen by this lane.
@@ -343,14 +355,36 @@ __device__ __forceinline__ uint32_t batch_code(const MxBatch<PF> &b, int i) {
   return (b.c[i >> 2] >> (8 * (i & 3))) & 255u;
 }
 
+// Single loads through either source form (the literal path re-reads its
+// codes rather than index the register batch dynamically).
+__device__ __forceinline__ uint2 src_ld8(const Src1 &s, uint32_t off) { return ld8(s.w, off); }
+__device__ __forceinline__ uint32_t src_ld1(const Src1 &s, uint32_t off) { return ld1(s.s, off); }
+__device__ __forceinline__ uint2 src_ld8(const Src2 &s, uint32_t off) {
+  uint2 v;
+  if (s.hi)
+    v = ld8(s.b, off);
+  else
+    v = ld8(s.a, off);
+  return v;
+}
+__device__ __forceinline__ uint32_t src_ld1(const Src2 &s, uint32_t off) {
+  uint32_t v;
+  if (s.hi)
+    v = ld1(s.b, off);
+  else
+    v = ld1(s.a, off);
+  return v;
+}
+
 // One batch: if every lane's codes are inside its window the batch runs the
 // scaled decode as straight-line code, software-pipelined: group i+1's x
 // reads and products are issued ahead of group i's add chain, so LDS latency
 // and the chain's DPP read-after-write waits overlap independent work.
-// Otherwise the batch takes the literal decode.
-template <int PF>
-__device__ __forceinline__ float mx_consume(float acc, const MxBatch<PF> &b, const float *__restrict__ xh, int g0,
-                                            CodeWindow win) {
+// Otherwise the batch takes the literal decode, group by group, re-reading
+// its codes (compact code for a path real scale codes do not take).
+template <int PF, class Src>
+__device__ __forceinline__ float mx_consume(float acc, const MxBatch<PF> &b, const Src &src, uint32_t woff,
+                                            uint32_t soff, const float *__restrict__ xh, int g0, CodeWindow win) {
   bool ok = true;
 #pragma unroll
   for (int j = 0; j < PF / 4; ++j) ok = ok && codes_in(b.c[j], win);
@@ -371,12 +405,12 @@ __device__ __forceinline__ float mx_consume(float acc, const MxBatch<PF> &b, con
       acc = pair_chain16(acc, q);
     }
   } else {
-    float p[16];
-    X16 x;
-#pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      load_x16(x, xh + (g0 + i) * 32);
-      mx_products_literal(p, b.w[i], batch_code(b, i), x);
+#pragma unroll 1
+    for (int g = g0; g < g0 + PF; ++g) {
+      float p[16];
+      X16 x;
+      load_x16(x, xh + g * 32);
+      mx_products_literal(p, src_ld8(src, woff + 16u * uint32_t(g)), src_ld1(src, soff + uint32_t(g)), x);
       acc = pair_chain16(acc, p);
     }
   }
@@ -387,7 +421,8 @@ __device__ __forceinline__ float mx_consume(float acc, const MxBatch<PF> &b, con
 // 16 * (lane & 1)); result in the even lane.  `ba` arrives holding groups
 // [0, PF) (loaded by the caller with mx_load, ahead of its own set-up work);
 // two register batches of PF groups then ping-pong so that batch b+1 is in
-// flight while batch b is consumed.
+// flight while batch b is consumed.  (The loop prefetches one batch past
+// the row's end: neighbouring bytes or zeros, never consumed.)
 template <int PF, class Src>
 __device__ __forceinline__ float mx_row_pair(float acc, MxBatch<PF> &ba, const Src &src, uint32_t woff,
                                              uint32_t soff, int G, const float *__restrict__ xh, CodeWindow win) {
@@ -396,11 +431,31 @@ __device__ __forceinline__ float mx_row_pair(float acc, MxBatch<PF> &ba, const S
   int g0 = 0;
   for (; g0 + 2 * PF <= G; g0 += 2 * PF) {
     mx_load<PF>(bb, src, woff, soff, g0 + PF);
-    acc = mx_consume<PF>(acc, ba, xh, g0, win);
+    acc = mx_consume<PF>(acc, ba, src, woff, soff, xh, g0, win);
     mx_load<PF>(ba, src, woff, soff, g0 + 2 * PF);
-    acc = mx_consume<PF>(acc, bb, xh, g0 + PF, win);
+    acc = mx_consume<PF>(acc, bb, src, woff, soff, xh, g0 + PF, win);
   }
-  if (g0 < G) acc = mx_consume<PF>(acc, ba, xh, g0, win);  // one batch left
+  if (g0 < G) acc = mx_consume<PF>(acc, ba, src, woff, soff, xh, g0, win);  // one batch left
+  return acc;
+}
+
+// The same for a compile-time group count G (G % (2 PF) == 0), with the
+// last two batches peeled so that no load reaches past the row.
+template <int PF, int G, class Src>
+__device__ __forceinline__ float mx_row_pair_fixed(float acc, MxBatch<PF> &ba, const Src &src, uint32_t woff,
+                                                   uint32_t soff, const float *__restrict__ xh, CodeWindow win) {
+  static_assert(PF % 4 == 0 && G % (2 * PF) == 0, "whole batch pairs");
+  MxBatch<PF> bb;
+#pragma unroll 1
+  for (int g0 = 0; g0 < G - 2 * PF; g0 += 2 * PF) {
+    mx_load<PF>(bb, src, woff, soff, g0 + PF);
+    acc = mx_consume<PF>(acc, ba, src, woff, soff, xh, g0, win);
+    mx_load<PF>(ba, src, woff, soff, g0 + 2 * PF);
+    acc = mx_consume<PF>(acc, bb, src, woff, soff, xh, g0 + PF, win);
+  }
+  mx_load<PF>(bb, src, woff, soff, G - PF);
+  acc = mx_consume<PF>(acc, ba, src, woff, soff, xh, G - 2 * PF, win);
+  acc = mx_consume<PF>(acc, bb, src, woff, soff, xh, G - PF, win);
   return acc;
 }
 
@@ -497,6 +552,7 @@ __device__ __forceinline__ float fp8_row_pair(float acc, const Src &src, uint32_
 // ---------------------------------------------------------------------------
 
 constexpr int kExactChunk = 4096;
+constexpr int kPF = 16;  // groups per register batch in the fused exact kernels
 
 __global__ __launch_bounds__(64) void k_mxfp4_matvec_exact(uint32_t N, uint32_t K,
                                                            const float *__restrict__ x,
@@ -964,18 +1020,20 @@ __global__ __launch_bounds__(64 * kMaxTokens) void k_plan(RouteSpec rs, Workspac
   const RouterArgs &r = rs.r;
   const uint32_t k = r.topk;
   if (t < rs.tokens) {
-    // biased and unbiased scores and page addresses of experts lane + 64 j,
-    // all loaded up front (no memory access depends on a selection)
-    float v[4], sv[4];
+    // keys of the biased scores, unbiased scores and page addresses of
+    // experts lane + 64 j, all loaded up front (no memory access depends on
+    // a selection); key 0 marks an absent or already chosen expert, and a
+    // real score's key is >= 1 unless it is NaN
+    uint32_t kv[4];
+    float sv[4];
     uint64_t pv[4];
-    bool taken[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t ee = lane + 64u * j;
-      taken[j] = ee >= r.n_experts;
-      v[j] = taken[j] ? 0.0f : ws.biased[t * kMaxExperts + ee];
-      sv[j] = taken[j] ? 0.0f : ws.scores[t * kMaxExperts + ee];
-      pv[j] = (taken[j] || !rs.expert_pages) ? 0ull : rs.expert_pages[ee];
+      const bool absent = ee >= r.n_experts;
+      kv[j] = absent ? 0u : max(score_key(ws.biased[t * kMaxExperts + ee]), 1u);
+      sv[j] = absent ? 0.0f : ws.scores[t * kMaxExperts + ee];
+      pv[j] = (absent || !rs.expert_pages) ? 0ull : rs.expert_pages[ee];
     }
     float sum = 0.0f, my_s = 0.0f;
     uint32_t my_id = 0;
@@ -983,21 +1041,18 @@ __global__ __launch_bounds__(64 * kMaxTokens) void k_plan(RouteSpec rs, Workspac
 #pragma unroll
     for (uint32_t i = 0; i < uint32_t(kTopK); ++i) {
       if (i >= k) break;
-      float bv = 0.0f;
-      int bi = -1;
+      // max key over the wavefront, then the lowest expert index holding it
+      // (the oracle's strict '>' scan keeps the first of equal scores)
+      const uint32_t top = wave_max_u32(max(max(kv[0], kv[1]), max(kv[2], kv[3])));
+      uint32_t idx = 0xffffffffu;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (!taken[j] && (bi < 0 || v[j] > bv)) {
-          bv = v[j];
-          bi = int(lane + 64u * j);
-        }
-      }
-      const int best = wave_argmax(bv, bi);
+      for (int j = 3; j >= 0; --j) idx = kv[j] == top ? lane + 64u * j : idx;
+      const int best = int(wave_min_u32(idx));
       float cand = sv[0];
       uint64_t cpg = pv[0];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if (int(lane + 64u * j) == best) taken[j] = true;
+        if (int(lane + 64u * j) == best) kv[j] = 0u;
         if ((best >> 6) == j) {
           cand = sv[j];
           cpg = pv[j];
@@ -1039,23 +1094,29 @@ __global__ __launch_bounds__(64 * kMaxTokens) void k_plan(RouteSpec rs, Workspac
   }
   PairTable *tab = ws.table;
   if (mine) {
-    tab->page[rank] = pgs[mt][mr];
+    const uint64_t pg = pgs[mt][mr];
+    tab->page[rank] = pg;
     tab->fmt[rank] = S14_PAGE_MXFP4;
     tab->token[rank] = mt;
-    tab->weight[rank] = wts[mt][mr];
-    tab->is_shared[rank] = 0u;
-    tab->token_pairs[mt][mr] = rank;
+    tab->slot_pair[mt][mr] = rank;
+    tab->slot_page[mt][mr] = pg;
+    tab->slot_fmt[mt][mr] = S14_PAGE_MXFP4;
+    tab->slot_weight[mt][mr] = wts[mt][mr];
+    tab->slot_shared[mt][mr] = 0u;
   }
   const uint64_t firsts = __ballot(mine && first);
   if (lane < T) {
     const uint32_t sp = npr + lane;
-    tab->page[sp] = reinterpret_cast<uint64_t>(rs.shared_page);
+    const uint64_t pg = reinterpret_cast<uint64_t>(rs.shared_page);
+    tab->page[sp] = pg;
     tab->fmt[sp] = uint32_t(rs.shared_fmt);
     tab->token[sp] = lane;
-    tab->weight[sp] = 1.0f;
-    tab->is_shared[sp] = 1u;
-    tab->token_pairs[lane][k] = sp;
-    tab->token_npairs[lane] = k + 1;
+    tab->slot_pair[lane][k] = sp;
+    tab->slot_page[lane][k] = pg;
+    tab->slot_fmt[lane][k] = uint32_t(rs.shared_fmt);
+    tab->slot_weight[lane][k] = 1.0f;
+    tab->slot_shared[lane][k] = 1u;
+    tab->npairs[lane] = k + 1;
   }
   if (lane == 0) {
     tab->n_pairs = npr + T;
@@ -1111,11 +1172,11 @@ __global__ __launch_bounds__(64) void k_phase1_exact(PairTable plan, Workspace w
   if (pr.fmt == S14_PAGE_MXFP4) {
     const uint32_t woff = uint32_t(upper ? mx.w3 : mx.w1) + row * (kHidden / 2) + 8u * h;
     const uint32_t soff = uint32_t(upper ? mx.s3 : mx.s1) + row * (kHidden / 32);
-    MxBatch<16> ba;
-    mx_load<16>(ba, src, woff, soff, 0);  // first weights in flight during the x copy
+    MxBatch<kPF> ba;
+    mx_load<kPF>(ba, src, woff, soff, 0);  // first weights in flight during the x copy
     stage_x_wave<kHidden, 1>(dst, srcx, win);
     __syncthreads();
-    acc = mx_row_pair<16>(0.0f, ba, src, woff, soff, kHidden / 32, xs + 16 * h, win[0]);
+    acc = mx_row_pair_fixed<kPF, kHidden / 32>(0.0f, ba, src, woff, soff, xs + 16 * h, win[0]);
   } else {
     const uint32_t woff = uint32_t(upper ? f8.w3 : f8.w1) + row * kHidden + 16u * h;
     const uint32_t soff = uint32_t(upper ? f8.s3 : f8.s1) + (row / 128) * (kHidden / 128);
@@ -1179,61 +1240,80 @@ __global__ __launch_bounds__(256) void k_phase1_fast(PairTable plan, Workspace w
   }
 }
 
+// What every phase-2 workgroup needs about its token, read in one round trip
+// at kernel start: lane j (< kSlots) holds slot j's route weight and shared
+// flag.
+struct SlotInfo {
+  uint32_t np, chain;
+  float w;
+  uint32_t shared;
+};
+__device__ __forceinline__ SlotInfo load_slot_info(const PairTable *__restrict__ tab, uint32_t t) {
+  const uint32_t j = min(threadIdx.x & 63, uint32_t(kSlots - 1));
+  return SlotInfo{tab->npairs[t], tab->chain, tab->slot_weight[t][j], tab->slot_shared[t][j]};
+}
+
 // Phase 2 accumulation of one row tile of token t from part[slot][row]:
 // acc = 0; acc += w * down (routed, route order); acc += down (shared) — or
-// y = w * down for the single-expert chain.
+// y = w * down for the single-expert chain (s14_vulkan_numeric.rs:929-946,
+// :1300).  Called by one whole wavefront.
 template <int ROWS>
-__device__ __forceinline__ void phase2_accumulate(const PairTable *__restrict__ tab, uint32_t t, uint32_t np,
-                                                  const float (*part)[ROWS], uint32_t row0, float *__restrict__ Y) {
-  const uint32_t lane = threadIdx.x;
-  if (lane >= uint32_t(ROWS)) return;
+__device__ __forceinline__ void phase2_accumulate(const SlotInfo &si, const float (*part)[ROWS], uint32_t t,
+                                                  uint32_t row0, float *__restrict__ Y) {
+  const uint32_t lane = threadIdx.x & 63;
+  const bool row_lane = lane < uint32_t(ROWS);
   float acc = 0.0f;
-  if (tab->chain) {
-    acc = __fmul_rn(tab->weight[tab->token_pairs[t][0]], part[0][lane]);
+  if (si.chain) {
+    const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(si.w), 0));
+    acc = __fmul_rn(w, row_lane ? part[0][lane] : 0.0f);
   } else {
-    for (uint32_t j = 0; j < np; ++j) {
-      const uint32_t p = tab->token_pairs[t][j];
-      const float d = part[j][lane];
-      acc = tab->is_shared[p] ? __fadd_rn(acc, d) : __fadd_rn(acc, __fmul_rn(tab->weight[p], d));
+    for (uint32_t j = 0; j < si.np; ++j) {
+      const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(si.w), int(j)));
+      const uint32_t shared = uint32_t(__builtin_amdgcn_readlane(int(si.shared), int(j)));
+      const float d = row_lane ? part[j][lane] : 0.0f;
+      acc = shared ? __fadd_rn(acc, d) : __fadd_rn(acc, __fmul_rn(w, d));
     }
   }
-  Y[size_t(t) * kHidden + row0 + lane] = acc;
+  if (row_lane) Y[size_t(t) * kHidden + row0 + lane] = acc;
 }
 
 // Phase 2 EXACT: one workgroup of kP2ExactWaves wavefronts per (16-row tile,
 // token).  Wavefront w serves the token's pair slots 2w (lanes 0-31) and
 // 2w+1 (lanes 32-63), one row per lane pair, with each slot's h staged in
 // LDS (row stride padded so the two slots' reads fall in different banks).
-constexpr int kP2Slots = kTopK + 1;
 constexpr int kHStride = kInter + 8;
 
 __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairTable *__restrict__ tab,
                                                                      const float *__restrict__ H,
                                                                      float *__restrict__ Y, PageOffsets mx,
                                                                      PageOffsets f8) {
-  __shared__ float hs[kP2Slots][kHStride];
-  __shared__ float part[kP2Slots][kP2ExactRows];
+  __shared__ float hs[kSlots][kHStride];
+  __shared__ float part[kSlots][kP2ExactRows];
   const uint32_t t = blockIdx.y;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const uint32_t np = tab->token_npairs[t];
-  const uint32_t sa = 2 * wave, sb = 2 * wave + 1;
-  const bool has_a = sa < np, has_b = sb < np;
+  // slot records of both of this wavefront's slots, read unconditionally (in
+  // one round trip with the token's pair count); b falls back to a when absent
+  const uint32_t sa = 2 * wave, sb = min(2 * wave + 1, uint32_t(kSlots - 1));
+  const SlotInfo si = load_slot_info(tab, t);
+  const uint32_t qa = tab->slot_pair[t][sa], qb = tab->slot_pair[t][sb];
+  const uint32_t ga = tab->slot_fmt[t][sa], gb = tab->slot_fmt[t][sb];
+  const uint64_t ua = tab->slot_page[t][sa], ub = tab->slot_page[t][sb];
+  const uint32_t np = si.np;
+  const bool has_a = sa < np, has_b = 2 * wave + 1 < np;
+  const uint32_t pa = qa, pb = has_b ? qb : qa;
+  const uint32_t fa = ga, fb = has_b ? gb : ga;
   const bool hi = lane >= 32;
   const uint32_t h = lane & 1u, r = (lane & 31u) >> 1;
   const uint32_t row = blockIdx.x * kP2ExactRows + r;
   const uint32_t slot = (hi && has_b) ? sb : sa;
-  // pair, page and format of both slots (b falls back to a when absent)
-  const uint32_t pa = has_a ? tab->token_pairs[t][sa] : 0u;
-  const uint32_t pb = has_b ? tab->token_pairs[t][sb] : pa;
-  const uint32_t fa = tab->fmt[pa], fb = tab->fmt[pb];
-  const Src2 src{make_rsrc(reinterpret_cast<const uint8_t *>(tab->page[pa]), page_bytes(fa)),
-                 make_rsrc(reinterpret_cast<const uint8_t *>(tab->page[pb]), page_bytes(fb)), hi};
+  const Src2 src{make_rsrc(reinterpret_cast<const uint8_t *>(ua), page_bytes(fa)),
+                 make_rsrc(reinterpret_cast<const uint8_t *>(has_b ? ub : ua), page_bytes(fb)), hi};
   const bool mine_mx = (hi ? fb : fa) == S14_PAGE_MXFP4;
   const uint32_t mx_woff = uint32_t(mx.w2) + row * (kInter / 2) + 8u * h;
   const uint32_t mx_soff = uint32_t(mx.s2) + row * (kInter / 32);
-  MxBatch<16> ba;
+  MxBatch<kPF> ba;
   if (has_a && fa == S14_PAGE_MXFP4 && fb == S14_PAGE_MXFP4)
-    mx_load<16>(ba, src, mx_woff, mx_soff, 0);  // first weights in flight during the h copy
+    mx_load<kPF>(ba, src, mx_woff, mx_soff, 0);  // first weights in flight during the h copy
   CodeWindow win[2] = {{256, 0}, {256, 0}};
   if (has_b) {
     float *const dst[2] = {hs[sa], hs[sb]};
@@ -1251,11 +1331,11 @@ __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairT
     const float *xh = hs[slot] + 16 * h;
     float acc;
     if (fa == S14_PAGE_MXFP4 && fb == S14_PAGE_MXFP4) {
-      acc = mx_row_pair<16>(0.0f, ba, src, mx_woff, mx_soff, kInter / 32, xh, (hi ? win[1] : win[0]));
+      acc = mx_row_pair_fixed<kPF, kInter / 32>(0.0f, ba, src, mx_woff, mx_soff, xh, (hi ? win[1] : win[0]));
     } else if (mine_mx) {  // formats differ between the halves
-      MxBatch<16> bm;
-      mx_load<16>(bm, src, mx_woff, mx_soff, 0);
-      acc = mx_row_pair<16>(0.0f, bm, src, mx_woff, mx_soff, kInter / 32, xh, (hi ? win[1] : win[0]));
+      MxBatch<kPF> bm;
+      mx_load<kPF>(bm, src, mx_woff, mx_soff, 0);
+      acc = mx_row_pair_fixed<kPF, kInter / 32>(0.0f, bm, src, mx_woff, mx_soff, xh, (hi ? win[1] : win[0]));
     } else {
       acc = fp8_row_pair(0.0f, src, uint32_t(f8.w2) + row * kInter + 16u * h,
                          uint32_t(f8.s2) + (row / 128) * (kInter / 128), 0, kInter / 32, xh);
@@ -1263,7 +1343,7 @@ __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairT
     if (h == 0 && (!hi || has_b)) part[slot][r] = acc;
   }
   __syncthreads();
-  if (wave == 0) phase2_accumulate<kP2ExactRows>(tab, t, np, part, blockIdx.x * kP2ExactRows, Y);
+  if (wave == 0) phase2_accumulate<kP2ExactRows>(si, part, t, blockIdx.x * kP2ExactRows, Y);
 }
 
 // Phase 2 FAST: wavefront j computes kP2FastRows w2 rows of the token's j-th
@@ -1279,14 +1359,15 @@ __global__ __launch_bounds__(64 * kP2FastWaves) void k_phase2_fast(const PairTab
   __shared__ float part[kP2FastWaves][R];
   const uint32_t t = blockIdx.y;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const uint32_t np = tab->token_npairs[t];
+  const uint32_t j = min(wave, uint32_t(kSlots - 1));
+  const SlotInfo si = load_slot_info(tab, t);
+  const uint32_t p = tab->slot_pair[t][j], fmt = tab->slot_fmt[t][j];
+  const uint64_t page = tab->slot_page[t][j];
   const uint32_t row0 = blockIdx.x * R;
-  if (wave < np) {
-    const uint32_t p = tab->token_pairs[t][wave];
+  if (wave < si.np) {
     XReg<NSEG> xr;
     load_x_mx<NSEG>(xr, H + size_t(p) * kInter, kInter);
-    const uint32_t fmt = tab->fmt[p];
-    const Rsrc r = make_rsrc(reinterpret_cast<const uint8_t *>(tab->page[p]), page_bytes(fmt));
+    const Rsrc r = make_rsrc(reinterpret_cast<const uint8_t *>(page), page_bytes(fmt));
     float mine = 0.0f;
     if (fmt == S14_PAGE_MXFP4) {
       MxRowFrag f[R][NSEG];
@@ -1313,7 +1394,7 @@ __global__ __launch_bounds__(64 * kP2FastWaves) void k_phase2_fast(const PairTab
     if (lane < uint32_t(R)) part[wave][lane] = mine;
   }
   __syncthreads();
-  if (wave == 0) phase2_accumulate<kP2FastRows>(tab, t, np, part, row0, Y);
+  if (wave == 0) phase2_accumulate<kP2FastRows>(si, part, t, row0, Y);
 }
 
 inline unsigned blocks_for(size_t n, unsigned threads) { return unsigned((n + threads - 1) / threads); }

@@ -30,23 +30,45 @@ constexpr int kFastWaves = 4;
 constexpr int kP1FastRows = kP1FastRowsPerWave * kFastWaves;
 constexpr int kP2FastRows = 16;
 
-// One (token, expert) unit of work of a layer or block launch.  Routed pairs
-// come first, sorted by expert id so that all tokens of one expert page are
-// consecutive in the grid; the shared expert's pairs follow.
+constexpr int kSlots = kTopK + 1;  // pairs of one token: routed + shared
+
+// Work of a layer or block launch.  Phase 1 runs one grid row per
+// (token, expert) pair: routed pairs first, sorted by expert id so that all
+// tokens of one expert page are consecutive in the grid, the shared
+// expert's pairs last.  Phase 2 walks each token's pairs in accumulation
+// order (routed in route order, shared last) through per-token slot records,
+// so that a workgroup finds everything about its token with one round trip.
 struct PairTable {
   uint32_t n_pairs;
   uint32_t n_tokens;
   uint32_t n_distinct;  // distinct routed pages
   uint32_t chain;       // 1: output = weight * down (the single-expert chain)
+  // per pair (phase 1)
   uint64_t page[kMaxPairs];
   uint32_t fmt[kMaxPairs];
   uint32_t token[kMaxPairs];
-  float weight[kMaxPairs];
-  uint32_t is_shared[kMaxPairs];
-  // accumulation order per token: routed pairs in route order, shared last
-  uint32_t token_pairs[kMaxTokens][kTopK + 1];
-  uint32_t token_npairs[kMaxTokens];
+  // per token and slot (phase 2)
+  uint32_t npairs[kMaxTokens];
+  uint32_t slot_pair[kMaxTokens][kSlots];  // pair index: row of the h buffer
+  uint32_t slot_fmt[kMaxTokens][kSlots];
+  uint32_t slot_shared[kMaxTokens][kSlots];
+  float slot_weight[kMaxTokens][kSlots];  // route weight; 1 for the shared expert
+  uint64_t slot_page[kMaxTokens][kSlots];
 };
+
+// Host-built plans (fixed routes): pair p runs `page` for `token`, and is
+// slot j of that token's accumulation.
+inline void plan_pair(PairTable &t, uint32_t p, const void *page, uint32_t fmt, uint32_t token, uint32_t j,
+                      float weight, bool shared) {
+  t.page[p] = reinterpret_cast<uint64_t>(page);
+  t.fmt[p] = fmt;
+  t.token[p] = token;
+  t.slot_pair[token][j] = p;
+  t.slot_page[token][j] = reinterpret_cast<uint64_t>(page);
+  t.slot_fmt[token][j] = fmt;
+  t.slot_weight[token][j] = weight;
+  t.slot_shared[token][j] = shared ? 1u : 0u;
+}
 
 // Device workspace of a context (one allocation, carved by s14_api.cpp).
 struct Workspace {

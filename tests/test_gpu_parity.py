@@ -313,6 +313,34 @@ def test_router_matches_oracle(ctx, oracle, bank):
     np.testing.assert_allclose(host(wts)[0], w_o, rtol=1e-6)
 
 
+def test_router_ties_and_expert_counts(ctx, oracle, bank):
+    say("router exact ties (lowest index wins) and n_experts < 256")
+    x = synth.token(seed=5)
+    wr = bank["wr"].copy()
+    bias = bank["bias"].copy()
+    # four identical rows with identical (large) bias tie for the top places;
+    # a fifth pair ties further down the list
+    for e in (200, 5, 77, 130):
+        wr[e] = wr[42]
+        bias[e] = 3.0
+    wr[9], bias[9] = wr[250], 2.0
+    wr[250], bias[250] = wr[9], 2.0
+    scores = torch.empty((1, 256), dtype=torch.float32, device="cuda")
+    ids = torch.empty((1, 6), dtype=torch.int16, device="cuda")
+    wts = torch.empty((1, 6), dtype=torch.float32, device="cuda")
+    for n in (256, 100, 6):
+        wr_n, b_n = np.ascontiguousarray(wr[:n]), np.ascontiguousarray(bias[:n])
+        router = s14.Router(dev(wr_n), dev(b_n), n_experts=n)
+        s14.route(ctx, router, 1, dev(x), scores, ids, wts)
+        s_o, i_o, w_o = oracle.route(wr_n, b_n, x)
+        assert host(ids).astype(np.uint16)[0].tolist() == i_o.tolist(), f"n={n}"
+        assert_bit_exact(host(wts)[0], w_o, f"weights n={n}")
+        assert_bit_exact(host(scores)[0][:n], s_o, f"scores n={n}")
+    # the tie group occupies the first four places in index order
+    _, i_o, _ = oracle.route(wr, bias, x)
+    assert i_o.tolist() == [5, 77, 130, 200, 9, 250]
+
+
 def test_moe_layer_route_config2(ctx, oracle, bank):
     say("config 2 layer with device router, exact + fast")
     x = synth.token(seed=0)
