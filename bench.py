@@ -66,6 +66,9 @@ def parse():
     ap.add_argument("--profile-steps", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device copy 10 times (the known-size kernel that "
+                         "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     ap.add_argument("--only", choices=["k1", "k8", "all"], default="all",
                     help="restrict the timed work (for profiler runs)")
     return ap.parse_args()
@@ -87,6 +90,8 @@ def main() -> int:
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.init()
+    if args.copy_calibration:
+        return copy_calibration(torch)
     ctx = s14.Context(0)
     mode = s14.EXACT if args.mode == "exact" else s14.FAST
     NL, P = args.layers, args.tokens
@@ -131,7 +136,7 @@ def main() -> int:
 
     def stages(fn, steps, m):
         ctx.enable_stage_timing(True)
-        acc = np.zeros(3)
+        acc = np.zeros(4)
         for i in range(steps):
             fn(i, m)
             acc += np.array(ctx.stage_times())
@@ -154,7 +159,7 @@ def main() -> int:
             r["k1"] = {
                 "us_per_token": ms1 * 1e3,
                 "hbm_gbps": layer_bytes_k1() / (ms1 * 1e-3) / 1e9,
-                "stage_ms": {"router": st1[0], "phase1": st1[1], "phase2": st1[2]},
+                "stage_ms": {"router": st1[0], "plan": st1[1], "phase1": st1[2], "phase2": st1[3]},
             }
             r["k1"]["hbm_frac"] = r["k1"]["hbm_gbps"] / HBM_PEAK_GBPS
         if args.only in ("k8", "all"):
@@ -166,7 +171,7 @@ def main() -> int:
                 "ms_per_block": ms8,
                 "distinct_pages": d,
                 "hbm_gbps": block_bytes(round(d), 8) / (ms8 * 1e-3) / 1e9,
-                "stage_ms": {"router": st8[0], "phase1": st8[1], "phase2": st8[2]},
+                "stage_ms": {"router": st8[0], "plan": st8[1], "phase1": st8[2], "phase2": st8[3]},
             }
             r["k8"]["hbm_frac"] = r["k8"]["hbm_gbps"] / HBM_PEAK_GBPS
         out[name] = r
@@ -186,7 +191,7 @@ def main() -> int:
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
         "frac": achieved / HBM_PEAK_GBPS,
-        "traffic": None,
+        "traffic": measured_traffic(f"k_phase1_{args.mode}"),
         "algorithmic_bytes": p1_bytes,
         "avg_ms": p1_ms,
     }
@@ -228,6 +233,36 @@ def main() -> int:
     print(json.dumps(line), flush=True)
     ctx.synchronize()
     return 0
+
+
+COPY_BYTES = 256 << 20
+
+
+def copy_calibration(torch) -> int:
+    """A plain device copy of COPY_BYTES, 10 times: under rocprofv3 --pmc its
+    FETCH_SIZE / WRITE_SIZE per dispatch should read COPY_BYTES / 1024 KiB;
+    the ratio scales the counters of the S14 kernels."""
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "reps": 10}), flush=True)
+    return 0
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` (read + written) from the committed
+    counter summary: lines 'traffic <kernel> <fetch_bytes> <write_bytes>'
+    in profiles/*.md, already scaled by the copy calibration.  None when no
+    summary covers the kernel."""
+    for f in sorted((ROOT / "profiles").glob("*.md")):
+        for ln in f.read_text().splitlines():
+            parts = ln.strip().strip("`").split()
+            if len(parts) == 4 and parts[0] == "traffic" and parts[1] == kernel:
+                return int(parts[2]) + int(parts[3])
+    return None
 
 
 def cpu_baseline(args, bank, routers_h, X, ctx):

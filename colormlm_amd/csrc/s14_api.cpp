@@ -17,6 +17,11 @@
 
 using s14::fail;
 
+namespace {
+// stages of a fused launch timed by per-kernel start/stop events
+enum { kStageRouter = 0, kStagePlan = 1, kStagePhase1 = 2, kStagePhase2 = 3, kStages = 4 };
+}  // namespace
+
 struct s14_ctx {
   int device = 0;
   hipStream_t compute = nullptr;
@@ -24,10 +29,12 @@ struct s14_ctx {
   void *ws_base = nullptr;
   s14::Workspace ws{};
   s14::PageOffsets mx{}, fp8{};
-  // optional per-stage timestamps of the fused entry points (the role of
-  // the reference's Vulkan timestamp queries): plan/router, phase 1, phase 2
+  // optional per-kernel timing of the fused entry points (the role of the
+  // reference's Vulkan timestamp queries): router scores, plan, phase 1,
+  // phase 2
   bool stage_timing = false;
-  hipEvent_t stage_ev[4] = {nullptr, nullptr, nullptr, nullptr};
+  hipEvent_t stage_ev[2 * kStages] = {};  // start/stop per stage kernel
+  uint32_t stage_mask = 0;                 // stages the last fused launch ran
   bool stage_valid = false;
 };
 
@@ -345,26 +352,27 @@ s14::RouterArgs router_args(const s14_router *r) {
   return s14::RouterArgs{r->weight, r->bias, r->n_experts, r->topk, r->score_fn, r->route_scale};
 }
 
-// Records stage timestamp i on `st` when stage timing is on.
-int stage_mark(s14_ctx *ctx, hipStream_t st, int i) {
-  if (!ctx->stage_timing) return S14_OK;
-  if (i == 0) ctx->stage_valid = false;
-  S14_HIP(hipEventRecord(ctx->stage_ev[i], st), "hipEventRecord(stage)");
-  if (i == 3) ctx->stage_valid = true;
-  return S14_OK;
+// Stage-timing events for stage i of a fused launch (none when off).
+s14::KernelEvents stage_events(s14_ctx *ctx, int i) {
+  if (!ctx->stage_timing) return {};
+  ctx->stage_mask |= 1u << i;
+  return {ctx->stage_ev[2 * i], ctx->stage_ev[2 * i + 1]};
+}
+void stage_begin(s14_ctx *ctx) {
+  ctx->stage_mask = 0;
+  ctx->stage_valid = false;
 }
 
-// phase 1 -> phase 2 with stage marks 1..3 (mark 0 precedes the router and
-// the plan).
+// phase 1 -> phase 2 (the router and plan stages, when any, precede).
 int run_layer(s14_ctx *ctx, hipStream_t st, const s14::PairTable *host_plan, uint32_t n_pairs, uint32_t tokens,
               const float *x, float *y, int mode) {
-  if (int rc = stage_mark(ctx, st, 1)) return rc;
-  hipError_t e = s14::launch_phase1(st, ctx->ws, host_plan, n_pairs, ctx->mx, ctx->fp8, x, mode);
+  hipError_t e = s14::launch_phase1(st, ctx->ws, host_plan, n_pairs, tokens, ctx->mx, ctx->fp8, x, mode,
+                                    stage_events(ctx, kStagePhase1));
   if (e != hipSuccess) return hip_fail(e, "phase 1 launch");
-  if (int rc = stage_mark(ctx, st, 2)) return rc;
-  e = s14::launch_phase2(st, ctx->ws, tokens, ctx->mx, ctx->fp8, y, mode);
+  e = s14::launch_phase2(st, ctx->ws, tokens, ctx->mx, ctx->fp8, y, mode, stage_events(ctx, kStagePhase2));
   if (e != hipSuccess) return hip_fail(e, "phase 2 launch");
-  return stage_mark(ctx, st, 3);
+  ctx->stage_valid = ctx->stage_timing;
+  return S14_OK;
 }
 
 }  // namespace
@@ -384,7 +392,7 @@ extern "C" int s14_expert_chain(s14_ctx *ctx, void *stream, const uint8_t *page,
   s14::plan_pair(t, 0, page, S14_PAGE_MXFP4, 0, 0, route_w, false);
   t.npairs[0] = 1;
   hipStream_t st = pick(ctx, stream);
-  if (int rc = stage_mark(ctx, st, 0)) return rc;
+  stage_begin(ctx);
   return run_layer(ctx, st, &t, 1, 1, x, y, mode);
 }
 
@@ -416,7 +424,7 @@ extern "C" int s14_moe_layer(s14_ctx *ctx, void *stream, uint32_t topk, const ui
   t.n_distinct = topk;
   t.npairs[0] = n;
   hipStream_t st = pick(ctx, stream);
-  if (int rc = stage_mark(ctx, st, 0)) return rc;
+  stage_begin(ctx);
   return run_layer(ctx, st, &t, n, 1, x, y, mode);
 }
 
@@ -437,9 +445,9 @@ extern "C" int s14_moe_block_route(s14_ctx *ctx, void *stream, uint32_t tokens, 
   hipStream_t st = pick(ctx, stream);
   const s14::RouteSpec rs{router_args(router), tokens, shared_format, expert_pages_dev, shared_page, ids_out,
                           weights_out};
-  if (int rc = stage_mark(ctx, st, 0)) return rc;
-  hipError_t e = s14::launch_router_scores(st, ctx->ws, rs.r, tokens, x);
-  if (e == hipSuccess) e = s14::launch_plan(st, ctx->ws, rs);
+  stage_begin(ctx);
+  hipError_t e = s14::launch_router_scores(st, ctx->ws, rs.r, tokens, x, stage_events(ctx, kStageRouter));
+  if (e == hipSuccess) e = s14::launch_plan(st, ctx->ws, rs, stage_events(ctx, kStagePlan));
   if (e != hipSuccess) return hip_fail(e, "router launch");
   return run_layer(ctx, st, nullptr, tokens * (s14::kTopK + 1), tokens, x, y, mode);
 }
@@ -564,10 +572,13 @@ extern "C" int s14_ctx_stage_times(s14_ctx *ctx, float *ms, uint32_t cap, uint32
   if (int rc = check_ctx(ctx)) return rc;
   if (!ms || !n_stages) return fail(S14_ERR_INVALID, "NULL stage-time output");
   if (!ctx->stage_valid) return fail(S14_ERR_NOT_READY, "no timed launch recorded");
-  S14_HIP(hipEventSynchronize(ctx->stage_ev[3]), "hipEventSynchronize(stage)");
-  const uint32_t n = cap < 3 ? cap : 3;
-  for (uint32_t i = 0; i < n; ++i)
-    S14_HIP(hipEventElapsedTime(&ms[i], ctx->stage_ev[i], ctx->stage_ev[i + 1]), "hipEventElapsedTime");
-  *n_stages = 3;
+  const uint32_t n = cap < uint32_t(kStages) ? cap : uint32_t(kStages);
+  for (uint32_t i = 0; i < n; ++i) {
+    ms[i] = 0.0f;
+    if (!(ctx->stage_mask & (1u << i))) continue;
+    S14_HIP(hipEventSynchronize(ctx->stage_ev[2 * i + 1]), "hipEventSynchronize(stage)");
+    S14_HIP(hipEventElapsedTime(&ms[i], ctx->stage_ev[2 * i], ctx->stage_ev[2 * i + 1]), "hipEventElapsedTime");
+  }
+  *n_stages = uint32_t(kStages);
   return S14_OK;
 }

@@ -17,6 +17,7 @@
 //
 // Build: hipcc --offload-arch=gfx950 -ffp-contract=off (contraction would
 // fuse the exact kernels' multiply-then-add).
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "s14_device.hpp"
@@ -1154,7 +1155,9 @@ __device__ __forceinline__ uint32_t page_bytes(uint32_t fmt) {
 // Phase 1 EXACT: one wavefront per (16-row tile, pair); lanes 0-31 take the
 // tile's rows of w1, lanes 32-63 the same rows of w3, one row per lane pair;
 // h = swiglu(g, u) after a half swap.
-template <bool kHostPlan>
+// kTier (1: single-token launch, 8: block launch) only names the
+// instantiation, so traces and profiles keep the two workloads apart.
+template <bool kHostPlan, int kTier>
 __global__ __launch_bounds__(64) void k_phase1_exact(PairTable plan, Workspace ws, const float *__restrict__ X,
                                                      PageOffsets mx, PageOffsets f8) {
   __shared__ float xs[kHidden];
@@ -1190,7 +1193,7 @@ __global__ __launch_bounds__(64) void k_phase1_exact(PairTable plan, Workspace w
 
 // Phase 1 FAST: 4 wavefronts per workgroup, each kP1FastRowsPerWave rows of
 // w1 and w3 (x for the lane's k slices held in registers).
-template <bool kHostPlan>
+template <bool kHostPlan, int kTier>
 __global__ __launch_bounds__(256) void k_phase1_fast(PairTable plan, Workspace ws, const float *__restrict__ X,
                                                      PageOffsets mx, PageOffsets f8) {
   constexpr int NSEG = kHidden / 2048;
@@ -1283,6 +1286,7 @@ __device__ __forceinline__ void phase2_accumulate(const SlotInfo &si, const floa
 // LDS (row stride padded so the two slots' reads fall in different banks).
 constexpr int kHStride = kInter + 8;
 
+template <int kTier>
 __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairTable *__restrict__ tab,
                                                                      const float *__restrict__ H,
                                                                      float *__restrict__ Y, PageOffsets mx,
@@ -1350,6 +1354,7 @@ __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairT
 // pair.
 constexpr int kP2FastWaves = kTopK + 1;
 
+template <int kTier>
 __global__ __launch_bounds__(64 * kP2FastWaves) void k_phase2_fast(const PairTable *__restrict__ tab,
                                                                    const float *__restrict__ H,
                                                                    float *__restrict__ Y, PageOffsets mx,
@@ -1483,43 +1488,72 @@ hipError_t launch_fill_mxfp4_page(hipStream_t s, uint8_t *page, uint64_t seed, u
 }
 
 hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const RouterArgs &r, uint32_t tokens,
-                                const float *x) {
-  k_router_scores<<<dim3((r.n_experts + 3) / 4, tokens), 256, 0, s>>>(r, x, ws.scores, ws.biased);
+                                const float *x, KernelEvents ev) {
+  hipExtLaunchKernelGGL(k_router_scores, dim3((r.n_experts + 3) / 4, tokens), dim3(256), 0, s, ev.start, ev.stop, 0,
+                        r, x, ws.scores, ws.biased);
   return hipGetLastError();
 }
 
-hipError_t launch_plan(hipStream_t s, const Workspace &ws, const RouteSpec &rs) {
-  k_plan<<<1, 64 * kMaxTokens, 0, s>>>(rs, ws);
+hipError_t launch_plan(hipStream_t s, const Workspace &ws, const RouteSpec &rs, KernelEvents ev) {
+  hipExtLaunchKernelGGL(k_plan, dim3(1), dim3(64 * kMaxTokens), 0, s, ev.start, ev.stop, 0, rs, ws);
   return hipGetLastError();
 }
 
-hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *host_plan, uint32_t n_pairs,
-                         const PageOffsets &mx, const PageOffsets &fp8, const float *x, int mode) {
+namespace {
+template <int kTier>
+void phase1_tier(hipStream_t s, const Workspace &ws, const PairTable *host_plan, uint32_t n_pairs,
+                 const PageOffsets &mx, const PageOffsets &fp8, const float *x, int mode, KernelEvents ev) {
   PairTable plan{};
   if (host_plan) plan = *host_plan;
   if (mode == S14_MODE_FAST) {
     const dim3 grid(kInter / kP1FastRows, n_pairs);
     if (host_plan)
-      k_phase1_fast<true><<<grid, 256, 0, s>>>(plan, ws, x, mx, fp8);
+      hipExtLaunchKernelGGL(k_phase1_fast<true, kTier>, grid, dim3(256), 0, s, ev.start, ev.stop, 0, plan, ws, x, mx,
+                            fp8);
     else
-      k_phase1_fast<false><<<grid, 256, 0, s>>>(plan, ws, x, mx, fp8);
+      hipExtLaunchKernelGGL(k_phase1_fast<false, kTier>, grid, dim3(256), 0, s, ev.start, ev.stop, 0, plan, ws, x,
+                            mx, fp8);
   } else {
     const dim3 grid(kInter / kP1ExactRows, n_pairs);
     if (host_plan)
-      k_phase1_exact<true><<<grid, 64, 0, s>>>(plan, ws, x, mx, fp8);
+      hipExtLaunchKernelGGL(k_phase1_exact<true, kTier>, grid, dim3(64), 0, s, ev.start, ev.stop, 0, plan, ws, x, mx,
+                            fp8);
     else
-      k_phase1_exact<false><<<grid, 64, 0, s>>>(plan, ws, x, mx, fp8);
+      hipExtLaunchKernelGGL(k_phase1_exact<false, kTier>, grid, dim3(64), 0, s, ev.start, ev.stop, 0, plan, ws, x,
+                            mx, fp8);
   }
+}
+
+template <int kTier>
+void phase2_tier(hipStream_t s, const Workspace &ws, uint32_t tokens, const PageOffsets &mx, const PageOffsets &fp8,
+                 float *y, int mode, KernelEvents ev) {
+  const PairTable *tab = ws.table;
+  const float *h = ws.h;
+  if (mode == S14_MODE_FAST)
+    hipExtLaunchKernelGGL(k_phase2_fast<kTier>, dim3(kHidden / kP2FastRows, tokens), dim3(64 * kP2FastWaves), 0, s,
+                          ev.start, ev.stop, 0, tab, h, y, mx, fp8);
+  else
+    hipExtLaunchKernelGGL(k_phase2_exact<kTier>, dim3(kHidden / kP2ExactRows, tokens), dim3(64 * kP2ExactWaves), 0,
+                          s, ev.start, ev.stop, 0, tab, h, y, mx, fp8);
+}
+}  // namespace
+
+hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *host_plan, uint32_t n_pairs,
+                         uint32_t tokens, const PageOffsets &mx, const PageOffsets &fp8, const float *x, int mode,
+                         KernelEvents ev) {
+  if (tokens <= 1)
+    phase1_tier<1>(s, ws, host_plan, n_pairs, mx, fp8, x, mode, ev);
+  else
+    phase1_tier<kMaxTokens>(s, ws, host_plan, n_pairs, mx, fp8, x, mode, ev);
   return hipGetLastError();
 }
 
 hipError_t launch_phase2(hipStream_t s, const Workspace &ws, uint32_t tokens, const PageOffsets &mx,
-                         const PageOffsets &fp8, float *y, int mode) {
-  if (mode == S14_MODE_FAST)
-    k_phase2_fast<<<dim3(kHidden / kP2FastRows, tokens), 64 * kP2FastWaves, 0, s>>>(ws.table, ws.h, y, mx, fp8);
+                         const PageOffsets &fp8, float *y, int mode, KernelEvents ev) {
+  if (tokens <= 1)
+    phase2_tier<1>(s, ws, tokens, mx, fp8, y, mode, ev);
   else
-    k_phase2_exact<<<dim3(kHidden / kP2ExactRows, tokens), 64 * kP2ExactWaves, 0, s>>>(ws.table, ws.h, y, mx,
-                                                                                       fp8);
+    phase2_tier<kMaxTokens>(s, ws, tokens, mx, fp8, y, mode, ev);
   return hipGetLastError();
 }
 

@@ -103,6 +103,13 @@ struct RouteSpec {
   float *weights_out;
 };
 
+// Optional start/stop events a fused launcher attaches to its kernel launch
+// (hipExtLaunchKernelGGL): they time the kernel's own execution.
+struct KernelEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+
 // --- standalone dispatches (bind/cmd API) ---
 hipError_t launch_mxfp4_matvec(hipStream_t s, const s14_mxfp4_dispatch &d);
 hipError_t launch_fp8_matvec(hipStream_t s, const s14_fp8_dispatch &d);
@@ -120,19 +127,20 @@ hipError_t launch_fill_mxfp4_page(hipStream_t s, uint8_t *page, uint64_t seed, u
 // --- fused layer / block path: router -> plan -> phase 1 -> phase 2 ---
 // Scores and biased scores of every (token, expert) into ws.scores/biased.
 hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const RouterArgs &r,
-                                uint32_t tokens, const float *x);
+                                uint32_t tokens, const float *x, KernelEvents ev = {});
 // Top-k and weights of every token (after launch_router_scores) to
 // rs.ids_out/weights_out when given; with rs.expert_pages also the pair
 // table in ws.table.
-hipError_t launch_plan(hipStream_t s, const Workspace &ws, const RouteSpec &rs);
+hipError_t launch_plan(hipStream_t s, const Workspace &ws, const RouteSpec &rs, KernelEvents ev = {});
 // w1/w3 + SwiGLU of every pair.  host_plan != NULL: the pairs are given and
 // workgroup (0,0) publishes them for phase 2; otherwise they are read from
 // the table launch_plan wrote.
 hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *host_plan,
-                         uint32_t n_pairs, const PageOffsets &mx, const PageOffsets &fp8,
-                         const float *x, int mode);
+                         uint32_t n_pairs, uint32_t tokens, const PageOffsets &mx,
+                         const PageOffsets &fp8, const float *x, int mode, KernelEvents ev = {});
 // w2 of every pair and the per-token accumulation into y [tokens][hidden].
 hipError_t launch_phase2(hipStream_t s, const Workspace &ws, uint32_t tokens,
-                         const PageOffsets &mx, const PageOffsets &fp8, float *y, int mode);
+                         const PageOffsets &mx, const PageOffsets &fp8, float *y, int mode,
+                         KernelEvents ev = {});
 
 }  // namespace s14

@@ -91,11 +91,12 @@ class Context:
         check(lib().s14_ctx_enable_stage_timing(self._h, 1 if enable else 0))
 
     def stage_times(self):
-        """ms of {plan/router, phase 1, phase 2} of the last fused launch."""
-        ms = (C.c_float * 3)()
+        """Kernel ms of {router scores, plan, phase 1, phase 2} of the last
+        fused launch (0 for a stage it did not run)."""
+        ms = (C.c_float * 4)()
         n = C.c_uint32()
-        check(lib().s14_ctx_stage_times(self._h, ms, 3, C.byref(n)))
-        return [float(ms[i]) for i in range(3)]
+        check(lib().s14_ctx_stage_times(self._h, ms, 4, C.byref(n)))
+        return [float(ms[i]) for i in range(n.value)]
 
     def destroy(self) -> None:
         if self._h:

@@ -94,12 +94,14 @@ void s14_ctx_destroy(s14_ctx *ctx);
 void *s14_ctx_compute_stream(s14_ctx *ctx);
 void *s14_ctx_copy_stream(s14_ctx *ctx);
 int s14_ctx_synchronize(s14_ctx *ctx);
-/* Stage timestamps (the role of the reference's Vulkan timestamp queries,
+/* Stage timing (the role of the reference's Vulkan timestamp queries,
  * s14_vulkan_numeric.rs:1088-1101): when enabled, each fused entry point
- * (chain, layer, block) records a hipEvent before its plan/router kernel,
- * between its two expert phases and after the last.  s14_ctx_stage_times
- * waits for the last such launch and returns the elapsed ms of its three
- * stages {plan/router, phase 1 (w1, w3, SwiGLU), phase 2 (w2, mix)}. */
+ * (chain, layer, block) attaches start/stop hipEvents to each of its kernel
+ * launches, timing the kernels' own execution.  s14_ctx_stage_times waits
+ * for the last such launch and returns up to 4 stage durations in ms:
+ * {router scores, plan, phase 1 (w1, w3, SwiGLU), phase 2 (w2, mix)}; a
+ * stage the last launch did not run (chain and given-route layers have no
+ * router or plan) reads 0. */
 int s14_ctx_enable_stage_timing(s14_ctx *ctx, int enable);
 int s14_ctx_stage_times(s14_ctx *ctx, float *ms, uint32_t cap, uint32_t *n_stages);
 
