@@ -49,6 +49,20 @@ def block_bytes(distinct: int, tokens: int) -> int:
     return (distinct + 1) * PAGE + ROUTER + tokens * 2 * X_BYTES
 
 
+PREFILL_TOKENS = 512
+FP8_MFMA_PEAK_TFLOPS = 5000.0  # dense FP8 (the B operand's format; MXFP4 x FP8 runs at the FP8 rate)
+
+
+def prefill_bytes(distinct: int, tokens: int) -> int:
+    # each distinct routed page and the shared page once; router once; x in, y out
+    return (distinct + 1) * PAGE + ROUTER + tokens * 2 * X_BYTES
+
+
+def prefill_flops(tokens: int) -> int:
+    # 7 experts per token, w1 + w3 + w2 (3 x 2048 x 4096 MACs each), plus the router
+    return tokens * (7 * 3 * 2 * 2048 * 4096 + 2 * 256 * 4096)
+
+
 def phase1_bytes(pairs: int, tokens: int) -> int:
     # w1/s1/w3/s3 of every (token, expert) pair as launched, x read, h written
     return pairs * UP + tokens * X_BYTES + pairs * H_BYTES
@@ -69,7 +83,8 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy 10 times (the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
-    ap.add_argument("--only", choices=["k1", "k8", "all"], default="all",
+    ap.add_argument("--prefill-steps", type=int, default=20)
+    ap.add_argument("--only", choices=["k1", "k8", "prefill", "all"], default="all",
                     help="restrict the timed work (for profiler runs)")
     return ap.parse_args()
 
@@ -176,6 +191,13 @@ def main() -> int:
             r["k8"]["hbm_frac"] = r["k8"]["hbm_gbps"] / HBM_PEAK_GBPS
         out[name] = r
 
+    prefill = None
+    if args.only in ("prefill", "all"):
+        prefill = bench_prefill(args, ctx, tables, shared, NL, torch, np, s14, synth)
+    if args.only == "prefill":
+        print(json.dumps({"prefill": prefill}), flush=True)
+        return 0
+
     main_r = out[args.mode]
     key = "k1" if "k1" in main_r else "k8"
     headline = main_r[key]
@@ -227,12 +249,66 @@ def main() -> int:
         "k1": main_r.get("k1"),
         "k8": main_r.get("k8"),
         "other_mode": {k: v for k, v in out.items() if k != args.mode},
+        "prefill": prefill,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     ctx.synchronize()
     return 0
+
+
+def bench_prefill(args, ctx, tables, shared, NL, torch, np, s14, synth):
+    """Config 4: 512 tokens through the layer as grouped scaled-MFMA GEMMs,
+    layers rotated across steps (each prefill reads ~240 distinct pages,
+    3.2 GB, well past the MALL anyway)."""
+    T = PREFILL_TOKENS
+    routers = []
+    keep = []
+    for L in range(NL):
+        _, b = synth.prefill_router(args.seed, L)
+        bias = torch.from_numpy(b).cuda()
+        keep.append(bias)
+        w, _ = synth.router(args.seed, L)
+        wt = torch.from_numpy(w).cuda()
+        keep.append(wt)
+        routers.append(s14.Router(wt, bias))
+    xs = torch.from_numpy(synth.prefill_tokens(args.seed, T)).cuda()
+    y = torch.empty((T, 4096), dtype=torch.float32, device="cuda")
+
+    def step(i):
+        L = i % NL
+        s14.moe_prefill(ctx, T, routers[L], tables[L], shared[L], xs, y)
+
+    stats = []
+    for L in range(NL):
+        step(L)
+        stats.append(s14.last_prefill_stats(ctx))
+    steps = max(args.prefill_steps, 1)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        step(i)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    d = float(np.mean([s["distinct"] for s in stats]))
+    nbytes = prefill_bytes(round(d), T)
+    flops = prefill_flops(T)
+    return {
+        "tokens": T,
+        "ms_per_prefill": ms,
+        "us_per_token": ms * 1e3 / T,
+        "distinct_experts": d,
+        "max_tokens_per_expert": max(s["max_tokens_per_expert"] for s in stats),
+        "algorithmic_bytes": nbytes,
+        "hbm_gbps": nbytes / (ms * 1e-3) / 1e9,
+        "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+        "tflops": flops / (ms * 1e-3) / 1e12,
+        "mfma_frac_fp8": flops / (ms * 1e-3) / 1e12 / FP8_MFMA_PEAK_TFLOPS,
+        "steps": steps,
+    }
 
 
 COPY_BYTES = 256 << 20

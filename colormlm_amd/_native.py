@@ -145,6 +145,20 @@ class Router(C.Structure):
     ]
 
 
+class PrefillView(C.Structure):
+    _fields_ = [
+        ("xq", C.c_void_p),
+        ("xs", C.c_void_p),
+        ("hq", C.c_void_p),
+        ("hs", C.c_void_p),
+        ("down", C.c_void_p),
+        ("pair_token", C.c_void_p),
+        ("token_pair", C.c_void_p),
+        ("tokens", C.c_uint32),
+        ("n_pairs", C.c_uint32),
+    ]
+
+
 class ExpertKeyC(C.Structure):
     _fields_ = [("layer", C.c_uint32), ("kind", C.c_uint8), ("slot", C.c_uint32)]
 
@@ -213,6 +227,10 @@ SIGNATURES = {
     "s14_moe_block_route": (I, [P, P, U32, C.POINTER(Router), P, P, I, P, P, P, P, I]),
     "s14_last_block_distinct": (I, [P, C.POINTER(U32)]),
     "s14_route": (I, [P, P, C.POINTER(Router), U32, P, P, P, P]),
+    "s14_moe_prefill": (I, [P, P, U32, C.POINTER(Router), P, P, P, P, P, P]),
+    "s14_last_prefill_stats": (I, [P, C.POINTER(U32), C.POINTER(U32), C.POINTER(U32)]),
+    "s14_requant_e4m3": (I, [P, P, U32, U32, P, P, P]),
+    "s14_last_prefill_view": (I, [P, C.POINTER(PrefillView)]),
     "s14_fill_mxfp4_page": (I, [P, P, P, U64, U32, U32, U32, U32, I, I]),
     "s14_pool_create": (I, [P, U32, U64, C.POINTER(P)]),
     "s14_pool_destroy": (None, [P]),

@@ -20,7 +20,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "lib" / "libs14hip.so"
-SOURCES = ["s14_device.hip", "s14_api.cpp", "s14_pool.cpp"]
+SOURCES = ["s14_device.hip", "s14_prefill.hip", "s14_api.cpp", "s14_pool.cpp"]
 ARCH = os.environ.get("S14_OFFLOAD_ARCH", "gfx950")
 
 

@@ -14,6 +14,7 @@
 
 #include "s14_device.hpp"
 #include "s14_internal.hpp"
+#include "s14_prefill.hpp"
 
 using s14::fail;
 
@@ -27,6 +28,9 @@ struct s14_ctx {
   hipStream_t compute = nullptr;
   hipStream_t copy = nullptr;
   void *ws_base = nullptr;
+  void *prefill_base = nullptr;  // prefill workspace, made on the first prefill call
+  uint32_t prefill_tokens = 0;   // token count of the last prefill
+  s14::PrefillWorkspace pws{};
   s14::Workspace ws{};
   s14::PageOffsets mx{}, fp8{};
   // optional per-kernel timing of the fused entry points (the role of the
@@ -146,6 +150,7 @@ extern "C" void s14_ctx_destroy(s14_ctx *ctx) {
   if (ctx->compute) (void)hipStreamSynchronize(ctx->compute);
   if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
   if (ctx->ws_base) (void)hipFree(ctx->ws_base);
+  if (ctx->prefill_base) (void)hipFree(ctx->prefill_base);
   if (ctx->compute) (void)hipStreamDestroy(ctx->compute);
   if (ctx->copy) (void)hipStreamDestroy(ctx->copy);
   for (auto ev : ctx->stage_ev)
@@ -490,6 +495,120 @@ extern "C" int s14_route(s14_ctx *ctx, void *stream, const s14_router *router, u
       if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(scores)");
     }
   }
+  return S14_OK;
+}
+
+// ---------------------------------------------------------------------------
+// prefill (config 4)
+// ---------------------------------------------------------------------------
+
+namespace {
+
+// The prefill workspace for kMaxPrefillTokens tokens, allocated once per
+// context on first use (no allocation on later calls).
+int prefill_workspace(s14_ctx *ctx) {
+  if (ctx->prefill_base) return S14_OK;
+  using namespace s14;
+  const uint32_t T = kMaxPrefillTokens, P = kSlots * kMaxPrefillTokens;
+  size_t off = 0;
+  auto take = [&off](size_t bytes) {
+    const size_t o = off;
+    off = align_up(off + bytes, 256);
+    return o;
+  };
+  const size_t o_scores = take(sizeof(float) * T * kMaxExperts);
+  const size_t o_biased = take(sizeof(float) * T * kMaxExperts);
+  const size_t o_ids = take(sizeof(uint32_t) * T * kTopK);
+  const size_t o_w = take(sizeof(float) * T * kTopK);
+  const size_t o_bits = take(sizeof(uint32_t) * kMaxExperts * kPrefillBitWords);
+  const size_t o_items = take(sizeof(PrefillItem) * prefill_max_items(T));
+  const size_t o_stats = take(sizeof(uint32_t) * 4);
+  const size_t o_pt = take(sizeof(uint32_t) * P);
+  const size_t o_tp = take(sizeof(uint32_t) * T * kSlots);
+  const size_t o_xq = take(size_t(T) * kHidden);
+  const size_t o_xs = take(size_t(T) * (kHidden / 32));
+  const size_t o_hq = take(size_t(P) * kInter);
+  const size_t o_hs = take(size_t(P) * (kInter / 32));
+  const size_t o_down = take(sizeof(float) * size_t(P) * kHidden);
+  S14_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  S14_HIP(hipMalloc(&ctx->prefill_base, off), "hipMalloc(prefill workspace)");
+  uint8_t *b = static_cast<uint8_t *>(ctx->prefill_base);
+  PrefillWorkspace &w = ctx->pws;
+  w.scores = reinterpret_cast<float *>(b + o_scores);
+  w.biased = reinterpret_cast<float *>(b + o_biased);
+  w.ids = reinterpret_cast<uint32_t *>(b + o_ids);
+  w.weights = reinterpret_cast<float *>(b + o_w);
+  w.token_bits = reinterpret_cast<uint32_t *>(b + o_bits);
+  w.items = reinterpret_cast<PrefillItem *>(b + o_items);
+  w.stats = reinterpret_cast<uint32_t *>(b + o_stats);
+  w.pair_token = reinterpret_cast<uint32_t *>(b + o_pt);
+  w.token_pair = reinterpret_cast<uint32_t *>(b + o_tp);
+  w.xq = b + o_xq;
+  w.xs = b + o_xs;
+  w.hq = b + o_hq;
+  w.hs = b + o_hs;
+  w.down = reinterpret_cast<float *>(b + o_down);
+  w.bytes = off;
+  return S14_OK;
+}
+
+}  // namespace
+
+extern "C" int s14_moe_prefill(s14_ctx *ctx, void *stream, uint32_t tokens, const s14_router *router,
+                               const uint64_t *expert_pages_dev, const uint8_t *shared_page, const float *x,
+                               float *y, uint16_t *ids_out, float *weights_out) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_router(router)) return rc;
+  if (router->topk != uint32_t(s14::kTopK))
+    return fail(S14_ERR_SHAPE, "prefill requires topk=%d", s14::kTopK);
+  if (tokens == 0 || tokens > s14::kMaxPrefillTokens)
+    return fail(S14_ERR_SHAPE, "prefill token count %u outside 1..%u", tokens, s14::kMaxPrefillTokens);
+  if (!expert_pages_dev || !shared_page || !x || !y) return fail(S14_ERR_INVALID, "NULL prefill buffer");
+  if (int rc = prefill_workspace(ctx)) return rc;
+  hipStream_t st = pick(ctx, stream);
+  const s14::PrefillArgs a{router_args(router), tokens, expert_pages_dev, shared_page, ctx->mx, x, y,
+                           ids_out, weights_out};
+  const hipError_t e = s14::launch_prefill(st, a, ctx->pws);
+  if (e != hipSuccess) return hip_fail(e, "prefill launch");
+  ctx->prefill_tokens = tokens;
+  return S14_OK;
+}
+
+extern "C" int s14_requant_e4m3(s14_ctx *ctx, void *stream, uint32_t rows, uint32_t k, const float *x,
+                                uint8_t *q, uint8_t *scales) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (rows == 0 || k == 0 || k % 32 != 0) return fail(S14_ERR_SHAPE, "requant needs rows > 0 and k a multiple of 32");
+  if (uint64_t(rows) * k >= (uint64_t(1) << 32))
+    return fail(S14_ERR_SHAPE, "requant of %u x %u values exceeds 2^32 values", rows, k);
+  if (!x || !q || !scales) return fail(S14_ERR_INVALID, "NULL requant buffer");
+  const hipError_t e = s14::launch_requant_e4m3(pick(ctx, stream), rows, k, x, q, scales);
+  if (e != hipSuccess) return hip_fail(e, "requant launch");
+  return S14_OK;
+}
+
+extern "C" int s14_last_prefill_stats(s14_ctx *ctx, uint32_t *distinct, uint32_t *max_tokens, uint32_t *n_items) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!ctx->prefill_base) return fail(S14_ERR_NOT_READY, "no prefill launched on this context");
+  S14_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  S14_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  uint32_t st[4];
+  S14_HIP(hipMemcpy(st, ctx->pws.stats, sizeof(st), hipMemcpyDeviceToHost), "hipMemcpy(prefill stats)");
+  if (distinct) *distinct = st[1];
+  if (max_tokens) *max_tokens = st[2];
+  if (n_items) *n_items = st[0];
+  return S14_OK;
+}
+
+extern "C" int s14_last_prefill_view(s14_ctx *ctx, s14_prefill_view *out) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!out) return fail(S14_ERR_INVALID, "NULL prefill view");
+  if (!ctx->prefill_base || !ctx->prefill_tokens) return fail(S14_ERR_NOT_READY, "no prefill launched on this context");
+  S14_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  S14_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  uint32_t st[4];
+  S14_HIP(hipMemcpy(st, ctx->pws.stats, sizeof(st), hipMemcpyDeviceToHost), "hipMemcpy(prefill stats)");
+  const s14::PrefillWorkspace &w = ctx->pws;
+  *out = s14_prefill_view{w.xq, w.xs, w.hq, w.hs, w.down, w.pair_token, w.token_pair, ctx->prefill_tokens, st[3]};
   return S14_OK;
 }
 

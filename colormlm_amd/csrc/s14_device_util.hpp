@@ -1,0 +1,245 @@
+// Device helpers shared by the gfx950 kernel files (s14_device.hip,
+// s14_prefill.hip): buffer-resource loads, the decoders, SwiGLU, wavefront
+// DPP reductions and the top-k selection of one token's router scores.
+// Everything sits in an unnamed namespace: each kernel file gets its own
+// inline copy.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "s14_device.hpp"
+#include "s14_expf.h"
+
+namespace s14 {
+namespace {
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+// ---------------------------------------------------------------------------
+// buffer-resource loads: page addresses come from memory (generic pointers),
+// which would otherwise become flat loads that also occupy the LDS counter;
+// raw buffer loads keep weight traffic on the vector-memory counter only and
+// return 0 past num_records instead of faulting.
+// ---------------------------------------------------------------------------
+
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // gfx9 raw buffer descriptor flags
+
+__device__ __forceinline__ Rsrc make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, int(bytes), int(kRsrcWord3));
+}
+__device__ __forceinline__ uint4 ld16(Rsrc r, uint32_t off) {
+  const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld8(Rsrc r, uint32_t off) {
+  const v2u v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ld4(Rsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t ld1(Rsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+}
+__device__ __forceinline__ float ldf(Rsrc r, uint32_t off) { return __uint_as_float(ld4(r, off)); }
+
+// Where a row's bytes come from: one matrix (codes and scales may be
+// separate buffers), or two pages split by lane half (lanes 32-63 read page
+// b), each page holding its codes and scales.
+struct Src1 {
+  Rsrc w, s;
+};
+struct Src2 {
+  Rsrc a, b;
+  bool hi;
+};
+
+// ---------------------------------------------------------------------------
+// decoders (bit patterns; equal to s14_vulkan_numeric.rs:1716-1743)
+// ---------------------------------------------------------------------------
+
+// 2^(c-127) as f32; c = 0 is the subnormal 2^-127, c = 255 is +inf.
+__device__ __forceinline__ float ue8m0_f32(uint32_t c) {
+  return c == 0u ? __uint_as_float(0x00400000u) : __uint_as_float(c << 23);
+}
+
+// E2M1 nibble: magnitudes {0, .5, 1, 1.5, 2, 3, 4, 6}; for m >= 2 the f32
+// bit pattern is (m + 252) << 22, m == 1 is 0.5; bit 3 is the sign.
+__device__ __forceinline__ float e2m1_f32(uint32_t nib) {
+  const uint32_t m = nib & 7u;
+  const uint32_t bits = m == 0u ? 0u : (m == 1u ? 0x3F000000u : ((m + 252u) << 22));
+  return __uint_as_float(bits | ((nib & 8u) << 28));
+}
+
+// OCP E4M3FN: exponent 0 is m * 2^-9, otherwise (1 + m/8) * 2^(e-7).  The
+// NaN codes decode as 480 like the reference CPU decoder; they are rejected
+// on the host before upload (s14_vulkan.rs:151-156).
+__device__ __forceinline__ float e4m3_f32(uint32_t code) {
+  const uint32_t e = (code >> 3) & 15u, m = code & 7u;
+  const float mag = e == 0u ? float(m) * 0x1p-9f : __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return (code & 0x80u) ? -mag : mag;
+}
+
+__device__ __forceinline__ float bf16_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ float swiglu_exact(float gate, float up) {
+  // s14_vulkan_numeric.rs:1543-1556: gate.min(10) keeps -0 and maps NaN to
+  // 10; clamp passes NaN through.
+  const float g = (gate <= 10.0f) ? gate : 10.0f;
+  float u = up;
+  if (u < -10.0f) u = -10.0f;
+  if (u > 10.0f) u = 10.0f;
+  const float e = s14x::expf_glibc(-g);
+  return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
+}
+
+// ---------------------------------------------------------------------------
+// wavefront reductions and lane movement
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = min(v, __shfl_xor(v, m));
+  return v;
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m));
+  return v;
+}
+
+// DPP row operations.  dpp_f/dpp_i read the source lane given by CTRL; lanes
+// without a source (or in rows outside ROW_MASK) get `old`.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int dpp_i(int old, int v) {
+  return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xf, false);
+}
+
+// Value of the odd lane of each lane pair (quad_perm [1,1,3,3]); every lane
+// has a source, so the move folds into the consuming VALU op as a DPP operand.
+__device__ __forceinline__ float from_odd(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xF5, 0xf, 0xf, true));
+}
+
+// Full-wavefront sum (order-changing; FAST mode only), returned to every lane.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f<0xb1>(0.0f, v);        // quad_perm [1,0,3,2]
+  v += dpp_f<0x4e>(0.0f, v);        // quad_perm [2,3,0,1]
+  v += dpp_f<0x114>(0.0f, v);       // row_shr:4
+  v += dpp_f<0x118>(0.0f, v);       // row_shr:8
+  v += dpp_f<0x142, 0xa>(0.0f, v);  // row_bcast:15
+  v += dpp_f<0x143, 0xc>(0.0f, v);  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Wavefront max / min of a u32 (DPP row steps, then lane 63), returned to
+// every lane.  Lanes without a DPP source contribute the identity.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, uint32_t(dpp_i<0xb1>(0, int(v))));
+  v = max(v, uint32_t(dpp_i<0x4e>(0, int(v))));
+  v = max(v, uint32_t(dpp_i<0x114>(0, int(v))));
+  v = max(v, uint32_t(dpp_i<0x118>(0, int(v))));
+  v = max(v, uint32_t(dpp_i<0x142, 0xa>(0, int(v))));
+  v = max(v, uint32_t(dpp_i<0x143, 0xc>(0, int(v))));
+  return uint32_t(__builtin_amdgcn_readlane(int(v), 63));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, uint32_t(dpp_i<0xb1>(-1, int(v))));
+  v = min(v, uint32_t(dpp_i<0x4e>(-1, int(v))));
+  v = min(v, uint32_t(dpp_i<0x114>(-1, int(v))));
+  v = min(v, uint32_t(dpp_i<0x118>(-1, int(v))));
+  v = min(v, uint32_t(dpp_i<0x142, 0xa>(-1, int(v))));
+  v = min(v, uint32_t(dpp_i<0x143, 0xc>(-1, int(v))));
+  return uint32_t(__builtin_amdgcn_readlane(int(v), 63));
+}
+
+// Order-preserving key of a score for the top-k selection: larger float ->
+// larger key; -0 and +0 share a key (they compare equal); NaN gets key 0,
+// below every number (a NaN score is never preferred).
+__device__ __forceinline__ uint32_t score_key(float f) {
+  if (f != f) return 0u;
+  const uint32_t u = __float_as_uint(f + 0.0f);  // -0 + 0 = +0
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Top-k of one token's scores, computed by one whole wavefront
+// (executor.py:647-667 semantics, orders fixed here): largest score + bias
+// first, equal values to the lower expert index (as the oracle's strict '>'
+// scan), sum of the chosen unbiased scores sequential in selection order.
+// Lane i < k receives the i-th choice: expert id, unbiased score and the
+// expert's page address (0 when `pages` is NULL).  All loads are issued
+// before the first selection, so no memory access waits on one.
+struct TopK {
+  uint32_t id;
+  float s;
+  uint64_t page;
+  float sum;
+};
+__device__ __forceinline__ TopK select_topk(const float *__restrict__ biased, const float *__restrict__ scores,
+                                            const uint64_t *__restrict__ pages, uint32_t n_experts, uint32_t k) {
+  const uint32_t lane = threadIdx.x & 63;
+  // key 0 marks an absent or already chosen expert; a real score's key is
+  // >= 1 unless it is NaN
+  uint32_t kv[4];
+  float sv[4];
+  uint64_t pv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t ee = lane + 64u * j;
+    const bool absent = ee >= n_experts;
+    kv[j] = absent ? 0u : max(score_key(biased[ee]), 1u);
+    sv[j] = absent ? 0.0f : scores[ee];
+    pv[j] = (absent || !pages) ? 0ull : pages[ee];
+  }
+  TopK mine{0u, 0.0f, 0ull, 0.0f};
+  float sum = 0.0f;
+#pragma unroll
+  for (uint32_t i = 0; i < uint32_t(kTopK); ++i) {
+    if (i >= k) break;
+    // max key over the wavefront, then the lowest expert index holding it
+    const uint32_t top = wave_max_u32(max(max(kv[0], kv[1]), max(kv[2], kv[3])));
+    uint32_t idx = 0xffffffffu;
+#pragma unroll
+    for (int j = 3; j >= 0; --j) idx = kv[j] == top ? lane + 64u * j : idx;
+    const int best = int(wave_min_u32(idx));
+    float cand = sv[0];
+    uint64_t cpg = pv[0];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (int(lane + 64u * j) == best) kv[j] = 0u;
+      if ((best >> 6) == j) {
+        cand = sv[j];
+        cpg = pv[j];
+      }
+    }
+    const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cand), best & 63));
+    const uint64_t pg = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(cpg >> 32), best & 63))) << 32) |
+                        uint32_t(__builtin_amdgcn_readlane(int(uint32_t(cpg)), best & 63));
+    sum = __fadd_rn(sum, s);
+    if (lane == i) {
+      mine.id = uint32_t(best);
+      mine.s = s;
+      mine.page = pg;
+    }
+  }
+  mine.sum = sum;
+  return mine;
+}
+
+// Route weight of a choice: s / sum, then * route_scale unless it is 1.
+__device__ __forceinline__ float route_weight(const TopK &c, float route_scale) {
+  float w = __fdiv_rn(c.s, c.sum);
+  if (route_scale != 1.0f) w = __fmul_rn(w, route_scale);
+  return w;
+}
+
+}  // namespace
+}  // namespace s14

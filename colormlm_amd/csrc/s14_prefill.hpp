@@ -1,0 +1,68 @@
+// Prefill (config 4) launcher and its device workspace, used by the C ABI in
+// s14_api.cpp; kernels in s14_prefill.hip.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#include "s14_device.hpp"
+
+namespace s14 {
+
+constexpr uint32_t kMaxPrefillTokens = 1024;
+constexpr uint32_t kPrefillBitWords = kMaxPrefillTokens / 32;  // token bitmap words per expert
+constexpr uint32_t kItemTokens = 128;                          // tokens of one expert per GEMM work item
+
+// One GEMM work item: `count` consecutive pairs of one expert, starting at
+// pair `first` (expert kMaxExperts is the shared expert).
+struct PrefillItem {
+  uint32_t expert;
+  uint32_t first;
+  uint32_t count;
+};
+
+// Upper bound of the work items of T tokens: every expert contributes at
+// most one partial item beyond its full ones.
+constexpr uint32_t prefill_max_items(uint32_t tokens) {
+  return (kTopK * tokens + kItemTokens - 1) / kItemTokens + kMaxExperts + (tokens + kItemTokens - 1) / kItemTokens;
+}
+
+struct PrefillArgs {
+  RouterArgs r;
+  uint32_t tokens;
+  const uint64_t *expert_pages;  // device [256] page addresses
+  const uint8_t *shared_page;
+  PageOffsets mx;
+  const float *x;  // [tokens][4096]
+  float *y;        // [tokens][4096]
+  uint16_t *ids_out;
+  float *weights_out;
+};
+
+// Device workspace for up to kMaxPrefillTokens tokens (one allocation per
+// context, made on the first prefill call).
+struct PrefillWorkspace {
+  float *scores;          // [T][256]
+  float *biased;          // [T][256]
+  uint32_t *ids;          // [T][kTopK]
+  float *weights;         // [T][kTopK]
+  uint32_t *token_bits;   // [256][kPrefillBitWords]
+  PrefillItem *items;     // [prefill_max_items]
+  uint32_t *stats;        // {items, distinct routed experts, max tokens per expert, pairs}
+  uint32_t *pair_token;   // [7T]
+  uint32_t *token_pair;   // [T][kSlots]
+  uint8_t *xq;            // [T][4096] e4m3, MFMA order per 64-k step
+  uint8_t *xs;            // [T][128] E8M0
+  uint8_t *hq;            // [7T][2048] e4m3, MFMA order
+  uint8_t *hs;            // [7T][64] E8M0
+  float *down;            // [7T][4096]
+  size_t bytes;
+};
+
+hipError_t launch_prefill(hipStream_t s, const PrefillArgs &a, const PrefillWorkspace &ws);
+// e4m3 requant of a row-major [rows, k] f32 matrix, groups of 32 along k
+// (natural layout): q [rows, k], scales [rows, k/32] E8M0.
+hipError_t launch_requant_e4m3(hipStream_t s, uint32_t rows, uint32_t k, const float *x, uint8_t *q,
+                               uint8_t *scales);
+
+}  // namespace s14

@@ -399,6 +399,64 @@ def route(ctx: Context, router: Router, tokens: int, x, scores_out=None, ids_out
     )
 
 
+def moe_prefill(ctx: Context, tokens: int, router: Router, expert_pages, shared_page, x, y, ids_out=None,
+                weights_out=None, stream=None) -> None:
+    """Config 4: `tokens` rows of x [tokens, 4096] through the router and the
+    top-6 routed + shared MXFP4 experts as grouped scaled-MFMA GEMMs on
+    e4m3-requantised activations (per-32 E8M0); y [tokens, 4096].  Not
+    order-exact (the MFMA's own summation), see the C header."""
+    r = router.c()
+    check(
+        lib().s14_moe_prefill(
+            ctx.handle, _stream(stream), tokens, C.byref(r), _ptr(expert_pages), _ptr(shared_page), _ptr(x), _ptr(y),
+            _ptr(ids_out), _ptr(weights_out)
+        )
+    )
+
+
+def last_prefill_stats(ctx: Context) -> dict:
+    """Distinct routed experts, largest tokens-per-expert and GEMM work items of
+    the last prefill (synchronises)."""
+    d, m, n = C.c_uint32(), C.c_uint32(), C.c_uint32()
+    check(lib().s14_last_prefill_stats(ctx.handle, C.byref(d), C.byref(m), C.byref(n)))
+    return {"distinct": int(d.value), "max_tokens_per_expert": int(m.value), "items": int(n.value)}
+
+
+def last_prefill_view(ctx: Context) -> dict:
+    """Host copies of the last prefill's intermediates (synchronises): xq/xs
+    and hq/hs in MFMA step order, down [pairs, 4096], pair_token and
+    token_pair [tokens, 7]."""
+    import torch
+
+    v = N.PrefillView()
+    check(lib().s14_last_prefill_view(ctx.handle, C.byref(v)))
+    T, P = int(v.tokens), int(v.n_pairs)
+
+    def grab(ptr, n, typestr):
+        class _Dev:  # a device range exposed to torch without a copy
+            __cuda_array_interface__ = {"shape": (n,), "typestr": typestr, "data": (int(ptr), False), "version": 2}
+
+        return torch.as_tensor(_Dev(), device="cuda").cpu().numpy()
+
+    return {
+        "tokens": T,
+        "n_pairs": P,
+        "xq": grab(v.xq, T * N.HIDDEN, "|u1").reshape(T, N.HIDDEN),
+        "xs": grab(v.xs, T * (N.HIDDEN // 32), "|u1").reshape(T, N.HIDDEN // 32),
+        "hq": grab(v.hq, P * N.INTER, "|u1").reshape(P, N.INTER),
+        "hs": grab(v.hs, P * (N.INTER // 32), "|u1").reshape(P, N.INTER // 32),
+        "down": grab(v.down, P * N.HIDDEN, "<f4").reshape(P, N.HIDDEN),
+        "pair_token": grab(v.pair_token, P, "<i4"),
+        "token_pair": grab(v.token_pair, T * 7, "<i4").reshape(T, 7),
+    }
+
+
+def requant_e4m3(ctx: Context, rows: int, k: int, x, q, scales, stream=None) -> None:
+    """e4m3 requant with per-32 E8M0 scales, natural layout (the prefill's
+    activation quantiser as a standalone dispatch)."""
+    check(lib().s14_requant_e4m3(ctx.handle, _stream(stream), rows, k, _ptr(x), _ptr(q), _ptr(scales)))
+
+
 def fill_mxfp4_page(
     ctx: Context,
     page,

@@ -214,3 +214,27 @@ def block_tokens(seed: int = 0, tokens: int = 8, a: float = 0.5) -> np.ndarray:
         z = gen_normal(seed, STREAM_BLOCK + t, HIDDEN)
         xs[t] = np.float32(a) * xs[t - 1] + b * z
     return xs
+
+
+STREAM_PREFILL = (1 << 48) + (1 << 40)  # + token
+STREAM_ZIPF_PERM = (1 << 48) + 32
+
+
+def prefill_tokens(seed: int = 0, tokens: int = 512) -> np.ndarray:
+    """Config 4 activations X[tokens, 4096] ~ N(0, 1), one stream per token."""
+    return np.stack([gen_normal(seed, STREAM_PREFILL + t, HIDDEN) for t in range(tokens)])
+
+
+def prefill_router(seed: int = 0, layer: int = 0, beta: float = 0.04, s: float = 1.1):
+    """Config 4 router: W_r as config 2, bias_e = beta * log(zipf_pmf(rank_e))
+    over a seeded permutation of the experts, so expert popularity is skewed
+    Zipf(s)-like.  beta = 0.04 gives, over 512 tokens, about 240 distinct
+    experts with the busiest at about 100 tokens (mean about 13)."""
+    wr, _ = router(seed, layer)
+    keys = rand_u64(seed, STREAM_ZIPF_PERM + (layer << 8), np.arange(N_EXPERTS, dtype=np.uint64))
+    rank = np.empty(N_EXPERTS, dtype=np.int64)
+    rank[np.argsort(keys, kind="stable")] = np.arange(N_EXPERTS)
+    pmf = 1.0 / np.power(rank + 1.0, s)
+    pmf /= pmf.sum()
+    bias = (beta * np.log(pmf)).astype(np.float32)
+    return wr, bias

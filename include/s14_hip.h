@@ -259,6 +259,48 @@ int s14_last_block_distinct(s14_ctx *ctx, uint32_t *n_distinct);
 int s14_route(s14_ctx *ctx, void *stream, const s14_router *router, uint32_t tokens,
               const float *x, float *scores_out, uint16_t *ids_out, float *weights_out);
 
+/* Prefill (config 4; the reference has no GPU code for it, its layer
+ * semantics are s14_vulkan_numeric.rs:929-946): tokens <= 1024 through the
+ * router and the top-6 routed + shared MXFP4 experts as grouped GEMMs on
+ * the gfx950 scaled MFMA, activations requantised to e4m3 with per-32 E8M0
+ * scales 2^ceil(log2(max(amax,1e-4)/448)) (l42_reference.py:390-403 with
+ * group 32) before w1/w3 and again (h) before w2.  Not order-exact: results
+ * agree with the CPU oracle to a measured tolerance.  The shared page must
+ * be MXFP4.  ids_out [T, 6] u16 and weights_out [T, 6] f32 may be NULL.
+ * The first call on a context allocates its prefill workspace. */
+int s14_moe_prefill(s14_ctx *ctx, void *stream, uint32_t tokens, const s14_router *router,
+                    const uint64_t *expert_pages_dev, const uint8_t *shared_page, const float *x,
+                    float *y, uint16_t *ids_out, float *weights_out);
+/* Distinct routed experts, the largest tokens-per-expert and the number of
+ * GEMM work items of the last prefill (synchronises the device). */
+int s14_last_prefill_stats(s14_ctx *ctx, uint32_t *distinct, uint32_t *max_tokens,
+                           uint32_t *n_items);
+#define S14_MAX_PREFILL_TOKENS 1024u
+/* Read-only device view of the last prefill's intermediates on this context
+ * (valid until the next prefill on it), for stage-by-stage verification.
+ * No counterpart in the reference, whose GPU code has no prefill.
+ *   xq [tokens][4096] e4m3 and xs [tokens][128] E8M0: the requantised
+ *     activations; within each 64-value step the bytes are ordered
+ *     k 0-15, 32-47, 16-31, 48-63 (the MFMA operand order);
+ *   hq [n_pairs][2048], hs [n_pairs][64]: the SwiGLU output of each
+ *     (token, expert) pair, requantised the same way;
+ *   down [n_pairs][4096] f32: each pair's w2 output, route weight not applied;
+ *   pair_token [n_pairs]: the token of each pair; token_pair [tokens][7]:
+ *     each token's pairs in route order, the shared expert's last.
+ * Pairs are grouped by routed expert ascending, the shared expert's last. */
+typedef struct s14_prefill_view {
+  const uint8_t *xq, *xs, *hq, *hs;
+  const float *down;
+  const uint32_t *pair_token, *token_pair;
+  uint32_t tokens, n_pairs;
+} s14_prefill_view;
+int s14_last_prefill_view(s14_ctx *ctx, s14_prefill_view *out);
+/* The prefill's activation requant as a standalone dispatch (natural
+ * layout): x f32 [rows, k] -> q e4m3 [rows, k] and scales E8M0
+ * [rows, k/32], bit-identical to the CPU oracle's requant. */
+int s14_requant_e4m3(s14_ctx *ctx, void *stream, uint32_t rows, uint32_t k, const float *x,
+                     uint8_t *q, uint8_t *scales);
+
 /* ======================================================================
  * Synthetic page fill (bench / tests): integer hash, same spec as the
  * oracle's generator, computed on the device.

@@ -90,6 +90,8 @@ def _declare(L):
         "s14o_route": (None, [U32, U32, P, P, P, I, U32, F, P, P, P]),
         "s14o_error_stats_compute": (None, [C.c_size_t, P, P, C.POINTER(ErrorStats)]),
         "s14o_requant_e4m3": (None, [U32, U32, U32, P, P, P]),
+        "s14o_dequant_requant": (None, [U32, U32, U32, P, P, P]),
+        "s14o_mxfp4_expert_down_requant": (None, [U32, U32, U32, P, C.POINTER(_Expert), P]),
         "s14o_num_threads": (I, []),
         "s14o_set_num_threads": (None, [I]),
     }
@@ -278,6 +280,34 @@ def requant_e4m3(x, group: int = 32):
     s = np.empty((rows, k // group), dtype=np.uint8)
     lib().s14o_requant_e4m3(rows, k, group, _p(x), _p(q), _p(s))
     return q, s
+
+
+def dequant_requant(q, scale_codes, group: int = 32):
+    q = np.ascontiguousarray(np.atleast_2d(q), dtype=np.uint8)
+    sc = np.ascontiguousarray(np.atleast_2d(scale_codes), dtype=np.uint8)
+    rows, k = q.shape
+    out = np.empty((rows, k), dtype=np.float32)
+    lib().s14o_dequant_requant(rows, k, group, _p(q), _p(sc), _p(out))
+    return out
+
+
+def expert_down_requant(x, page, group: int = 32, hidden=HIDDEN, inter=INTER) -> np.ndarray:
+    """Prefill expert on requantised activations (config 4), route weight not applied."""
+    x = _f32(x)
+    e = _expert(page, "mxfp4", hidden, inter)
+    out = np.empty(hidden, dtype=np.float32)
+    lib().s14o_mxfp4_expert_down_requant(hidden, inter, group, _p(x), C.byref(e), _p(out))
+    return out
+
+
+def moe_prefill_token(x, routed_pages, weights, shared_page, group: int = 32) -> np.ndarray:
+    """One token of the config-4 layer: acc = 0; acc += w_i * down_i in route
+    order; acc += shared_down (s14_vulkan_numeric.rs:929-946 order), each
+    down computed by expert_down_requant."""
+    acc = np.zeros(HIDDEN, dtype=np.float32)
+    for p, w in zip(routed_pages, _f32(weights)):
+        acc = (acc + np.float32(w) * expert_down_requant(x, p, group)).astype(np.float32)
+    return (acc + expert_down_requant(x, shared_page, group)).astype(np.float32)
 
 
 def set_num_threads(n: int) -> None:

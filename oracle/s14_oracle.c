@@ -393,3 +393,30 @@ void s14o_requant_e4m3(uint32_t rows, uint32_t k, uint32_t group, const float *x
     }
   }
 }
+
+void s14o_dequant_requant(uint32_t rows, uint32_t k, uint32_t group, const uint8_t *q,
+                          const uint8_t *scale_codes, float *out) {
+  size_t groups = k / group;
+  for (size_t r = 0; r < rows; ++r)
+    for (size_t i = 0; i < k; ++i)
+      out[r * k + i] = ldexpf(s14o_e4m3fn(q[r * k + i]), (int)scale_codes[r * groups + i / group] - 127);
+}
+
+void s14o_mxfp4_expert_down_requant(uint32_t hidden, uint32_t inter, uint32_t group,
+                                    const float *x, const s14o_mxfp4_expert *e, float *down) {
+  size_t big = hidden > inter ? hidden : inter;
+  float *xd = (float *)malloc(sizeof(float) * (big + 3 * inter));
+  float *gate = xd + big, *up = gate + inter, *h = up + inter;
+  uint8_t *q = (uint8_t *)malloc(big + big / group);
+  uint8_t *sc = q + big;
+  s14o_requant_e4m3(1, hidden, group, x, q, sc);
+  s14o_dequant_requant(1, hidden, group, q, sc, xd);
+  s14o_mxfp4_matvec(inter, hidden, xd, e->w1, e->s1, gate);
+  s14o_mxfp4_matvec(inter, hidden, xd, e->w3, e->s3, up);
+  s14o_swiglu_limit(inter, gate, up, h);
+  s14o_requant_e4m3(1, inter, group, h, q, sc);
+  s14o_dequant_requant(1, inter, group, q, sc, xd);
+  s14o_mxfp4_matvec(hidden, inter, xd, e->w2, e->s2, down);
+  free(q);
+  free(xd);
+}

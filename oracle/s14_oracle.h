@@ -134,6 +134,20 @@ void s14o_error_stats_compute(size_t n, const float *actual, const float *expect
 void s14o_requant_e4m3(uint32_t rows, uint32_t k, uint32_t group, const float *x,
                        uint8_t *q, uint8_t *scale_codes);
 
+/* Dequantise requantised activations: x = e4m3(q) * 2^(code-127), exact. */
+void s14o_dequant_requant(uint32_t rows, uint32_t k, uint32_t group, const uint8_t *q,
+                          const uint8_t *scale_codes, float *out);
+
+/* Prefill expert (config 4, BASELINE: FP8-requantised activations, per-32
+ * E8M0 scales): xd = dequant(requant(x)); g = w1.xd, u = w3.xd in the oracle
+ * order; h = swiglu(g, u); hd = dequant(requant(h)); down = w2.hd.  The
+ * route weight and the accumulation are applied by the caller in the layer
+ * order (s14_vulkan_numeric.rs:929-946).  This is the reference CPU order
+ * applied to the quantised operands; the GPU's MFMA sums them in another
+ * order, so parity for this config is a measured tolerance. */
+void s14o_mxfp4_expert_down_requant(uint32_t hidden, uint32_t inter, uint32_t group,
+                                    const float *x, const s14o_mxfp4_expert *e, float *down);
+
 int s14o_num_threads(void);
 void s14o_set_num_threads(int n);
 

@@ -425,3 +425,259 @@ def test_pool_upload_publish_compute_release(ctx, oracle, bank):
     pages.release_after_compute_fence(lease)
     want = oracle.moe_layer(x, [hosts[e] for e in ids], np.array(w, np.float32), hosts[256])
     assert_bit_exact(host(y), want, "layer from pool slots")
+
+
+# ---------------------------------------------------------------------------
+# prefill (config 4): e4m3 requant + grouped scaled-MFMA GEMM
+# ---------------------------------------------------------------------------
+
+
+def _requant_edge_rows(k: int) -> np.ndarray:
+    """Rows exercising the requant's special cases: zeros and -0 (amax clamp
+    to 1e-4), a tiny row, amax/448 an exact power of two (ceil(log2) must not
+    round up), values on e4m3 round-half-even midpoints, the subnormal grid,
+    NaN (ignored by amax, coded 0x7f) and +-inf-free huge values."""
+    rows = [np.zeros(k, np.float32), np.full(k, -0.0, np.float32), np.full(k, 3e-5, np.float32)]
+    r = np.linspace(-1.0, 1.0, k, dtype=np.float32)
+    r[::32] = 448.0 * 2.0 ** -3  # amax = 56 -> amax / 448 = 2^-3 exactly
+    rows.append(r)
+    # midpoints between adjacent e4m3 values at scale 1 (amax 448 in each group)
+    mids = np.array([1.0625, 1.1875, 3.25 + 0.125, 0.001953125 * 1.5, 0.009765625 * 0.5 + 0.0078125 * 0.5, 240.0 + 8.0],
+                    np.float32)
+    m = np.resize(mids, k).astype(np.float32)
+    m[::32] = 448.0
+    m[1::64] *= -1
+    rows.append(m)
+    sub = (np.arange(k, dtype=np.float32) % 17) * np.float32(2.0 ** -10)  # subnormal e4m3 at scale 1
+    sub[::32] = 448.0
+    rows.append(sub)
+    nan = np.linspace(-3.0, 3.0, k, dtype=np.float32)
+    nan[5::97] = np.nan
+    rows.append(nan)
+    rows.append(np.linspace(-3e30, 3e30, k, dtype=np.float32))
+    return np.stack(rows)
+
+
+def test_requant_e4m3_bit_exact(ctx, oracle):
+    say("e4m3 requant (per-32 E8M0) vs oracle, random + edge rows")
+    k = 4096
+    rng = np.random.default_rng(7)
+    rand = rng.standard_normal((56, k)).astype(np.float32)
+    rand *= np.float32(2.0) ** rng.integers(-30, 20, size=(56, 1)).astype(np.float32)
+    x = np.concatenate([rand, _requant_edge_rows(k)]).astype(np.float32)
+    for rows, kk in ((x.shape[0], k), (3, 96), (1, 32)):
+        xs = np.ascontiguousarray(x[:rows, :kk])
+        q = torch.empty((rows, kk), dtype=torch.uint8, device="cuda")
+        sc = torch.empty((rows, kk // 32), dtype=torch.uint8, device="cuda")
+        s14.requant_e4m3(ctx, rows, kk, dev(xs), q, sc)
+        q_o, s_o = oracle.requant_e4m3(xs)
+        assert np.array_equal(host(sc), s_o), f"scales {rows}x{kk}"
+        qh = host(q)
+        bad = np.argwhere(qh != q_o)
+        assert bad.size == 0, f"codes {rows}x{kk}: {len(bad)} differ, first {bad[:3].tolist()}"
+    with pytest.raises(N.S14Error):
+        s14.requant_e4m3(ctx, 1, 48, dev(x[0, :48]), q, sc)
+
+
+@pytest.fixture(scope="module")
+def prefill_router(bank):
+    wr, bias = synth.prefill_router(seed=0, layer=0)
+    assert np.array_equal(wr, bank["wr"])
+    return {"wr": wr, "bias": bias, "router": s14.Router(bank["wr_d"], dev(bias))}
+
+
+def _run_prefill(ctx, bank, pr, xs):
+    T = xs.shape[0]
+    y = torch.empty((T, HIDDEN), dtype=torch.float32, device="cuda")
+    ids = torch.empty((T, 6), dtype=torch.int16, device="cuda")
+    wts = torch.empty((T, 6), dtype=torch.float32, device="cuda")
+    s14.moe_prefill(ctx, T, pr["router"], bank["table"], bank["pages"][256], dev(xs), y, ids, wts)
+    return host(y), host(ids).astype(np.uint16), host(wts)
+
+
+def _natural(mfma_rows: np.ndarray) -> np.ndarray:
+    """Undo the MFMA byte order of each 64-value step (k 0-15, 32-47, 16-31,
+    48-63) -> natural k order."""
+    k = np.arange(mfma_rows.shape[-1])
+    pos = (k // 64) * 64 + 32 * ((k >> 4) & 1) + 16 * ((k & 63) >> 5) + (k & 15)
+    return mfma_rows[..., pos]
+
+
+# End-to-end tolerance of the MFMA path against the CPU oracle, relative to
+# the output's scale (|y| reaches ~290 here, where one f32 ulp is 3e-5, so an
+# absolute 2e-5 gate cannot hold even between two CPU summation orders).
+# The MFMA sums each 64-k step at its own internal precision (~5e-5 of the
+# tile's largest output), and a perturbed g/u moves an element of h across an
+# e4m3 rounding boundary now and then (~0.05% of them).  Each such flip is one
+# e4m3 step of h (1/16 to 1/8 of it; |h| reaches ~100 at the SwiGLU clamps)
+# and moves the layer output by that step times a w2 column, so one flip of a
+# large element alone costs ~0.5% of max|y| (measured: token 510 of the
+# 512-token case, rmse_rel 5.1e-3).  The stage checks below pin everything
+# else: x and h requant, the grouped GEMMs, the pair bookkeeping and the
+# combine.
+PREFILL_MAX_REL = 2e-2   # max |y - y_ref| / max |y_ref|
+PREFILL_RMSE_REL = 1e-2  # rmse(y - y_ref) / rms(y_ref)
+GEMM_REL = 2e-4          # a grouped GEMM given the GPU's own operands, vs the oracle's f32 matvec
+FLIP_FRACTION = 2e-3     # h codes allowed to differ from the oracle's requant (each by one e4m3 step)
+
+
+def _prefill_close(oracle, got, want, what):
+    st = oracle.error_stats(got, want)
+    scale = float(np.max(np.abs(want)))
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    rel = {"max_rel": st["max_abs"] / scale, "rmse_rel": st["rmse"] / rms}
+    say(f"  {what}: max_abs {st['max_abs']:.3g} rmse {st['rmse']:.3g} max|y| {scale:.1f} -> {rel}")
+    assert st["finite"]
+    assert rel["max_rel"] <= PREFILL_MAX_REL and rel["rmse_rel"] <= PREFILL_RMSE_REL, f"{what}: {rel}"
+    return rel
+
+
+def _e4m3_values(oracle):
+    vals = np.array([oracle.e4m3fn(c) for c in range(256)], np.float64)
+    finite = np.unique(vals[np.isfinite(vals)])
+    return vals, finite
+
+
+def _check_prefill_stages(oracle, bank, view, xs, ids, wts, y, pairs_to_check):
+    """x requant bit-exact; pair bookkeeping; each checked pair's w1/w3 GEMM +
+    SwiGLU + h requant (codes equal to the oracle's or one e4m3 step away, at
+    most FLIP_FRACTION of them) and w2 GEMM (given the GPU's own h, within
+    GEMM_REL); the combine bit-exact for every token."""
+    T = xs.shape[0]
+    q_o, s_o = oracle.requant_e4m3(xs)
+    assert np.array_equal(_natural(view["xq"]), q_o), "x requant codes"
+    assert np.array_equal(view["xs"], s_o), "x requant scales"
+    tp, pt = view["token_pair"], view["pair_token"]
+    assert view["n_pairs"] == 7 * T
+    # pairs grouped by expert ascending, the shared expert's last; token order within an expert
+    expert_of = np.empty(7 * T, np.int64)
+    for t in range(T):
+        for s_ in range(7):
+            p = tp[t, s_]
+            assert pt[p] == t
+            expert_of[p] = ids[t, s_] if s_ < 6 else 256
+    assert np.all(np.diff(expert_of) >= 0)
+    same = np.diff(expert_of) == 0
+    assert np.all(np.diff(pt)[same] > 0)
+    # combine: acc = 0; acc += w * down in route order; acc += shared down
+    down = view["down"]
+    for t in range(T):
+        acc = np.zeros(HIDDEN, np.float32)
+        for s_ in range(6):
+            acc = (acc + np.float32(wts[t, s_]) * down[tp[t, s_]]).astype(np.float32)
+        acc = (acc + down[tp[t, 6]]).astype(np.float32)
+        assert_bit_exact(y[t], acc, f"combine token {t}")
+    vals, grid = _e4m3_values(oracle)
+    flips = codes = scale_miss = 0
+    worst_gemm = 0.0
+    pages = {}
+    for p in pairs_to_check:
+        e = int(expert_of[p])
+        if e not in pages:
+            pages[e] = mx_parts(page_host(bank, e))
+        m = pages[e]
+        t = int(pt[p])
+        xd = oracle.dequant_requant(q_o[t], s_o[t])[0]
+        h_ref = oracle.swiglu_limit(oracle.mxfp4_matvec(xd, m["w1"], m["s1"]), oracle.mxfp4_matvec(xd, m["w3"], m["s3"]))
+        hq_ref, hs_ref = oracle.requant_e4m3(h_ref)
+        hq = _natural(view["hq"][p])
+        ok_scale = view["hs"][p] == hs_ref[0]
+        scale_miss += int(np.count_nonzero(~ok_scale))
+        in_ok = np.repeat(ok_scale, 32)
+        diff = np.flatnonzero((hq != hq_ref[0]) & in_ok)
+        steps = np.abs(np.searchsorted(grid, vals[hq[diff]]) - np.searchsorted(grid, vals[hq_ref[0][diff]]))
+        assert np.all(steps <= 1), f"pair {p}: h codes more than one e4m3 step off at {diff[steps > 1][:5]}"
+        flips += diff.size
+        codes += int(np.count_nonzero(in_ok))
+        hd = oracle.dequant_requant(_natural(view["hq"][p])[None], view["hs"][p][None])[0]
+        d_ref = oracle.mxfp4_matvec(hd, m["w2"], m["s2"])
+        rel = float(np.max(np.abs(down[p] - d_ref)) / np.max(np.abs(d_ref)))
+        worst_gemm = max(worst_gemm, rel)
+        assert rel <= GEMM_REL, f"pair {p} (expert {e}, token {t}): w2 GEMM rel {rel:.3g}"
+    say(f"  stages: {len(pairs_to_check)} pairs, w2 GEMM worst rel {worst_gemm:.3g}, h flips {flips}/{codes}, "
+        f"h scale groups off {scale_miss}")
+    assert flips <= FLIP_FRACTION * codes
+    assert scale_miss <= 2e-3 * len(pairs_to_check) * 64
+
+
+def test_prefill_config4_against_oracle(ctx, oracle, bank, prefill_router):
+    T = 64
+    say(f"config 4 prefill T={T}: routes exact, stages, outputs vs oracle")
+    xs = synth.prefill_tokens(seed=0, tokens=T)
+    y, ids, wts = _run_prefill(ctx, bank, prefill_router, xs)
+    counts = np.zeros(256, np.int64)
+    for t in range(T):
+        _, i_o, w_o = oracle.route(prefill_router["wr"], prefill_router["bias"], xs[t])
+        assert ids[t].tolist() == i_o.tolist(), f"route t={t}"
+        assert_bit_exact(wts[t], w_o, f"route weights t={t}")
+        counts[i_o] += 1
+    st = s14.last_prefill_stats(ctx)
+    assert st["distinct"] == int(np.count_nonzero(counts))
+    assert st["max_tokens_per_expert"] == int(counts.max())
+    assert st["items"] == int(np.sum((counts + 127) // 128)) + (T + 127) // 128
+    say(f"  stats {st}")
+    view = s14.last_prefill_view(ctx)
+    check = sorted({int(p) for t in range(0, T, 8) for p in view["token_pair"][t]})
+    _check_prefill_stages(oracle, bank, view, xs, ids, wts, y, check)
+    shared = page_host(bank, 256)
+    for t in (0, 21, 63):
+        want = oracle.moe_prefill_token(xs[t], [page_host(bank, int(e)) for e in ids[t]], wts[t], shared)
+        _prefill_close(oracle, y[t], want, f"token {t}")
+
+
+def test_prefill_config4_512_properties(ctx, oracle, bank, prefill_router):
+    """Full config-4 size.  Each token's output depends only on its own row
+    (an MFMA column does not see its neighbours), so the first 64 tokens
+    must equal a 64-token run bit for bit, whatever tiles and work items the
+    grouping gave them; repeat runs are identical; all 512 routes match the
+    oracle; and the stages of the busiest expert's pairs (items of 128
+    tokens, four column tiles) and of the shared expert's pairs check out."""
+    T = 512
+    say(f"config 4 prefill T={T}: properties, stages of the busiest experts")
+    xs = synth.prefill_tokens(seed=0, tokens=T)
+    y, ids, wts = _run_prefill(ctx, bank, prefill_router, xs)
+    st = s14.last_prefill_stats(ctx)
+    view = s14.last_prefill_view(ctx)
+    counts = np.zeros(256, np.int64)
+    for t in range(T):
+        _, i_o, w_o = oracle.route(prefill_router["wr"], prefill_router["bias"], xs[t])
+        assert ids[t].tolist() == i_o.tolist(), f"route t={t}"
+        counts[i_o] += 1
+    assert st["distinct"] == int(np.count_nonzero(counts))
+    assert st["max_tokens_per_expert"] == int(counts.max())
+    assert st["items"] == int(np.sum((counts + 127) // 128)) + (T + 127) // 128
+    say(f"  stats {st}; tokens/expert mean {counts[counts > 0].mean():.2f}")
+    busiest = int(np.argmax(counts))
+    on_busiest = np.flatnonzero((ids == busiest).any(axis=1))
+    check = [int(view["token_pair"][t][list(ids[t]).index(busiest)]) for t in on_busiest[[0, 40, -1]]]
+    check += [int(view["token_pair"][t][6]) for t in (0, 127, 128, 300, 511)]
+    _check_prefill_stages(oracle, bank, view, xs, ids, wts, y, sorted(check))
+    y2, ids2, _ = _run_prefill(ctx, bank, prefill_router, xs)
+    assert_bit_exact(y2, y, "repeat run")
+    assert np.array_equal(ids2, ids)
+    y64, ids64, _ = _run_prefill(ctx, bank, prefill_router, np.ascontiguousarray(xs[:64]))
+    assert np.array_equal(ids64, ids[:64])
+    assert_bit_exact(y64, y[:64], "first 64 tokens of T=512 vs T=64")
+    shared = page_host(bank, 256)
+    for t in (int(on_busiest[-1]), 511):
+        want = oracle.moe_prefill_token(xs[t], [page_host(bank, int(e)) for e in ids[t]], wts[t], shared)
+        _prefill_close(oracle, y[t], want, f"token {t}")
+
+
+@pytest.mark.parametrize("tokens", [1, 5, 1024])
+def test_prefill_ragged_and_max_tokens(ctx, oracle, bank, prefill_router, tokens):
+    """1 and 5 tokens (partial MFMA column tiles) and the 1024-token maximum:
+    each token's row equals its row in a separate run of a different size."""
+    say(f"prefill T={tokens} vs per-token consistency")
+    xs = synth.prefill_tokens(seed=1, tokens=tokens)
+    y, ids, wts = _run_prefill(ctx, bank, prefill_router, xs)
+    if tokens <= 5:
+        view = s14.last_prefill_view(ctx)
+        _check_prefill_stages(oracle, bank, view, xs, ids, wts, y, list(view["token_pair"][tokens - 1]))
+    pick = sorted({0, tokens // 2, tokens - 1})
+    y1, ids1, _ = _run_prefill(ctx, bank, prefill_router, np.ascontiguousarray(xs[pick]))
+    assert np.array_equal(ids1, ids[pick])
+    assert_bit_exact(y1, y[pick], f"T={tokens} rows {pick} vs a {len(pick)}-token run")
+    with pytest.raises(N.S14Error):
+        s14.moe_prefill(ctx, 1025, prefill_router["router"], bank["table"], bank["pages"][256], dev(xs[:1]),
+                        torch.empty(1, device="cuda"))
