@@ -300,14 +300,14 @@ def expert_down_requant(x, page, group: int = 32, hidden=HIDDEN, inter=INTER) ->
     return out
 
 
-def moe_prefill_token(x, routed_pages, weights, shared_page, group: int = 32) -> np.ndarray:
+def moe_prefill_token(x, routed_pages, weights, shared_page, group: int = 32, hidden=HIDDEN, inter=INTER) -> np.ndarray:
     """One token of the config-4 layer: acc = 0; acc += w_i * down_i in route
     order; acc += shared_down (s14_vulkan_numeric.rs:929-946 order), each
     down computed by expert_down_requant."""
-    acc = np.zeros(HIDDEN, dtype=np.float32)
+    acc = np.zeros(hidden, dtype=np.float32)
     for p, w in zip(routed_pages, _f32(weights)):
-        acc = (acc + np.float32(w) * expert_down_requant(x, p, group)).astype(np.float32)
-    return (acc + expert_down_requant(x, shared_page, group)).astype(np.float32)
+        acc = (acc + np.float32(w) * expert_down_requant(x, p, group, hidden, inter)).astype(np.float32)
+    return (acc + expert_down_requant(x, shared_page, group, hidden, inter)).astype(np.float32)
 
 
 def set_num_threads(n: int) -> None:

@@ -278,3 +278,58 @@ def test_requant_e4m3_against_torch(oracle):
             scaled = np.clip(blk / np.float32(2.0**want), -448, 448).astype(np.float32)
             ref = torch.from_numpy(scaled).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
             assert np.array_equal(q[r, g * 32:(g + 1) * 32], ref)
+
+
+def test_dequant_requant_against_torch(oracle):
+    """dequant_requant(q, c) = e4m3fn(q) * 2^(c - 127), decoded by torch."""
+    rng = np.random.default_rng(13)
+    q = rng.integers(0, 256, (3, 96)).astype(np.uint8)
+    q[(q & 0x7F) == 0x7F] = 0x11  # NaN codes are outside the requant's range
+    c = rng.integers(100, 150, (3, 3)).astype(np.uint8)
+    got = oracle.dequant_requant(q, c)
+    dec = torch.from_numpy(q).view(torch.float8_e4m3fn).to(torch.float64).numpy()
+    want = (dec * np.ldexp(1.0, c.astype(np.int64) - 127).repeat(32, axis=1)).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_requant_round_trip_is_exact_on_the_grid(oracle):
+    """x whose 32-groups are e4m3 values times 2^s, each group holding +-448 * 2^s:
+    the scale code is 127 + s and requant -> dequant returns x bit for bit
+    (covers normals, subnormals, zeros and both signs)."""
+    rng = np.random.default_rng(14)
+    finite = [c for c in range(256) if (c & 0x7F) != 0x7F]
+    vals = torch.tensor(finite, dtype=torch.uint8).view(torch.float8_e4m3fn).to(torch.float32).numpy()
+    x = vals[rng.integers(0, len(finite), (4, 256))].astype(np.float32)
+    s = rng.integers(-20, 12, (4, 8))
+    x[:, ::32] = np.float32(448.0) * np.where(rng.random((4, 8)) < 0.5, -1, 1)
+    x = (x * np.ldexp(np.float32(1.0), s).astype(np.float32).repeat(32, axis=1)).astype(np.float32)
+    q, c = oracle.requant_e4m3(x)
+    assert np.array_equal(c.astype(np.int64) - 127, s)
+    back = oracle.dequant_requant(q, c)
+    assert np.array_equal(np.abs(back), np.abs(x)) and np.array_equal(np.signbit(back[x != 0]), np.signbit(x[x != 0]))
+
+
+def test_prefill_token_composition(oracle):
+    """expert_down_requant = w2 . deq(req(swiglu(w1 . deq(req(x)), w3 . deq(req(x))))) through the
+    pinned matvec, swiglu and requant; the prefill token = route-order
+    combine with the shared expert last."""
+    hidden, inter = 256, 128
+    rng = np.random.default_rng(15)
+    pages = [synth.gen_mxfp4_page(6, 2, e, hidden=hidden, inter=inter) for e in range(3)]
+    shared = synth.gen_mxfp4_page(6, 2, synth.SHARED_EXPERT, hidden=hidden, inter=inter)
+    x = rng.normal(0, 1, hidden).astype(np.float32)
+    o = synth.page_offsets("mxfp4", hidden, inter)
+    p = pages[1]
+    xd = oracle.dequant_requant(*oracle.requant_e4m3(x))[0]
+    g = oracle.mxfp4_matvec(xd, p[o["w1"]:o["s1"]].reshape(inter, hidden // 2), p[o["s1"]:o["w3"]].reshape(inter, hidden // 32))
+    u = oracle.mxfp4_matvec(xd, p[o["w3"]:o["s3"]].reshape(inter, hidden // 2), p[o["s3"]:o["w2"]].reshape(inter, hidden // 32))
+    hd = oracle.dequant_requant(*oracle.requant_e4m3(oracle.swiglu_limit(g, u)))[0]
+    d = oracle.mxfp4_matvec(hd, p[o["w2"]:o["s2"]].reshape(hidden, inter // 2), p[o["s2"]:o["total"]].reshape(hidden, inter // 32))
+    assert np.array_equal(d, oracle.expert_down_requant(x, p, hidden=hidden, inter=inter))
+    w = np.array([0.5, 0.3, 0.2], dtype=np.float32)
+    y = oracle.moe_prefill_token(x, pages, w, shared, hidden=hidden, inter=inter)
+    acc = np.zeros(hidden, dtype=np.float32)
+    for wi, pg in zip(w, pages):
+        acc = (acc + wi * oracle.expert_down_requant(x, pg, hidden=hidden, inter=inter)).astype(np.float32)
+    acc = (acc + oracle.expert_down_requant(x, shared, hidden=hidden, inter=inter)).astype(np.float32)
+    assert np.array_equal(y, acc)
