@@ -987,56 +987,61 @@ __global__ __launch_bounds__(64) void k_phase1_exact(PairTable plan, Workspace w
   if (!upper && h == 0) ws.h[size_t(p) * kInter + row] = swiglu_exact(acc, other);
 }
 
-// Phase 1 FAST: 4 wavefronts per workgroup, each kP1FastRowsPerWave rows of
-// w1 and w3 (x for the lane's k slices held in registers).
+// Phase 1 FAST: 4 wavefronts per workgroup; each streams kP1FastRowsPerWave
+// row pairs (the same row of w1 and of w3) with kP1FastDepth row pairs of
+// codes in flight, x for the lane's k slices held in registers throughout.
+// The grid stays within one round of resident workgroups: a workgroup that
+// starts only when another finishes costs a whole extra load latency.
 template <bool kHostPlan, int kTier>
 __global__ __launch_bounds__(256) void k_phase1_fast(PairTable plan, Workspace ws, const float *__restrict__ X,
                                                      PageOffsets mx, PageOffsets f8) {
   constexpr int NSEG = kHidden / 2048;
   constexpr int R = kP1FastRowsPerWave;
+  constexpr int D = kP1FastDepth;
   const uint32_t p = blockIdx.y;
   const PairRef pr = phase1_pair<kHostPlan>(plan, ws.table, p);
-  XReg<NSEG> xr;
-  load_x_mx<NSEG>(xr, X + size_t(pr.token) * kHidden, kHidden);
   const uint32_t row0 = blockIdx.x * kP1FastRows + (threadIdx.x >> 6) * R;
   const Rsrc r = make_rsrc(pr.page, page_bytes(pr.fmt));
-  float g[R], u[R];
+  const int lane = threadIdx.x & 63;
+  float gv = 0.0f, uv = 0.0f;  // lane i keeps row pair i
+  XReg<NSEG> xr;
+  load_x_mx<NSEG>(xr, X + size_t(pr.token) * kHidden, kHidden);
   if (pr.fmt == S14_PAGE_MXFP4) {
-    MxRowFrag f1[R][NSEG], f3[R][NSEG];
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      const uint32_t row = row0 + i;
-      load_mx_row_frag<NSEG>(f1[i], r, uint32_t(mx.w1) + row * (kHidden / 2), r,
+    MxRowFrag f1[D][NSEG], f3[D][NSEG];
+    auto load = [&](int slot, uint32_t row) {
+      load_mx_row_frag<NSEG>(f1[slot], r, uint32_t(mx.w1) + row * (kHidden / 2), r,
                              uint32_t(mx.s1) + row * (kHidden / 32), kHidden);
-      load_mx_row_frag<NSEG>(f3[i], r, uint32_t(mx.w3) + row * (kHidden / 2), r,
+      load_mx_row_frag<NSEG>(f3[slot], r, uint32_t(mx.w3) + row * (kHidden / 2), r,
                              uint32_t(mx.s3) + row * (kHidden / 32), kHidden);
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < D && i < R; ++i) load(i, row0 + i);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      g[i] = wave_sum_dpp(mx_row_fast_partial<NSEG>(f1[i], xr));
-      u[i] = wave_sum_dpp(mx_row_fast_partial<NSEG>(f3[i], xr));
+      const int slot = i % D;
+      const float g = wave_sum_dpp(mx_row_fast_partial<NSEG>(f1[slot], xr));
+      const float u = wave_sum_dpp(mx_row_fast_partial<NSEG>(f3[slot], xr));
+      if (i + D < R) load(slot, row0 + i + D);
+      if (lane == i) {
+        gv = g;
+        uv = u;
+      }
     }
   } else {
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const uint32_t row = row0 + i;
-      g[i] = wave_sum_dpp(fp8_row_fast_partial<NSEG>(r, uint32_t(f8.w1) + row * kHidden,
-                                                     uint32_t(f8.s1) + (row / 128) * (kHidden / 128), xr));
-      u[i] = wave_sum_dpp(fp8_row_fast_partial<NSEG>(r, uint32_t(f8.w3) + row * kHidden,
-                                                     uint32_t(f8.s3) + (row / 128) * (kHidden / 128), xr));
+      const float g = wave_sum_dpp(fp8_row_fast_partial<NSEG>(r, uint32_t(f8.w1) + row * kHidden,
+                                                              uint32_t(f8.s1) + (row / 128) * (kHidden / 128), xr));
+      const float u = wave_sum_dpp(fp8_row_fast_partial<NSEG>(r, uint32_t(f8.w3) + row * kHidden,
+                                                              uint32_t(f8.s3) + (row / 128) * (kHidden / 128), xr));
+      if (lane == i) {
+        gv = g;
+        uv = u;
+      }
     }
   }
-  const int lane = threadIdx.x & 63;
-  if (lane < R) {
-    float gv = g[0], uv = u[0];
-#pragma unroll
-    for (int i = 1; i < R; ++i)
-      if (lane == i) {
-        gv = g[i];
-        uv = u[i];
-      }
-    ws.h[size_t(p) * kInter + row0 + lane] = swiglu_exact(gv, uv);
-  }
+  if (lane < R) ws.h[size_t(p) * kInter + row0 + lane] = swiglu_exact(gv, uv);
 }
 
 // What every phase-2 workgroup needs about its token, read in one round trip

@@ -23,9 +23,10 @@ constexpr int kMaxExperts = 256;
 constexpr int kP1ExactRows = 16;
 constexpr int kP2ExactRows = 16;
 constexpr int kP2ExactWaves = 4;
-// Fast-mode tiles: phase 1 = 4 wavefronts x 4 rows of w1 and w3; phase 2 =
+// Fast-mode tiles: phase 1 = 4 wavefronts x 8 rows of w1 and w3 (streamed); phase 2 =
 // 16 rows of w2 per wavefront (one wavefront per pair of the token).
-constexpr int kP1FastRowsPerWave = 4;
+constexpr int kP1FastRowsPerWave = 8;
+constexpr int kP1FastDepth = 3;  // row pairs of codes in flight per wavefront
 constexpr int kFastWaves = 4;
 constexpr int kP1FastRows = kP1FastRowsPerWave * kFastWaves;
 constexpr int kP2FastRows = 16;
