@@ -151,7 +151,7 @@ def main() -> int:
 
     def stages(fn, steps, m):
         ctx.enable_stage_timing(True)
-        acc = np.zeros(4)
+        acc = np.zeros(3)
         for i in range(steps):
             fn(i, m)
             acc += np.array(ctx.stage_times())
@@ -174,7 +174,7 @@ def main() -> int:
             r["k1"] = {
                 "us_per_token": ms1 * 1e3,
                 "hbm_gbps": layer_bytes_k1() / (ms1 * 1e-3) / 1e9,
-                "stage_ms": {"router": st1[0], "plan": st1[1], "phase1": st1[2], "phase2": st1[3]},
+                "stage_ms": {"route": st1[0], "phase1": st1[1], "phase2": st1[2]},
             }
             r["k1"]["hbm_frac"] = r["k1"]["hbm_gbps"] / HBM_PEAK_GBPS
         if args.only in ("k8", "all"):
@@ -186,7 +186,7 @@ def main() -> int:
                 "ms_per_block": ms8,
                 "distinct_pages": d,
                 "hbm_gbps": block_bytes(round(d), 8) / (ms8 * 1e-3) / 1e9,
-                "stage_ms": {"router": st8[0], "plan": st8[1], "phase1": st8[2], "phase2": st8[3]},
+                "stage_ms": {"route": st8[0], "phase1": st8[1], "phase2": st8[2]},
             }
             r["k8"]["hbm_frac"] = r["k8"]["hbm_gbps"] / HBM_PEAK_GBPS
         out[name] = r

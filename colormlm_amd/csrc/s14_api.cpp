@@ -20,7 +20,7 @@ using s14::fail;
 
 namespace {
 // stages of a fused launch timed by per-kernel start/stop events
-enum { kStageRouter = 0, kStagePlan = 1, kStagePhase1 = 2, kStagePhase2 = 3, kStages = 4 };
+enum { kStageRoute = 0, kStagePhase1 = 1, kStagePhase2 = 2, kStages = 3 };
 }  // namespace
 
 struct s14_ctx {
@@ -106,7 +106,7 @@ extern "C" int s14_ctx_create(int device, s14_ctx **out) {
     s14_ctx_destroy(ctx);
     return hip_fail(e, "hipStreamCreate");
   }
-  // workspace: table | h | scores | biased
+  // workspace: table | h | scores | biased | route counter
   size_t off = 0;
   const size_t o_table = off;
   off = align_up(off + sizeof(s14::PairTable), 256);
@@ -116,6 +116,8 @@ extern "C" int s14_ctx_create(int device, s14_ctx **out) {
   off = align_up(off + sizeof(float) * s14::kMaxTokens * s14::kMaxExperts, 256);
   const size_t o_biased = off;
   off = align_up(off + sizeof(float) * s14::kMaxTokens * s14::kMaxExperts, 256);
+  const size_t o_count = off;
+  off = align_up(off + sizeof(uint32_t) * (1 + s14::kMaxTokens), 256);
   e = hipMalloc(&ctx->ws_base, off);
   if (e != hipSuccess) {
     s14_ctx_destroy(ctx);
@@ -126,6 +128,7 @@ extern "C" int s14_ctx_create(int device, s14_ctx **out) {
   ctx->ws.h = reinterpret_cast<float *>(b + o_h);
   ctx->ws.scores = reinterpret_cast<float *>(b + o_scores);
   ctx->ws.biased = reinterpret_cast<float *>(b + o_biased);
+  ctx->ws.route_count = reinterpret_cast<uint32_t *>(b + o_count);  // zeroed below; each route launch leaves it 0
   ctx->ws.bytes = off;
   // one clear at creation, outside any launch sequence
   e = hipMemset(ctx->ws_base, 0, off);
@@ -451,8 +454,7 @@ extern "C" int s14_moe_block_route(s14_ctx *ctx, void *stream, uint32_t tokens, 
   const s14::RouteSpec rs{router_args(router), tokens, shared_format, expert_pages_dev, shared_page, ids_out,
                           weights_out};
   stage_begin(ctx);
-  hipError_t e = s14::launch_router_scores(st, ctx->ws, rs.r, tokens, x, stage_events(ctx, kStageRouter));
-  if (e == hipSuccess) e = s14::launch_plan(st, ctx->ws, rs, stage_events(ctx, kStagePlan));
+  hipError_t e = s14::launch_route(st, ctx->ws, rs, x, stage_events(ctx, kStageRoute));
   if (e != hipSuccess) return hip_fail(e, "router launch");
   return run_layer(ctx, st, nullptr, tokens * (s14::kTopK + 1), tokens, x, y, mode);
 }
@@ -485,8 +487,7 @@ extern "C" int s14_route(s14_ctx *ctx, void *stream, const s14_router *router, u
   if (!x) return fail(S14_ERR_INVALID, "NULL router input");
   hipStream_t st = pick(ctx, stream);
   const s14::RouteSpec rs{router_args(router), tokens, S14_PAGE_MXFP4, nullptr, nullptr, ids_out, weights_out};
-  hipError_t e = s14::launch_router_scores(st, ctx->ws, rs.r, tokens, x);
-  if (e == hipSuccess) e = s14::launch_plan(st, ctx->ws, rs);
+  hipError_t e = s14::launch_route(st, ctx->ws, rs, x);
   if (e != hipSuccess) return hip_fail(e, "router launch");
   if (scores_out) {
     for (uint32_t t = 0; t < tokens; ++t) {

@@ -812,12 +812,11 @@ __global__ void k_fill_page(uint8_t *__restrict__ page, uint64_t seed, uint32_t 
 // BLAS's): lane l sums k = 256c + 4l + j (c ascending, j = 0..3), then the
 // xor butterfly over lanes.  Score: sigmoid (north-star config) or
 // sqrt(softplus) with torch's threshold 20 (executor.py:642).
-__global__ __launch_bounds__(256) void k_router_scores(RouterArgs r, const float *__restrict__ X,
-                                                       float *__restrict__ scores, float *__restrict__ biased) {
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t t = blockIdx.y;
-  const uint32_t e = blockIdx.x * 4u + wave;
-  if (e >= r.n_experts) return;
+// Score of expert e for token t, computed by one whole wavefront; valid in
+// lane 0 (the biased score in .y).
+__device__ __forceinline__ float2 router_score(const RouterArgs &r, const float *__restrict__ X, uint32_t t,
+                                               uint32_t e) {
+  const uint32_t lane = threadIdx.x & 63;
   const uint32_t K = kHidden;
   const float *x = X + size_t(t) * K;
   const float *row = r.weight + size_t(e) * K;
@@ -837,51 +836,63 @@ __global__ __launch_bounds__(256) void k_router_scores(RouterArgs r, const float
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, m));
+  float sc;
+  if (r.score_fn == S14_SCORE_SIGMOID) {
+    sc = __fdiv_rn(1.0f, __fadd_rn(1.0f, s14x::expf_glibc(-acc)));
+  } else {
+    const float sp = acc > 20.0f ? acc : log1pf(s14x::expf_glibc(acc));
+    sc = __fsqrt_rn(sp);
+  }
+  return make_float2(sc, __fadd_rn(sc, r.bias[e]));
+}
+
+// Router scores only (the prefill's first step): one wavefront per (expert,
+// token).
+__global__ __launch_bounds__(256) void k_router_scores(RouterArgs r, const float *__restrict__ X,
+                                                       float *__restrict__ scores, float *__restrict__ biased) {
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t t = blockIdx.y;
+  const uint32_t e = blockIdx.x * 4u + wave;
+  if (e >= r.n_experts) return;
+  const float2 s = router_score(r, X, t, e);
   if (lane == 0) {
-    float s;
-    if (r.score_fn == S14_SCORE_SIGMOID) {
-      s = __fdiv_rn(1.0f, __fadd_rn(1.0f, s14x::expf_glibc(-acc)));
-    } else {
-      const float sp = acc > 20.0f ? acc : log1pf(s14x::expf_glibc(acc));
-      s = __fsqrt_rn(sp);
-    }
-    scores[t * kMaxExperts + e] = s;
-    biased[t * kMaxExperts + e] = __fadd_rn(s, r.bias[e]);
+    scores[t * kMaxExperts + e] = s.x;
+    biased[t * kMaxExperts + e] = s.y;
   }
 }
 
-// Plan: wavefront t selects token t's top-k of score + bias (ties to the
+// Plan of one token (one wavefront): top-k of score + bias (ties to the
 // lower index) and its weights s/sum (sum sequential in selection order)
-// times route_scale (executor.py:647-667); wavefront 0 then sorts the
-// (expert, token) pairs expert-major, appends the shared pairs and
-// publishes the pair table.  expert_pages == NULL: route only.
-__global__ __launch_bounds__(64 * kMaxTokens) void k_plan(RouteSpec rs, Workspace ws) {
-  __shared__ uint32_t ids[kMaxTokens][kTopK];
-  __shared__ float wts[kMaxTokens][kTopK];
-  __shared__ uint64_t pgs[kMaxTokens][kTopK];
+// times route_scale (executor.py:647-667), into the LDS lists.
+struct PlanLds {
+  uint32_t ids[kMaxTokens][kTopK];
+  float wts[kMaxTokens][kTopK];
+  uint64_t pgs[kMaxTokens][kTopK];
+};
+__device__ __forceinline__ void plan_token(const RouteSpec &rs, uint32_t t, const float *biased, const float *scores,
+                                           const uint64_t *pages, PlanLds &pl) {
   const uint32_t lane = threadIdx.x & 63;
-  const uint32_t t = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const RouterArgs &r = rs.r;
-  const uint32_t k = r.topk;
-  if (t < rs.tokens) {
-    const TopK c = select_topk(ws.biased + t * kMaxExperts, ws.scores + t * kMaxExperts, rs.expert_pages,
-                               r.n_experts, k);
-    if (lane < k) {
-      const float wgt = route_weight(c, r.route_scale);
-      ids[t][lane] = c.id;
-      wts[t][lane] = wgt;
-      pgs[t][lane] = c.page;
-      if (rs.ids_out) rs.ids_out[t * k + lane] = uint16_t(c.id);
-      if (rs.weights_out) rs.weights_out[t * k + lane] = wgt;
-    }
+  const uint32_t k = rs.r.topk;
+  const TopK c = select_topk(biased, scores, pages, rs.r.n_experts, k);
+  if (lane < k) {
+    const float wgt = route_weight(c, rs.r.route_scale);
+    pl.ids[t][lane] = c.id;
+    pl.wts[t][lane] = wgt;
+    pl.pgs[t][lane] = c.page;
+    if (rs.ids_out) rs.ids_out[t * k + lane] = uint16_t(c.id);
+    if (rs.weights_out) rs.weights_out[t * k + lane] = wgt;
   }
-  if (!rs.expert_pages) return;  // route only (uniform: no barrier below is skipped by part of the group)
-  __syncthreads();
-  if (t != 0) return;
+}
+
+// Publication of the pair table by one wavefront: the (expert, token) pairs
+// sorted expert-major, the shared pairs appended, the per-token slot records.
+__device__ __forceinline__ void plan_publish(const RouteSpec &rs, PairTable *tab, const PlanLds &pl) {
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t k = rs.r.topk;
   const uint32_t T = rs.tokens, npr = T * k;  // routed pairs, <= 48
   const bool mine = lane < npr;
   const uint32_t mt = mine ? lane / k : 0u, mr = mine ? lane % k : 0u;
-  const uint32_t me = mine ? ids[mt][mr] : 0u;
+  const uint32_t me = mine ? pl.ids[mt][mr] : 0u;
   const uint32_t key = mine ? me * 8u + mt : 0xffffffffu;  // unique: an expert appears once per token
   uint32_t rank = 0, first = 1;
   for (uint32_t j = 0; j < npr; ++j) {
@@ -889,16 +900,15 @@ __global__ __launch_bounds__(64 * kMaxTokens) void k_plan(RouteSpec rs, Workspac
     rank += kj < key ? 1u : 0u;
     if ((kj >> 3) == (key >> 3) && kj < key) first = 0;
   }
-  PairTable *tab = ws.table;
   if (mine) {
-    const uint64_t pg = pgs[mt][mr];
+    const uint64_t pg = pl.pgs[mt][mr];
     tab->page[rank] = pg;
     tab->fmt[rank] = S14_PAGE_MXFP4;
     tab->token[rank] = mt;
     tab->slot_pair[mt][mr] = rank;
     tab->slot_page[mt][mr] = pg;
     tab->slot_fmt[mt][mr] = S14_PAGE_MXFP4;
-    tab->slot_weight[mt][mr] = wts[mt][mr];
+    tab->slot_weight[mt][mr] = pl.wts[mt][mr];
     tab->slot_shared[mt][mr] = 0u;
   }
   const uint64_t firsts = __ballot(mine && first);
@@ -921,6 +931,77 @@ __global__ __launch_bounds__(64 * kMaxTokens) void k_plan(RouteSpec rs, Workspac
     tab->n_distinct = uint32_t(__popcll(firsts));
     tab->chain = 0u;
   }
+}
+
+// Router and plan in one launch.  Every workgroup scores kRouteWaves experts
+// of one token; the last workgroup to finish (a device-scope counter in the
+// workspace, which that workgroup resets) gathers all scores, selects every
+// token's top-k (one wavefront per token) and publishes the pair table.
+// expert_pages == NULL: route only.  Saves a dependent kernel launch per
+// layer.
+constexpr int kRouteWaves = kMaxTokens;
+__global__ __launch_bounds__(64 * kRouteWaves) void k_route(RouteSpec rs, Workspace ws, const float *__restrict__ X) {
+  __shared__ float sc[kMaxTokens][kMaxExperts];
+  __shared__ float bs[kMaxTokens][kMaxExperts];
+  __shared__ uint64_t pages[kMaxExperts];
+  __shared__ PlanLds pl;
+  __shared__ uint32_t is_last;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t t = blockIdx.y;
+  const uint32_t e = blockIdx.x * kRouteWaves + wave;
+  if (e < rs.r.n_experts) {
+    const float2 s = router_score(rs.r, X, t, e);
+    if (lane == 0) {
+      // device-coherent stores (no cache writeback needed to publish them)
+      __hip_atomic_store(&ws.scores[t * kMaxExperts + e], s.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&ws.biased[t * kMaxExperts + e], s.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // this wavefront's stores complete before the count (a device-scope
+  // release fence would write the whole L2 back: measured several us)
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  // two-level count (per token, then tokens) so that no counter takes more
+  // than gridDim.x increments; each level's last workgroup resets its counter
+  if (threadIdx.x == 0) {
+    uint32_t *tok = ws.route_count + 1 + t;
+    bool last = __hip_atomic_fetch_add(tok, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    if (last) {
+      __hip_atomic_store(tok, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = __hip_atomic_fetch_add(ws.route_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.y - 1;
+      if (last) __hip_atomic_store(ws.route_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    is_last = last;
+  }
+  __syncthreads();
+  if (!is_last) return;  // uniform per workgroup
+  // gather every (token, expert) score and the page table: all loads issued
+  // before any is used
+  constexpr int kPer = kMaxTokens * kMaxExperts / (64 * kRouteWaves);
+  const uint32_t T = rs.tokens;
+  const bool with_pages = rs.expert_pages != nullptr;
+  const uint64_t pg = (with_pages && threadIdx.x < rs.r.n_experts) ? rs.expert_pages[threadIdx.x] : 0ull;
+  float gs[kPer], gb[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const uint32_t i = threadIdx.x + j * 64u * kRouteWaves;  // token i / 256, expert i % 256
+    const bool in = i / kMaxExperts < T;
+    gs[j] = in ? __hip_atomic_load(&ws.scores[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+    gb[j] = in ? __hip_atomic_load(&ws.biased[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const uint32_t i = threadIdx.x + j * 64u * kRouteWaves;
+    sc[i / kMaxExperts][i % kMaxExperts] = gs[j];
+    bs[i / kMaxExperts][i % kMaxExperts] = gb[j];
+  }
+  if (threadIdx.x < kMaxExperts) pages[threadIdx.x] = pg;
+  __syncthreads();
+  if (wave < T) plan_token(rs, wave, bs[wave], sc[wave], with_pages ? pages : nullptr, pl);
+  if (!rs.expert_pages) return;  // route only (uniform)
+  __syncthreads();
+  if (wave == 0) plan_publish(rs, ws.table, pl);
 }
 
 // Pair p of phase 1: from the host plan (by value; workgroup (0,0) also
@@ -1295,8 +1376,9 @@ hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const Router
   return hipGetLastError();
 }
 
-hipError_t launch_plan(hipStream_t s, const Workspace &ws, const RouteSpec &rs, KernelEvents ev) {
-  hipExtLaunchKernelGGL(k_plan, dim3(1), dim3(64 * kMaxTokens), 0, s, ev.start, ev.stop, 0, rs, ws);
+hipError_t launch_route(hipStream_t s, const Workspace &ws, const RouteSpec &rs, const float *x, KernelEvents ev) {
+  hipExtLaunchKernelGGL(k_route, dim3((rs.r.n_experts + kRouteWaves - 1) / kRouteWaves, rs.tokens),
+                        dim3(64 * kRouteWaves), 0, s, ev.start, ev.stop, 0, rs, ws, x);
   return hipGetLastError();
 }
 

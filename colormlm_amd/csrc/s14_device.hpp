@@ -77,6 +77,7 @@ struct Workspace {
   float *h;       // [kMaxPairs][kInter]
   float *scores;  // [kMaxTokens][kMaxExperts]
   float *biased;  // [kMaxTokens][kMaxExperts]
+  uint32_t *route_count;  // [1 + kMaxTokens]: tokens, then per-token workgroups, of the running route launch that are done
   size_t bytes;
 };
 
@@ -125,17 +126,19 @@ hipError_t launch_fill_mxfp4_page(hipStream_t s, uint8_t *page, uint64_t seed, u
                                   uint32_t expert, uint32_t hidden, uint32_t inter, int lo, int hi,
                                   const PageOffsets &off);
 
-// --- fused layer / block path: router -> plan -> phase 1 -> phase 2 ---
-// Scores and biased scores of every (token, expert) into ws.scores/biased.
+// --- fused layer / block path: route (router + plan) -> phase 1 -> phase 2 ---
+// Scores and biased scores of every (token, expert) into ws.scores/biased
+// (the prefill's router; the layer path uses launch_route).
 hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const RouterArgs &r,
                                 uint32_t tokens, const float *x, KernelEvents ev = {});
-// Top-k and weights of every token (after launch_router_scores) to
-// rs.ids_out/weights_out when given; with rs.expert_pages also the pair
-// table in ws.table.
-hipError_t launch_plan(hipStream_t s, const Workspace &ws, const RouteSpec &rs, KernelEvents ev = {});
+// Scores, then the top-k and weights of every token to rs.ids_out /
+// weights_out when given; with rs.expert_pages also the pair table in
+// ws.table.  One launch (the last workgroup plans).
+hipError_t launch_route(hipStream_t s, const Workspace &ws, const RouteSpec &rs, const float *x,
+                        KernelEvents ev = {});
 // w1/w3 + SwiGLU of every pair.  host_plan != NULL: the pairs are given and
 // workgroup (0,0) publishes them for phase 2; otherwise they are read from
-// the table launch_plan wrote.
+// the table launch_route wrote.
 hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *host_plan,
                          uint32_t n_pairs, uint32_t tokens, const PageOffsets &mx,
                          const PageOffsets &fp8, const float *x, int mode, KernelEvents ev = {});

@@ -140,8 +140,8 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// Wavefront max / min of a u32 (DPP row steps, then lane 63), returned to
-// every lane.  Lanes without a DPP source contribute the identity.
+// Wavefront max of a u32 (DPP row steps, then lane 63), returned to every
+// lane.  Lanes without a DPP source contribute the identity.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   v = max(v, uint32_t(dpp_i<0xb1>(0, int(v))));
   v = max(v, uint32_t(dpp_i<0x4e>(0, int(v))));
@@ -149,15 +149,6 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   v = max(v, uint32_t(dpp_i<0x118>(0, int(v))));
   v = max(v, uint32_t(dpp_i<0x142, 0xa>(0, int(v))));
   v = max(v, uint32_t(dpp_i<0x143, 0xc>(0, int(v))));
-  return uint32_t(__builtin_amdgcn_readlane(int(v), 63));
-}
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-  v = min(v, uint32_t(dpp_i<0xb1>(-1, int(v))));
-  v = min(v, uint32_t(dpp_i<0x4e>(-1, int(v))));
-  v = min(v, uint32_t(dpp_i<0x114>(-1, int(v))));
-  v = min(v, uint32_t(dpp_i<0x118>(-1, int(v))));
-  v = min(v, uint32_t(dpp_i<0x142, 0xa>(-1, int(v))));
-  v = min(v, uint32_t(dpp_i<0x143, 0xc>(-1, int(v))));
   return uint32_t(__builtin_amdgcn_readlane(int(v), 63));
 }
 
@@ -204,12 +195,18 @@ __device__ __forceinline__ TopK select_topk(const float *__restrict__ biased, co
 #pragma unroll
   for (uint32_t i = 0; i < uint32_t(kTopK); ++i) {
     if (i >= k) break;
-    // max key over the wavefront, then the lowest expert index holding it
+    // max key over the wavefront, then the lowest expert index holding it:
+    // expert lane + 64 j, so the first j whose ballot is non-empty, at its
+    // lowest lane
     const uint32_t top = wave_max_u32(max(max(kv[0], kv[1]), max(kv[2], kv[3])));
-    uint32_t idx = 0xffffffffu;
-#pragma unroll
-    for (int j = 3; j >= 0; --j) idx = kv[j] == top ? lane + 64u * j : idx;
-    const int best = int(wave_min_u32(idx));
+    // (scalar selects, no branches: the masks are wavefront-uniform)
+    constexpr uint64_t kHi = 1ull << 63;
+    const uint64_t m0 = __ballot(kv[0] == top), m1 = __ballot(kv[1] == top);
+    const uint64_t m2 = __ballot(kv[2] == top), m3 = __ballot(kv[3] == top);
+    int best = 192 + __builtin_ctzll(m3 | kHi);
+    best = m2 ? 128 + __builtin_ctzll(m2 | kHi) : best;
+    best = m1 ? 64 + __builtin_ctzll(m1 | kHi) : best;
+    best = m0 ? __builtin_ctzll(m0 | kHi) : best;
     float cand = sv[0];
     uint64_t cpg = pv[0];
 #pragma unroll

@@ -91,7 +91,7 @@ class Context:
         check(lib().s14_ctx_enable_stage_timing(self._h, 1 if enable else 0))
 
     def stage_times(self):
-        """Kernel ms of {router scores, plan, phase 1, phase 2} of the last
+        """Kernel ms of {route (router + plan), phase 1, phase 2} of the last
         fused launch (0 for a stage it did not run)."""
         ms = (C.c_float * 4)()
         n = C.c_uint32()

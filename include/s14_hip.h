@@ -98,10 +98,10 @@ int s14_ctx_synchronize(s14_ctx *ctx);
  * s14_vulkan_numeric.rs:1088-1101): when enabled, each fused entry point
  * (chain, layer, block) attaches start/stop hipEvents to each of its kernel
  * launches, timing the kernels' own execution.  s14_ctx_stage_times waits
- * for the last such launch and returns up to 4 stage durations in ms:
- * {router scores, plan, phase 1 (w1, w3, SwiGLU), phase 2 (w2, mix)}; a
- * stage the last launch did not run (chain and given-route layers have no
- * router or plan) reads 0. */
+ * for the last such launch and returns up to 3 stage durations in ms:
+ * {route (router scores and top-k plan, one launch), phase 1 (w1, w3,
+ * SwiGLU), phase 2 (w2, mix)}; a stage the last launch did not run (chain
+ * and given-route layers have no route) reads 0. */
 int s14_ctx_enable_stage_timing(s14_ctx *ctx, int enable);
 int s14_ctx_stage_times(s14_ctx *ctx, float *ms, uint32_t cap, uint32_t *n_stages);
 
