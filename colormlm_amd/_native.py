@@ -149,13 +149,15 @@ class PrefillView(C.Structure):
     _fields_ = [
         ("xq", C.c_void_p),
         ("xs", C.c_void_p),
-        ("hq", C.c_void_p),
-        ("hs", C.c_void_p),
+        ("ht", C.c_void_p),
+        ("hts", C.c_void_p),
         ("down", C.c_void_p),
         ("pair_token", C.c_void_p),
         ("token_pair", C.c_void_p),
+        ("items", C.c_void_p),
         ("tokens", C.c_uint32),
         ("n_pairs", C.c_uint32),
+        ("n_items", C.c_uint32),
     ]
 
 

@@ -528,8 +528,11 @@ int prefill_workspace(s14_ctx *ctx) {
   const size_t o_tp = take(sizeof(uint32_t) * T * kSlots);
   const size_t o_xq = take(size_t(T) * kHidden);
   const size_t o_xs = take(size_t(T) * (kHidden / 32));
-  const size_t o_hq = take(size_t(P) * kInter);
-  const size_t o_hs = take(size_t(P) * (kInter / 32));
+  const size_t n_items = prefill_max_items(T);
+  const size_t o_xt = take(n_items * kXTileBytes);
+  const size_t o_xts = take(n_items * kXScaleBytes);
+  const size_t o_ht = take(n_items * kHTileBytes);
+  const size_t o_hts = take(n_items * kHScaleBytes);
   const size_t o_down = take(sizeof(float) * size_t(P) * kHidden);
   S14_HIP(hipSetDevice(ctx->device), "hipSetDevice");
   S14_HIP(hipMalloc(&ctx->prefill_base, off), "hipMalloc(prefill workspace)");
@@ -546,8 +549,10 @@ int prefill_workspace(s14_ctx *ctx) {
   w.token_pair = reinterpret_cast<uint32_t *>(b + o_tp);
   w.xq = b + o_xq;
   w.xs = b + o_xs;
-  w.hq = b + o_hq;
-  w.hs = b + o_hs;
+  w.xt = b + o_xt;
+  w.xts = b + o_xts;
+  w.ht = b + o_ht;
+  w.hts = b + o_hts;
   w.down = reinterpret_cast<float *>(b + o_down);
   w.bytes = off;
   return S14_OK;
@@ -609,7 +614,17 @@ extern "C" int s14_last_prefill_view(s14_ctx *ctx, s14_prefill_view *out) {
   uint32_t st[4];
   S14_HIP(hipMemcpy(st, ctx->pws.stats, sizeof(st), hipMemcpyDeviceToHost), "hipMemcpy(prefill stats)");
   const s14::PrefillWorkspace &w = ctx->pws;
-  *out = s14_prefill_view{w.xq, w.xs, w.hq, w.hs, w.down, w.pair_token, w.token_pair, ctx->prefill_tokens, st[3]};
+  *out = s14_prefill_view{w.xq,
+                          w.xs,
+                          w.ht,
+                          w.hts,
+                          w.down,
+                          w.pair_token,
+                          w.token_pair,
+                          reinterpret_cast<const uint32_t *>(w.items),
+                          ctx->prefill_tokens,
+                          st[3],
+                          st[0]};
   return S14_OK;
 }
 

@@ -812,6 +812,18 @@ __global__ void k_fill_page(uint8_t *__restrict__ page, uint64_t seed, uint32_t 
 // BLAS's): lane l sums k = 256c + 4l + j (c ascending, j = 0..3), then the
 // xor butterfly over lanes.  Score: sigmoid (north-star config) or
 // sqrt(softplus) with torch's threshold 20 (executor.py:642).
+// Score and biased score of expert e from its logit.
+__device__ __forceinline__ float2 router_finish(const RouterArgs &r, float logit, uint32_t e) {
+  float sc;
+  if (r.score_fn == S14_SCORE_SIGMOID) {
+    sc = __fdiv_rn(1.0f, __fadd_rn(1.0f, s14x::expf_glibc(-logit)));
+  } else {
+    const float sp = logit > 20.0f ? logit : log1pf(s14x::expf_glibc(logit));
+    sc = __fsqrt_rn(sp);
+  }
+  return make_float2(sc, __fadd_rn(sc, r.bias[e]));
+}
+
 // Score of expert e for token t, computed by one whole wavefront; valid in
 // lane 0 (the biased score in .y).
 __device__ __forceinline__ float2 router_score(const RouterArgs &r, const float *__restrict__ X, uint32_t t,
@@ -836,26 +848,64 @@ __device__ __forceinline__ float2 router_score(const RouterArgs &r, const float 
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, m));
-  float sc;
-  if (r.score_fn == S14_SCORE_SIGMOID) {
-    sc = __fdiv_rn(1.0f, __fadd_rn(1.0f, s14x::expf_glibc(-acc)));
-  } else {
-    const float sp = acc > 20.0f ? acc : log1pf(s14x::expf_glibc(acc));
-    sc = __fsqrt_rn(sp);
-  }
-  return make_float2(sc, __fadd_rn(sc, r.bias[e]));
+  return router_finish(r, acc, e);
 }
 
-// Router scores only (the prefill's first step): one wavefront per (expert,
-// token).
-__global__ __launch_bounds__(256) void k_router_scores(RouterArgs r, const float *__restrict__ X,
+// Router scores of many tokens (the prefill's first step): one wavefront per
+// tile of kRtE experts x kRtT tokens, every logit summed in router_score's
+// order (bit-identical), each weight and x chunk loaded once per tile
+// instead of once per (expert, token).
+constexpr uint32_t kRtE = 8, kRtT = 8;
+__global__ __launch_bounds__(256) void k_router_scores(RouterArgs r, uint32_t tokens, const float *__restrict__ X,
                                                        float *__restrict__ scores, float *__restrict__ biased) {
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t t = blockIdx.y;
-  const uint32_t e = blockIdx.x * 4u + wave;
-  if (e >= r.n_experts) return;
-  const float2 s = router_score(r, X, t, e);
-  if (lane == 0) {
+  const uint32_t e0 = (blockIdx.x * 4u + wave) * kRtE, t0 = blockIdx.y * kRtT;
+  if (e0 >= r.n_experts) return;
+  const float *wrow[kRtE];
+  const float *xrow[kRtT];
+#pragma unroll
+  for (uint32_t i = 0; i < kRtE; ++i) wrow[i] = r.weight + size_t(min(e0 + i, r.n_experts - 1)) * kHidden + lane * 4;
+#pragma unroll
+  for (uint32_t j = 0; j < kRtT; ++j) xrow[j] = X + size_t(min(t0 + j, tokens - 1)) * kHidden + lane * 4;
+  float acc[kRtE][kRtT];
+#pragma unroll
+  for (uint32_t i = 0; i < kRtE; ++i)
+#pragma unroll
+    for (uint32_t j = 0; j < kRtT; ++j) acc[i][j] = 0.0f;
+#pragma unroll 2
+  for (uint32_t c = 0; c < kHidden / 256; ++c) {
+    float4 wv[kRtE], xv[kRtT];
+#pragma unroll
+    for (uint32_t i = 0; i < kRtE; ++i) wv[i] = *reinterpret_cast<const float4 *>(wrow[i] + c * 256);
+#pragma unroll
+    for (uint32_t j = 0; j < kRtT; ++j) xv[j] = *reinterpret_cast<const float4 *>(xrow[j] + c * 256);
+#pragma unroll
+    for (uint32_t i = 0; i < kRtE; ++i)
+#pragma unroll
+      for (uint32_t j = 0; j < kRtT; ++j) {
+        float a = acc[i][j];
+        a = __fadd_rn(a, __fmul_rn(wv[i].x, xv[j].x));
+        a = __fadd_rn(a, __fmul_rn(wv[i].y, xv[j].y));
+        a = __fadd_rn(a, __fmul_rn(wv[i].z, xv[j].z));
+        a = __fadd_rn(a, __fmul_rn(wv[i].w, xv[j].w));
+        acc[i][j] = a;
+      }
+  }
+  // the same xor butterfly per logit; afterwards every lane holds all of
+  // them and lane i * kRtT + j finishes logit (i, j)
+  float mine = 0.0f;
+#pragma unroll
+  for (uint32_t i = 0; i < kRtE; ++i)
+#pragma unroll
+    for (uint32_t j = 0; j < kRtT; ++j) {
+      float a = acc[i][j];
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) a = __fadd_rn(a, __shfl_xor(a, m));
+      mine = lane == i * kRtT + j ? a : mine;
+    }
+  const uint32_t e = e0 + lane / kRtT, t = t0 + lane % kRtT;
+  if (e < r.n_experts && t < tokens) {
+    const float2 s = router_finish(r, mine, e);
     scores[t * kMaxExperts + e] = s.x;
     biased[t * kMaxExperts + e] = s.y;
   }
@@ -1371,8 +1421,8 @@ hipError_t launch_fill_mxfp4_page(hipStream_t s, uint8_t *page, uint64_t seed, u
 
 hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const RouterArgs &r, uint32_t tokens,
                                 const float *x, KernelEvents ev) {
-  hipExtLaunchKernelGGL(k_router_scores, dim3((r.n_experts + 3) / 4, tokens), dim3(256), 0, s, ev.start, ev.stop, 0,
-                        r, x, ws.scores, ws.biased);
+  hipExtLaunchKernelGGL(k_router_scores, dim3((r.n_experts + 4 * kRtE - 1) / (4 * kRtE), (tokens + kRtT - 1) / kRtT),
+                        dim3(256), 0, s, ev.start, ev.stop, 0, r, tokens, x, ws.scores, ws.biased);
   return hipGetLastError();
 }
 

@@ -231,6 +231,34 @@ __global__ __launch_bounds__(1024) void k_prefill_group(PrefillArgs a, PrefillWo
 // grouped GEMMs
 // ---------------------------------------------------------------------------
 
+// Each work item's x rows (MFMA order, from requant_x) into the item's tile,
+// zero past its count.  One thread per 16 tile bytes; the thread holding
+// part 0 of the first step of a chunk also writes that chunk's scale word.
+__global__ __launch_bounds__(256) void k_tile_x(PrefillWorkspace ws) {
+  constexpr uint32_t kPerItem = kXTileBytes / 16;
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t i = gid / kPerItem;
+  if (i >= ws.stats[0]) return;
+  const uint32_t r = gid % kPerItem;
+  const uint32_t lane = r & 63u, part = (r >> 6) & 1u, s = r >> 7;
+  const uint32_t col = lane & 31u, h = lane >> 5;
+  const PrefillItem it = ws.items[i];
+  const bool live = col < it.count;
+  const uint32_t t = live ? ws.pair_token[it.first + col] : 0u;
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (live) v = *reinterpret_cast<const uint4 *>(ws.xq + size_t(t) * kHidden + 64u * s + 32u * h + 16u * part);
+  *reinterpret_cast<uint4 *>(ws.xt + size_t(i) * kXTileBytes + 16u * r) = v;
+  if (part == 0 && s % kChunkSteps == 0) {
+    uint32_t word = 0;
+    if (live) {
+      const uint8_t *sc = ws.xs + size_t(t) * (kHidden / kQGroup) + 2u * s + h;  // group 2 (s + k) + h
+#pragma unroll
+      for (uint32_t k = 0; k < kChunkSteps; ++k) word |= uint32_t(sc[2u * k]) << (8u * k);
+    }
+    reinterpret_cast<uint32_t *>(ws.xts + size_t(i) * kXScaleBytes)[(s / kChunkSteps) * 64u + lane] = word;
+  }
+}
+
 __device__ __forceinline__ Rsrc page_rsrc(const PrefillArgs &a, uint32_t e) {
   const uint8_t *page = e < kMaxExperts ? reinterpret_cast<const uint8_t *>(a.expert_pages[e]) : a.shared_page;
   return make_rsrc(page, uint32_t(S14_EXPERT_PAGE_BYTES));
@@ -256,194 +284,293 @@ __device__ __forceinline__ void mfma_settle(v16f (&acc)[NT]) {
   for (int j = 0; j < NT; ++j) asm volatile("" : "+a"(acc[j]));
 }
 
-template <int NT>
-struct BStep {
-  uint4 lo[NT], hi[NT];
-  uint32_t sc[NT];
-};
+// Weight operand through LDS.  A wavefront streams its 32-row weight tile in
+// chunks of kChunkSteps K steps (128 bytes of each row): the DMA form of the
+// buffer load (buffer_load_dwordx4 ... lds) writes each chunk into a ring
+// slot with 8 lanes per row, so every quarter-wave reads 256 contiguous bytes
+// of two rows; the MFMA then reads one 16-byte piece of 32 rows from LDS.
+// Loading the MFMA layout straight from HBM instead has each quarter-wave
+// touch 16 rows: the vector L1 then handles one 64-byte sector per 16 useful
+// bytes and, not HBM, bounds the kernel.  Row r's piece q sits at piece
+// q ^ swz(r) of its 128 bytes, so the 16 rows of a read pass land in
+// distinct banks.  Each slot is its own LDS array, which lets the compiler
+// wait for one slot's DMA loads without draining the others.
+__device__ __forceinline__ uint32_t swz(uint32_t r) { return (r + (r >> 3)) & 7u; }
+// The same for the phase-2 scale tile (64-byte rows, 4 pieces).
+__device__ __forceinline__ uint32_t swz4(uint32_t r) { return (r + (r >> 2)) & 3u; }
 
-// B operands of step s for NT token tiles: lane (c, h) loads 32 bytes of
-// its token's requantised row at 64 s + 32 h and the scale of block 2 s + h.
-// Columns past the item's token count read token 0's row (never stored).
-template <int NT>
-__device__ __forceinline__ void load_b(BStep<NT> &b, const uint8_t *__restrict__ q, const uint8_t *__restrict__ sc,
-                                       const uint32_t (&row)[NT], uint32_t row_bytes, uint32_t s, uint32_t h) {
-#pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    const uint4 *p = reinterpret_cast<const uint4 *>(q + size_t(row[j]) * row_bytes + 64u * s + 32u * h);
-    b.lo[j] = p[0];
-    b.hi[j] = p[1];
-    b.sc[j] = sc[size_t(row[j]) * (row_bytes / kQGroup) + 2u * s + h];
-  }
+constexpr uint32_t kUpSlotBytes = 2 * 32 * 128;  // w1 and w3 chunks
+constexpr uint32_t kDnSlotBytes = 32 * 128;      // w2 chunk
+__shared__ __attribute__((aligned(16))) uint8_t up_slot0[kUpSlotBytes];
+__shared__ __attribute__((aligned(16))) uint8_t up_slot1[kUpSlotBytes];
+__shared__ __attribute__((aligned(16))) uint8_t up_slot2[kUpSlotBytes];
+__shared__ __attribute__((aligned(16))) uint8_t up_slot3[kUpSlotBytes];
+__shared__ __attribute__((aligned(16))) uint8_t up_scales[2 * 32 * (kHidden / 32)];  // s1, s3 of the tile
+__shared__ __attribute__((aligned(16))) uint8_t dn_slot0[kDnSlotBytes];
+__shared__ __attribute__((aligned(16))) uint8_t dn_slot1[kDnSlotBytes];
+__shared__ __attribute__((aligned(16))) uint8_t dn_slot2[kDnSlotBytes];
+__shared__ __attribute__((aligned(16))) uint8_t dn_slot3[kDnSlotBytes];
+__shared__ __attribute__((aligned(16))) uint8_t dn_scales[32 * (kInter / 32)];  // s2 of the tile
+
+template <int S>
+struct Slot {
+  static constexpr int value = S;
+};
+template <int S>
+__device__ __forceinline__ uint8_t *up_slot() {
+  if constexpr (S == 0) return up_slot0;
+  else if constexpr (S == 1) return up_slot1;
+  else if constexpr (S == 2) return up_slot2;
+  else return up_slot3;
+}
+template <int S>
+__device__ __forceinline__ uint8_t *dn_slot() {
+  if constexpr (S == 0) return dn_slot0;
+  else if constexpr (S == 1) return dn_slot1;
+  else if constexpr (S == 2) return dn_slot2;
+  else return dn_slot3;
 }
 
-// Phase 1: one wavefront per (32-row tile of w1/w3, work item of <= 128
-// tokens of one expert).  K loop of 64 steps, NT token tiles at once; then
-// h = swiglu(g, u), requantised per token over the tile's 32 rows (one E8M0
-// group of phase 2's K) and stored in MFMA order.
-template <int NT>
-__device__ __forceinline__ void prefill_up_tiles(const PrefillArgs &a, const PrefillWorkspace &ws,
-                                                 const PrefillItem &it, uint32_t rt) {
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ __forceinline__ void dma16(Rsrc r, uint8_t *lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(lds), 16, off, 0, 0, 0);
+}
+// Before a DMA load refills a slot: the LDS reads of its previous chunk
+// have returned (they fed MFMAs already issued; this makes it explicit).
+__device__ __forceinline__ void lds_reads_done() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+// Activation operand: a VGPR ring of kRing chunks, each refilled right after
+// its last use, from the item tile (two coalesced 1 KiB loads per step).
+constexpr int kRing = 4;
+struct BChunk {
+  uint4 lo[kChunkSteps], hi[kChunkSteps];
+  uint32_t sc;  // byte k: scale of step k for this lane's half
+};
+__device__ __forceinline__ void load_bchunk(BChunk &b, Rsrc tile, Rsrc scales, uint32_t c, uint32_t lane) {
+#pragma unroll
+  for (uint32_t k = 0; k < kChunkSteps; ++k) {
+    const uint32_t s = c * kChunkSteps + k;
+    b.lo[k] = ld16(tile, 2048u * s + 16u * lane);
+    b.hi[k] = ld16(tile, 2048u * s + 1024u + 16u * lane);
+  }
+  b.sc = ld4(scales, (c * 64u + lane) * 4u);
+}
+
+// Phase 1: one wavefront per (32-row tile of w1/w3, work item of <= 32
+// pairs of one expert).  K = 4096 in 16 chunks; weights kRing - 1 chunks
+// ahead in LDS, activations kRing chunks ahead in VGPRs.  Then h =
+// swiglu(g, u), requantised per token over the tile's 32 rows (one E8M0
+// group of phase 2's K) and stored into the item's phase-2 tile.
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_prefill_up(PrefillArgs a,
+                                                                                                PrefillWorkspace ws) {
+  const uint32_t n_items = ws.stats[0];
+  const uint32_t item = blockIdx.y;
+  if (item >= n_items) return;
+  const PrefillItem it = ws.items[item];
+  const uint32_t rt = blockIdx.x;
   const uint32_t lane = threadIdx.x & 63, col = lane & 31, h = lane >> 5;
   const Rsrc rp = page_rsrc(a, it.expert);
-  const uint32_t row = rt * 32u + col;  // A row of this lane
-  const uint32_t w1 = uint32_t(a.mx.w1) + row * (kHidden / 2) + 16u * h;
-  const uint32_t w3 = uint32_t(a.mx.w3) + row * (kHidden / 2) + 16u * h;
-  const uint32_t s1 = uint32_t(a.mx.s1) + row * (kHidden / 32) + h;
-  const uint32_t s3 = uint32_t(a.mx.s3) + row * (kHidden / 32) + h;
-  uint32_t xrow[NT];
+  constexpr uint32_t kRowBytes = kHidden / 2, kScaleRow = kHidden / 32;
+  constexpr uint32_t kChunks = kHidden / 64 / kChunkSteps;
+  // DMA lane map: load j of a chunk covers rows 8j..8j+7 of the tile, lane
+  // -> row 8j + lane/8, piece (lane % 8) ^ swz(row) (swz(8j + r) = (j + r) % 8)
+  const uint32_t lrow = lane >> 3;
+  uint32_t dma_off[4];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    const uint32_t i = 32u * j + col;
-    xrow[j] = ws.pair_token[it.first + (i < it.count ? i : 0u)];
-  }
-  v16f g[NT], u[NT];
+  for (uint32_t j = 0; j < 4; ++j)
+    dma_off[j] = (rt * 32u + 8u * j + lrow) * kRowBytes + 16u * ((lane & 7u) ^ ((j + lrow) & 7u));
+  const uint32_t w1 = uint32_t(a.mx.w1), w3 = uint32_t(a.mx.w3);
+  auto issue = [&](auto slot_tag, uint32_t c) {
+    uint8_t *dst = up_slot<decltype(slot_tag)::value>();
+    lds_reads_done();
 #pragma unroll
-  for (int j = 0; j < NT; ++j)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) g[j][i] = u[j][i] = 0.0f;
-  uint4 a1 = ld16(rp, w1), a3 = ld16(rp, w3);
-  uint32_t c1 = ld1(rp, s1), c3 = ld1(rp, s3);
-  BStep<NT> b;
-  load_b<NT>(b, ws.xq, ws.xs, xrow, kHidden, 0, h);
-  constexpr uint32_t kSteps = kHidden / 64;
-  for (uint32_t s = 0; s < kSteps; ++s) {
-    // next step's operands in flight during this step's MFMAs (past the
-    // last step: reads inside the page or of token rows, never consumed)
-    const uint32_t sn = s + 1 < kSteps ? s + 1 : s;
-    const uint4 na1 = ld16(rp, w1 + 32u * sn), na3 = ld16(rp, w3 + 32u * sn);
-    const uint32_t nc1 = ld1(rp, s1 + 2u * sn), nc3 = ld1(rp, s3 + 2u * sn);
-    BStep<NT> nb;
-    load_b<NT>(nb, ws.xq, ws.xs, xrow, kHidden, sn, h);
-    const v8i A1 = a_operand(a1), A3 = a_operand(a3);
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const v8i B = b_operand(b.lo[j], b.hi[j]);
-      g[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A1, B, g[j], 4, 0, 0, int(c1), 0, int(b.sc[j]));
-      u[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A3, B, u[j], 4, 0, 0, int(c3), 0, int(b.sc[j]));
+    for (uint32_t j = 0; j < 4; ++j) {
+      dma16(rp, dst + 1024u * j, w1 + dma_off[j] + 128u * c);
+      dma16(rp, dst + 4096u + 1024u * j, w3 + dma_off[j] + 128u * c);
     }
-    a1 = na1;
-    a3 = na3;
-    c1 = nc1;
-    c3 = nc3;
-    b = nb;
+  };
+  // the tile's scales, whole K: 32 rows x 128 bytes per matrix, same swizzle
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    const uint32_t so = (rt * 32u + 8u * j + lrow) * kScaleRow + 16u * ((lane & 7u) ^ ((j + lrow) & 7u));
+    dma16(rp, up_scales + 1024u * j, uint32_t(a.mx.s1) + so);
+    dma16(rp, up_scales + 4096u + 1024u * j, uint32_t(a.mx.s3) + so);
   }
-  mfma_settle<NT>(g);
-  mfma_settle<NT>(u);
-  // epilogue: lane (col, h) holds rows 8q + 4h + v (q, v = 0..3) of token col
+  const Rsrc xt = make_rsrc(ws.xt + size_t(item) * kXTileBytes, kXTileBytes);
+  const Rsrc xts = make_rsrc(ws.xts + size_t(item) * kXScaleBytes, kXScaleBytes);
+  BChunk rb[kRing];
+  issue(Slot<0>{}, 0);
+  issue(Slot<1>{}, 1);
+  issue(Slot<2>{}, 2);
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    float hv[16];
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      hv[i] = swiglu_exact(g[j][i], u[j][i]);
-      amax = fabsf(hv[i]) > amax ? fabsf(hv[i]) : amax;
-    }
-    const float other = __shfl_xor(amax, 32);  // the other 16 rows of the column
-    amax = other > amax ? other : amax;
-    const uint32_t code = requant_code(amax);
-    const float inv = __uint_as_float((254u - code) << 23);
-    const uint32_t i_tok = 32u * j + col;
-    if (i_tok >= it.count) continue;
-    const uint32_t p = it.first + i_tok;
-    uint8_t *dst = ws.hq + size_t(p) * kInter + 64u * (rt >> 1);
-    const uint32_t blk = rt & 1u;  // this tile's 32 rows are group rt of phase 2's K
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) word |= e4m3_rne_sat(__fmul_rn(hv[4 * q4 + v], inv)) << (8 * v);
-      const uint32_t r0 = 8u * q4 + 4u * h;  // first of 4 consecutive rows (k of the group)
-      const uint32_t pos = r0 < 16u ? 16u * blk + r0 : 32u + 16u * blk + (r0 - 16u);
-      *reinterpret_cast<uint32_t *>(dst + pos) = word;
-    }
-    if (h == 0) ws.hs[size_t(p) * (kInter / kQGroup) + rt] = uint8_t(code);
+  for (int j = 0; j < kRing; ++j) {
+    load_bchunk(rb[j], xt, xts, uint32_t(j), lane);
+    __builtin_amdgcn_sched_barrier(0);  // chunk order, so the loop's waits count the ring right
   }
-}
-
-__global__ __launch_bounds__(64) void k_prefill_up(PrefillArgs a, PrefillWorkspace ws) {
-  const uint32_t n_items = ws.stats[0];
-  if (blockIdx.y >= n_items) return;
-  const PrefillItem it = ws.items[blockIdx.y];
-  const uint32_t nt = (it.count + 31) / 32;
-  if (nt <= 1)
-    prefill_up_tiles<1>(a, ws, it, blockIdx.x);
-  else if (nt == 2)
-    prefill_up_tiles<2>(a, ws, it, blockIdx.x);
-  else if (nt == 3)
-    prefill_up_tiles<3>(a, ws, it, blockIdx.x);
-  else
-    prefill_up_tiles<4>(a, ws, it, blockIdx.x);
+  v16f g, u;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) g[i] = u[i] = 0.0f;
+  const uint32_t sw = swz(col);
+  auto chunk = [&](auto slot_tag, uint32_t c, bool refill) {
+    constexpr int S = decltype(slot_tag)::value;
+    const uint8_t *src = up_slot<S>() + 128u * col;
+#pragma unroll
+    for (uint32_t k = 0; k < kChunkSteps; ++k) {
+      const uint32_t q = (2u * k + h) ^ sw;
+      const uint4 a1 = *reinterpret_cast<const uint4 *>(src + 16u * q);
+      const uint4 a3 = *reinterpret_cast<const uint4 *>(src + 4096u + 16u * q);
+      const uint32_t sb = 2u * (c * kChunkSteps + k) + h;  // scale byte of this lane's weight block
+      const uint32_t sp = 128u * col + 16u * ((sb >> 4) ^ sw) + (sb & 15u);
+      const uint32_t c1 = up_scales[sp], c3 = up_scales[4096u + sp];
+      const uint32_t cb = (rb[S].sc >> (8u * k)) & 0xffu;
+      const v8i B = b_operand(rb[S].lo[k], rb[S].hi[k]);
+      g = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a_operand(a1), B, g, 4, 0, 0, int(c1), 0, int(cb));
+      u = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a_operand(a3), B, u, 4, 0, 0, int(c3), 0, int(cb));
+    }
+    if (refill) load_bchunk(rb[S], xt, xts, c + kRing, lane);
+    // keep the refill here: left free, the scheduler sinks loads to the end
+    // of the loop body, and the next round's first wait then drains the ring
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  static_assert(kRing == 4 && kChunks % 4 == 0 && kChunks >= 8, "four ring slots, whole rounds");
+  // Every round but the last refills unconditionally, so the ring stays in
+  // fixed registers across the back edge.
+#pragma unroll 1
+  for (uint32_t c = 0; c + 4 < kChunks; c += 4) {
+    issue(Slot<3>{}, c + 3);
+    chunk(Slot<0>{}, c, true);
+    issue(Slot<0>{}, c + 4);
+    chunk(Slot<1>{}, c + 1, true);
+    issue(Slot<1>{}, c + 5);
+    chunk(Slot<2>{}, c + 2, true);
+    issue(Slot<2>{}, c + 6);
+    chunk(Slot<3>{}, c + 3, true);
+  }
+  issue(Slot<3>{}, kChunks - 1);
+  chunk(Slot<0>{}, kChunks - 4, false);
+  chunk(Slot<1>{}, kChunks - 3, false);
+  chunk(Slot<2>{}, kChunks - 2, false);
+  chunk(Slot<3>{}, kChunks - 1, false);
+  v16f acc[2] = {g, u};
+  mfma_settle<2>(acc);
+  g = acc[0];
+  u = acc[1];
+  // epilogue: lane (col, h) holds rows 8q + 4h + v (q, v = 0..3) of column col
+  float hv[16];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    hv[i] = swiglu_exact(g[i], u[i]);
+    amax = fabsf(hv[i]) > amax ? fabsf(hv[i]) : amax;
+  }
+  const float other = __shfl_xor(amax, 32);  // the other 16 rows of the column
+  amax = other > amax ? other : amax;
+  const uint32_t code = requant_code(amax);
+  const float inv = __uint_as_float((254u - code) << 23);
+  // this tile's 32 rows are half blk of phase 2's K step s2 (group rt)
+  const uint32_t s2 = rt >> 1, blk = rt & 1u;
+  uint8_t *tile = ws.ht + size_t(item) * kHTileBytes + 2048u * s2;
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) word |= e4m3_rne_sat(__fmul_rn(hv[4 * q4 + v], inv)) << (8 * v);
+    const uint32_t r0 = 8u * q4 + 4u * h;  // first of 4 consecutive rows (k of the group)
+    const uint32_t pos = r0 < 16u ? 16u * blk + r0 : 32u + 16u * blk + (r0 - 16u);  // MFMA order in the step
+    *reinterpret_cast<uint32_t *>(tile + 1024u * ((pos >> 4) & 1u) + 16u * (col + 32u * (pos >> 5)) + (pos & 15u)) =
+        word;
+  }
+  if (h == 0) ws.hts[size_t(item) * kHScaleBytes + ((s2 / kChunkSteps) * 64u + col + 32u * blk) * 4u + s2 % kChunkSteps] =
+      uint8_t(code);
 }
 
 // Phase 2: one wavefront per (32-row tile of w2, work item): down rows of
-// every pair of the item, f32, route weight not applied.
-template <int NT>
-__device__ __forceinline__ void prefill_down_tiles(const PrefillArgs &a, const PrefillWorkspace &ws,
-                                                   const PrefillItem &it, uint32_t rt) {
+// every pair of the item, f32, route weight not applied.  K = 2048 in 8
+// chunks, the same rings as phase 1.
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_prefill_down(PrefillArgs a,
+                                                                                             PrefillWorkspace ws) {
+  const uint32_t n_items = ws.stats[0];
+  const uint32_t item = blockIdx.y;
+  if (item >= n_items) return;
+  const PrefillItem it = ws.items[item];
+  const uint32_t rt = blockIdx.x;
   const uint32_t lane = threadIdx.x & 63, col = lane & 31, h = lane >> 5;
   const Rsrc rp = page_rsrc(a, it.expert);
-  const uint32_t row = rt * 32u + col;
-  const uint32_t w2 = uint32_t(a.mx.w2) + row * (kInter / 2) + 16u * h;
-  const uint32_t s2 = uint32_t(a.mx.s2) + row * (kInter / 32) + h;
-  uint32_t prow[NT];
+  constexpr uint32_t kRowBytes = kInter / 2, kScaleRow = kInter / 32;
+  constexpr uint32_t kChunks = kInter / 64 / kChunkSteps;
+  const uint32_t lrow = lane >> 3;
+  uint32_t dma_off[4];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    const uint32_t i = 32u * j + col;
-    prow[j] = it.first + (i < it.count ? i : 0u);
+  for (uint32_t j = 0; j < 4; ++j)
+    dma_off[j] = uint32_t(a.mx.w2) + (rt * 32u + 8u * j + lrow) * kRowBytes + 16u * ((lane & 7u) ^ ((j + lrow) & 7u));
+  auto issue = [&](auto slot_tag, uint32_t c) {
+    uint8_t *dst = dn_slot<decltype(slot_tag)::value>();
+    lds_reads_done();
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) dma16(rp, dst + 1024u * j, dma_off[j] + 128u * c);
+  };
+  // scales: 32 rows x 64 bytes; load j covers rows 16j..16j+15, 4 lanes a row
+#pragma unroll
+  for (uint32_t j = 0; j < 2; ++j) {
+    const uint32_t row = 16u * j + (lane >> 2);
+    dma16(rp, dn_scales + 1024u * j,
+          uint32_t(a.mx.s2) + (rt * 32u + row) * kScaleRow + 16u * ((lane & 3u) ^ swz4(row)));
   }
-  v16f d[NT];
+  const Rsrc ht = make_rsrc(ws.ht + size_t(item) * kHTileBytes, kHTileBytes);
+  const Rsrc hts = make_rsrc(ws.hts + size_t(item) * kHScaleBytes, kHScaleBytes);
+  BChunk rb[kRing];
+  issue(Slot<0>{}, 0);
+  issue(Slot<1>{}, 1);
+  issue(Slot<2>{}, 2);
 #pragma unroll
-  for (int j = 0; j < NT; ++j)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) d[j][i] = 0.0f;
-  uint4 aw = ld16(rp, w2);
-  uint32_t cw = ld1(rp, s2);
-  BStep<NT> b;
-  load_b<NT>(b, ws.hq, ws.hs, prow, kInter, 0, h);
-  constexpr uint32_t kSteps = kInter / 64;
-  for (uint32_t s = 0; s < kSteps; ++s) {
-    const uint32_t sn = s + 1 < kSteps ? s + 1 : s;
-    const uint4 naw = ld16(rp, w2 + 32u * sn);
-    const uint32_t ncw = ld1(rp, s2 + 2u * sn);
-    BStep<NT> nb;
-    load_b<NT>(nb, ws.hq, ws.hs, prow, kInter, sn, h);
-    const v8i A = a_operand(aw);
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-      d[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, b_operand(b.lo[j], b.hi[j]), d[j], 4, 0, 0, int(cw),
-                                                              0, int(b.sc[j]));
-    aw = naw;
-    cw = ncw;
-    b = nb;
+  for (int j = 0; j < kRing; ++j) {
+    load_bchunk(rb[j], ht, hts, uint32_t(j), lane);
+    __builtin_amdgcn_sched_barrier(0);  // chunk order, so the loop's waits count the ring right
   }
-  mfma_settle<NT>(d);
+  v16f d[1];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    const uint32_t i_tok = 32u * j + col;
-    if (i_tok >= it.count) continue;
-    float *dst = ws.down + size_t(it.first + i_tok) * kHidden + rt * 32u;
+  for (int i = 0; i < 16; ++i) d[0][i] = 0.0f;
+  const uint32_t sw = swz(col), sw4 = swz4(col);
+  auto chunk = [&](auto slot_tag, uint32_t c, bool refill) {
+    constexpr int S = decltype(slot_tag)::value;
+    const uint8_t *src = dn_slot<S>() + 128u * col;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4)
-      *reinterpret_cast<float4 *>(dst + 8u * q4 + 4u * h) =
-          make_float4(d[j][4 * q4], d[j][4 * q4 + 1], d[j][4 * q4 + 2], d[j][4 * q4 + 3]);
+    for (uint32_t k = 0; k < kChunkSteps; ++k) {
+      const uint32_t q = (2u * k + h) ^ sw;
+      const uint4 aw = *reinterpret_cast<const uint4 *>(src + 16u * q);
+      const uint32_t sb = 2u * (c * kChunkSteps + k) + h;
+      const uint32_t ca = dn_scales[64u * col + 16u * ((sb >> 4) ^ sw4) + (sb & 15u)];
+      const uint32_t cb = (rb[S].sc >> (8u * k)) & 0xffu;
+      d[0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a_operand(aw), b_operand(rb[S].lo[k], rb[S].hi[k]), d[0],
+                                                              4, 0, 0, int(ca), 0, int(cb));
+    }
+    if (refill) load_bchunk(rb[S], ht, hts, c + kRing, lane);
+    __builtin_amdgcn_sched_barrier(0);  // as in phase 1
+  };
+  static_assert(kRing == 4 && kChunks % 4 == 0 && kChunks >= 8, "four ring slots, whole rounds");
+#pragma unroll 1
+  for (uint32_t c = 0; c + 4 < kChunks; c += 4) {
+    issue(Slot<3>{}, c + 3);
+    chunk(Slot<0>{}, c, true);
+    issue(Slot<0>{}, c + 4);
+    chunk(Slot<1>{}, c + 1, true);
+    issue(Slot<1>{}, c + 5);
+    chunk(Slot<2>{}, c + 2, true);
+    issue(Slot<2>{}, c + 6);
+    chunk(Slot<3>{}, c + 3, true);
   }
-}
-
-__global__ __launch_bounds__(64) void k_prefill_down(PrefillArgs a, PrefillWorkspace ws) {
-  const uint32_t n_items = ws.stats[0];
-  if (blockIdx.y >= n_items) return;
-  const PrefillItem it = ws.items[blockIdx.y];
-  const uint32_t nt = (it.count + 31) / 32;
-  if (nt <= 1)
-    prefill_down_tiles<1>(a, ws, it, blockIdx.x);
-  else if (nt == 2)
-    prefill_down_tiles<2>(a, ws, it, blockIdx.x);
-  else if (nt == 3)
-    prefill_down_tiles<3>(a, ws, it, blockIdx.x);
-  else
-    prefill_down_tiles<4>(a, ws, it, blockIdx.x);
+  issue(Slot<3>{}, kChunks - 1);
+  chunk(Slot<0>{}, kChunks - 4, false);
+  chunk(Slot<1>{}, kChunks - 3, false);
+  chunk(Slot<2>{}, kChunks - 2, false);
+  chunk(Slot<3>{}, kChunks - 1, false);
+  mfma_settle<1>(d);
+  if (col >= it.count) return;
+  float *dst = ws.down + size_t(it.first + col) * kHidden + rt * 32u;
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4)
+    *reinterpret_cast<float4 *>(dst + 8u * q4 + 4u * h) =
+        make_float4(d[0][4 * q4], d[0][4 * q4 + 1], d[0][4 * q4 + 2], d[0][4 * q4 + 3]);
 }
 
 // y[t] = 0; y += w_s * down_s in route order; y += shared down
@@ -495,6 +622,7 @@ hipError_t launch_prefill(hipStream_t s, const PrefillArgs &a, const PrefillWork
   k_prefill_group<<<1, 1024, 0, s>>>(a, ws);
   k_requant_x<<<(T * (kHidden / kQGroup) + 255) / 256, 256, 0, s>>>(T, a.x, ws.xq, ws.xs);
   const uint32_t max_items = prefill_max_items(T);
+  k_tile_x<<<max_items * (kXTileBytes / 16 / 256), 256, 0, s>>>(ws);
   k_prefill_up<<<dim3(kInter / 32, max_items), 64, 0, s>>>(a, ws);
   k_prefill_down<<<dim3(kHidden / 32, max_items), 64, 0, s>>>(a, ws);
   k_prefill_combine<<<(T * (kHidden / 4) + 255) / 256, 256, 0, s>>>(a, ws);

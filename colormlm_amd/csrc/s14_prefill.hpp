@@ -11,7 +11,7 @@ namespace s14 {
 
 constexpr uint32_t kMaxPrefillTokens = 1024;
 constexpr uint32_t kPrefillBitWords = kMaxPrefillTokens / 32;  // token bitmap words per expert
-constexpr uint32_t kItemTokens = 128;                          // tokens of one expert per GEMM work item
+constexpr uint32_t kItemTokens = 32;  // tokens of one expert per GEMM work item: one MFMA column tile
 
 // One GEMM work item: `count` consecutive pairs of one expert, starting at
 // pair `first` (expert kMaxExperts is the shared expert).
@@ -20,6 +20,18 @@ struct PrefillItem {
   uint32_t first;
   uint32_t count;
 };
+
+// Item tiles: the activation operand (B) of one work item laid out so each
+// K step is two coalesced 1 KiB loads: tile[step][part][lane][16 bytes],
+// lane = column + 32 h holding bytes 32 h + 16 part .. +15 of the column's
+// 64-byte step block in MFMA order (columns past the item's count are
+// zero).  Scales: [chunk of kChunkSteps steps][lane] u32, byte k = the E8M0
+// of step kChunkSteps * chunk + k for the lane's half.
+constexpr uint32_t kChunkSteps = 4;
+constexpr uint32_t kXTileBytes = (kHidden / 64) * 2048;                      // phase 1: 128 KiB
+constexpr uint32_t kXScaleBytes = (kHidden / 64 / kChunkSteps) * 64 * 4;     // 4 KiB
+constexpr uint32_t kHTileBytes = (kInter / 64) * 2048;                       // phase 2: 64 KiB
+constexpr uint32_t kHScaleBytes = (kInter / 64 / kChunkSteps) * 64 * 4;      // 2 KiB
 
 // Upper bound of the work items of T tokens: every expert contributes at
 // most one partial item beyond its full ones.
@@ -53,8 +65,10 @@ struct PrefillWorkspace {
   uint32_t *token_pair;   // [T][kSlots]
   uint8_t *xq;            // [T][4096] e4m3, MFMA order per 64-k step
   uint8_t *xs;            // [T][128] E8M0
-  uint8_t *hq;            // [7T][2048] e4m3, MFMA order
-  uint8_t *hs;            // [7T][64] E8M0
+  uint8_t *xt;            // [items][kXTileBytes] x of each item's pairs, item tile
+  uint8_t *xts;           // [items][kXScaleBytes]
+  uint8_t *ht;            // [items][kHTileBytes] e4m3 SwiGLU output, item tile
+  uint8_t *hts;           // [items][kHScaleBytes]
   float *down;            // [7T][4096]
   size_t bytes;
 };

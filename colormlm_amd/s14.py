@@ -438,13 +438,27 @@ def last_prefill_view(ctx: Context) -> dict:
 
         return torch.as_tensor(_Dev(), device="cuda").cpu().numpy()
 
+    n_items = int(v.n_items)
+    items = grab(v.items, 3 * n_items, "<u4").reshape(n_items, 3)
+    steps = N.INTER // 64
+    tiles = grab(v.ht, n_items * steps * 2048, "|u1").reshape(n_items, steps, 2, 2, 32, 16)  # [i][s][part][h][col][b]
+    tscales = grab(v.hts, n_items * steps * 64, "|u1").reshape(n_items, steps // 4, 2, 32, 4)  # [i][c][h][col][k]
+    hq = np.zeros((P, N.INTER), np.uint8)
+    hs = np.zeros((P, N.INTER // 32), np.uint8)
+    for i, (_, first, count) in enumerate(items.tolist()):
+        # pair first + col, step s: 64 bytes ordered [h][part][b]
+        blk = tiles[i, :, :, :, :count].transpose(3, 0, 2, 1, 4)  # [col][s][h][part][b]
+        hq[first:first + count] = blk.reshape(count, N.INTER)
+        sc = tscales[i, :, :, :count].transpose(2, 0, 3, 1)  # [col][c][k][h] -> group 2 (4c + k) + h
+        hs[first:first + count] = sc.reshape(count, N.INTER // 32)
     return {
         "tokens": T,
         "n_pairs": P,
         "xq": grab(v.xq, T * N.HIDDEN, "|u1").reshape(T, N.HIDDEN),
         "xs": grab(v.xs, T * (N.HIDDEN // 32), "|u1").reshape(T, N.HIDDEN // 32),
-        "hq": grab(v.hq, P * N.INTER, "|u1").reshape(P, N.INTER),
-        "hs": grab(v.hs, P * (N.INTER // 32), "|u1").reshape(P, N.INTER // 32),
+        "hq": hq,
+        "hs": hs,
+        "items": items,
         "down": grab(v.down, P * N.HIDDEN, "<f4").reshape(P, N.HIDDEN),
         "pair_token": grab(v.pair_token, P, "<i4"),
         "token_pair": grab(v.token_pair, T * 7, "<i4").reshape(T, 7),

@@ -282,17 +282,23 @@ int s14_last_prefill_stats(s14_ctx *ctx, uint32_t *distinct, uint32_t *max_token
  *   xq [tokens][4096] e4m3 and xs [tokens][128] E8M0: the requantised
  *     activations; within each 64-value step the bytes are ordered
  *     k 0-15, 32-47, 16-31, 48-63 (the MFMA operand order);
- *   hq [n_pairs][2048], hs [n_pairs][64]: the SwiGLU output of each
- *     (token, expert) pair, requantised the same way;
+ *   ht, hts: the SwiGLU output of each (token, expert) pair, requantised
+ *     the same way, in work-item tiles: item i's tile is 65536 bytes at
+ *     ht + 65536 i, byte (s, part, lane, b) at 2048 s + 1024 part +
+ *     16 lane + b holding byte 32 h + 16 part + b of step s of the pair
+ *     first_i + (lane % 32), h = lane / 32; its scales are 2048 bytes at
+ *     hts + 2048 i, u32 [s / 4][lane] with byte s % 4 = the E8M0 of step s,
+ *     half h;
  *   down [n_pairs][4096] f32: each pair's w2 output, route weight not applied;
  *   pair_token [n_pairs]: the token of each pair; token_pair [tokens][7]:
- *     each token's pairs in route order, the shared expert's last.
+ *     each token's pairs in route order, the shared expert's last;
+ *   items [n_items][3]: {expert, first pair, pairs} of each GEMM work item.
  * Pairs are grouped by routed expert ascending, the shared expert's last. */
 typedef struct s14_prefill_view {
-  const uint8_t *xq, *xs, *hq, *hs;
+  const uint8_t *xq, *xs, *ht, *hts;
   const float *down;
-  const uint32_t *pair_token, *token_pair;
-  uint32_t tokens, n_pairs;
+  const uint32_t *pair_token, *token_pair, *items;
+  uint32_t tokens, n_pairs, n_items;
 } s14_prefill_view;
 int s14_last_prefill_view(s14_ctx *ctx, s14_prefill_view *out);
 /* The prefill's activation requant as a standalone dispatch (natural

@@ -614,7 +614,7 @@ def test_prefill_config4_against_oracle(ctx, oracle, bank, prefill_router):
     st = s14.last_prefill_stats(ctx)
     assert st["distinct"] == int(np.count_nonzero(counts))
     assert st["max_tokens_per_expert"] == int(counts.max())
-    assert st["items"] == int(np.sum((counts + 127) // 128)) + (T + 127) // 128
+    assert st["items"] == int(np.sum((counts + 31) // 32)) + (T + 31) // 32
     say(f"  stats {st}")
     view = s14.last_prefill_view(ctx)
     check = sorted({int(p) for t in range(0, T, 8) for p in view["token_pair"][t]})
@@ -630,8 +630,8 @@ def test_prefill_config4_512_properties(ctx, oracle, bank, prefill_router):
     (an MFMA column does not see its neighbours), so the first 64 tokens
     must equal a 64-token run bit for bit, whatever tiles and work items the
     grouping gave them; repeat runs are identical; all 512 routes match the
-    oracle; and the stages of the busiest expert's pairs (items of 128
-    tokens, four column tiles) and of the shared expert's pairs check out."""
+    oracle; and the stages of the busiest expert's pairs (split over several
+    32-token work items) and of the shared expert's pairs check out."""
     T = 512
     say(f"config 4 prefill T={T}: properties, stages of the busiest experts")
     xs = synth.prefill_tokens(seed=0, tokens=T)
@@ -645,7 +645,7 @@ def test_prefill_config4_512_properties(ctx, oracle, bank, prefill_router):
         counts[i_o] += 1
     assert st["distinct"] == int(np.count_nonzero(counts))
     assert st["max_tokens_per_expert"] == int(counts.max())
-    assert st["items"] == int(np.sum((counts + 127) // 128)) + (T + 127) // 128
+    assert st["items"] == int(np.sum((counts + 31) // 32)) + (T + 31) // 32
     say(f"  stats {st}; tokens/expert mean {counts[counts > 0].mean():.2f}")
     busiest = int(np.argmax(counts))
     on_busiest = np.flatnonzero((ids == busiest).any(axis=1))
