@@ -148,6 +148,45 @@ __device__ __forceinline__ void mx_products_scaled(float (&p)[16], uint2 w, uint
     }
   }
 }
+// pair_chain16 of group g's products p with group g+1's products q formed
+// in between.  Each DPP add reads the accumulator the previous add wrote,
+// and a DPP read needs two wait states after that write: issued back to
+// back (as the scheduler otherwise leaves them) every DPP add waits behind
+// an s_nop.  Here q's 8 conversions and 16 multiplies sit between the DPP
+// adds, two before each while they last, and the scheduling barriers hold
+// that order; the 16 plain adds need no spacing and go first.
+__device__ __forceinline__ float pair_chain16_next(float acc, const float (&p)[16], float (&q)[16], uint2 w,
+                                                   uint32_t c, const X16 &x) {
+  const float sc = __uint_as_float(c << 23);
+  const uint32_t words[2] = {w.x, w.y};
+  v2f d[8];  // d[i]: byte i % 4 of word i / 4, scaled; q[2i], q[2i+1] use it
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc = __fadd_rn(acc, p[j]);
+#define S14_CVT(i) d[i] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[(i) >> 2], sc, (i)&3);
+#define S14_MUL(m) q[m] = __fmul_rn(x.v[m], ((m)&1) ? d[(m) >> 1].y : d[(m) >> 1].x);
+#define S14_DPP_ADD(j)                         \
+  __builtin_amdgcn_sched_barrier(0);           \
+  acc = __fadd_rn(acc, from_odd(p[j]));        \
+  __builtin_amdgcn_sched_barrier(0);
+  S14_CVT(0) S14_CVT(1) S14_DPP_ADD(0)
+  S14_MUL(0) S14_MUL(1) S14_DPP_ADD(1)
+  S14_CVT(2) S14_MUL(2) S14_DPP_ADD(2)
+  S14_MUL(3) S14_CVT(3) S14_DPP_ADD(3)
+  S14_MUL(4) S14_MUL(5) S14_DPP_ADD(4)
+  S14_CVT(4) S14_MUL(6) S14_DPP_ADD(5)
+  S14_MUL(7) S14_CVT(5) S14_DPP_ADD(6)
+  S14_MUL(8) S14_MUL(9) S14_DPP_ADD(7)
+  S14_CVT(6) S14_MUL(10) S14_DPP_ADD(8)
+  S14_MUL(11) S14_CVT(7) S14_DPP_ADD(9)
+  S14_MUL(12) S14_MUL(13) S14_DPP_ADD(10)
+  S14_MUL(14) S14_MUL(15) S14_DPP_ADD(11)
+  S14_DPP_ADD(12) S14_DPP_ADD(13) S14_DPP_ADD(14) S14_DPP_ADD(15)
+#undef S14_CVT
+#undef S14_MUL
+#undef S14_DPP_ADD
+  return acc;
+}
+
 // Literal: p = (x * e2m1) * ue8m0(c), any code.
 __device__ __forceinline__ void mx_products_literal(float (&p)[16], uint2 w, uint32_t c, const X16 &x) {
   const float s = ue8m0_f32(c);
@@ -184,6 +223,14 @@ __device__ __forceinline__ void mx_load(MxBatch<PF> &b, const Src2 &src, uint32_
     mx_load<PF>(b, Src1{src.a, src.a}, woff, soff, g0);
 }
 
+template <int PF>
+__device__ __forceinline__ void mx_load(MxBatch<PF> &b, const SrcP &src, uint32_t woff, uint32_t soff, int g0) {
+#pragma unroll
+  for (int i = 0; i < PF; ++i) b.w[i] = gld8(src.p + woff + 16u * uint32_t(g0 + i));
+#pragma unroll
+  for (int j = 0; j < PF / 4; ++j) b.c[j] = gld4(src.p + soff + uint32_t(g0) + 4u * j);
+}
+
 __device__ __forceinline__ bool codes_in(uint32_t word, CodeWindow win) {
   bool ok = true;
 #pragma unroll
@@ -211,6 +258,8 @@ __device__ __forceinline__ uint2 src_ld8(const Src2 &s, uint32_t off) {
     v = ld8(s.a, off);
   return v;
 }
+__device__ __forceinline__ uint2 src_ld8(const SrcP &s, uint32_t off) { return gld8(s.p + off); }
+__device__ __forceinline__ uint32_t src_ld1(const SrcP &s, uint32_t off) { return s.p[off]; }
 __device__ __forceinline__ uint32_t src_ld1(const Src2 &s, uint32_t off) {
   uint32_t v;
   if (s.hi)
@@ -242,11 +291,12 @@ __device__ __forceinline__ float mx_consume(float acc, const MxBatch<PF> &b, con
     for (int i = 0; i < PF; i += 2) {
       // p holds group i's products; xb holds group i+1's x
       if (i + 2 < PF) load_x16(xa, xh + (g0 + i + 2) * 32);
-      mx_products_scaled(q, b.w[i + 1], batch_code(b, i + 1), xb);
-      acc = pair_chain16(acc, p);
+      acc = pair_chain16_next(acc, p, q, b.w[i + 1], batch_code(b, i + 1), xb);
       if (i + 3 < PF) load_x16(xb, xh + (g0 + i + 3) * 32);
-      if (i + 2 < PF) mx_products_scaled(p, b.w[i + 2], batch_code(b, i + 2), xa);
-      acc = pair_chain16(acc, q);
+      if (i + 2 < PF)
+        acc = pair_chain16_next(acc, q, p, b.w[i + 2], batch_code(b, i + 2), xa);
+      else
+        acc = pair_chain16(acc, q);
     }
   } else {
 #pragma unroll 1
@@ -1247,9 +1297,11 @@ __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairT
   const bool mine_mx = (hi ? fb : fa) == S14_PAGE_MXFP4;
   const uint32_t mx_woff = uint32_t(mx.w2) + row * (kInter / 2) + 8u * h;
   const uint32_t mx_soff = uint32_t(mx.s2) + row * (kInter / 32);
+  // both halves MXFP4 (the normal case): per-lane page pointers
+  const SrcP srcp{(GPtr)(hi && has_b ? ub : ua)};
   MxBatch<kPF> ba;
   if (has_a && fa == S14_PAGE_MXFP4 && fb == S14_PAGE_MXFP4)
-    mx_load<kPF>(ba, src, mx_woff, mx_soff, 0);  // first weights in flight during the h copy
+    mx_load<kPF>(ba, srcp, mx_woff, mx_soff, 0);  // first weights in flight during the h copy
   CodeWindow win[2] = {{256, 0}, {256, 0}};
   if (has_b) {
     float *const dst[2] = {hs[sa], hs[sb]};
@@ -1267,7 +1319,7 @@ __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairT
     const float *xh = hs[slot] + 16 * h;
     float acc;
     if (fa == S14_PAGE_MXFP4 && fb == S14_PAGE_MXFP4) {
-      acc = mx_row_pair_fixed<kPF, kInter / 32>(0.0f, ba, src, mx_woff, mx_soff, xh, (hi ? win[1] : win[0]));
+      acc = mx_row_pair_fixed<kPF, kInter / 32>(0.0f, ba, srcp, mx_woff, mx_soff, xh, (hi ? win[1] : win[0]));
     } else if (mine_mx) {  // formats differ between the halves
       MxBatch<kPF> bm;
       mx_load<kPF>(bm, src, mx_woff, mx_soff, 0);

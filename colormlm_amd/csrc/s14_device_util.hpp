@@ -56,6 +56,20 @@ struct Src2 {
   Rsrc a, b;
   bool hi;
 };
+// A per-lane source: wavefronts that serve two pages (lanes 0-31 one, 32-63
+// the other) load through a per-lane global pointer.  A buffer descriptor
+// that differs between lanes has to be made uniform first, and the compiler
+// does that with a loop over the distinct descriptors around every load.
+// No bounds clamp: callers keep every load inside its row.
+typedef const __attribute__((address_space(1))) uint8_t *GPtr;
+struct SrcP {
+  GPtr p;
+};
+__device__ __forceinline__ uint2 gld8(GPtr p) {
+  const uint64_t v = *(const __attribute__((address_space(1))) uint64_t *)p;
+  return make_uint2(uint32_t(v), uint32_t(v >> 32));
+}
+__device__ __forceinline__ uint32_t gld4(GPtr p) { return *(const __attribute__((address_space(1))) uint32_t *)p; }
 
 // ---------------------------------------------------------------------------
 // decoders (bit patterns; equal to s14_vulkan_numeric.rs:1716-1743)
