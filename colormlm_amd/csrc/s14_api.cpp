@@ -106,7 +106,7 @@ extern "C" int s14_ctx_create(int device, s14_ctx **out) {
     s14_ctx_destroy(ctx);
     return hip_fail(e, "hipStreamCreate");
   }
-  // workspace: table | h | scores | biased | route counter
+  // workspace: table | h | scores | biased | route counter | h windows
   size_t off = 0;
   const size_t o_table = off;
   off = align_up(off + sizeof(s14::PairTable), 256);
@@ -118,6 +118,8 @@ extern "C" int s14_ctx_create(int device, s14_ctx **out) {
   off = align_up(off + sizeof(float) * s14::kMaxTokens * s14::kMaxExperts, 256);
   const size_t o_count = off;
   off = align_up(off + sizeof(uint32_t) * (1 + s14::kMaxTokens), 256);
+  const size_t o_hwin = off;
+  off = align_up(off + sizeof(uint32_t) * s14::kMaxPairs * (s14::kInter / s14::kP1ExactRows), 256);
   e = hipMalloc(&ctx->ws_base, off);
   if (e != hipSuccess) {
     s14_ctx_destroy(ctx);
@@ -129,6 +131,7 @@ extern "C" int s14_ctx_create(int device, s14_ctx **out) {
   ctx->ws.scores = reinterpret_cast<float *>(b + o_scores);
   ctx->ws.biased = reinterpret_cast<float *>(b + o_biased);
   ctx->ws.route_count = reinterpret_cast<uint32_t *>(b + o_count);  // zeroed below; each route launch leaves it 0
+  ctx->ws.hwin = reinterpret_cast<uint32_t *>(b + o_hwin);
   ctx->ws.bytes = off;
   // one clear at creation, outside any launch sequence
   e = hipMemset(ctx->ws_base, 0, off);

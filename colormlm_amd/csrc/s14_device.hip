@@ -83,6 +83,35 @@ __device__ __forceinline__ void stage_x_wave(float *const (&dst)[S], const float
   }
 }
 
+// The copy alone, for vectors whose window is known (phase 2's h).
+template <int N, int S>
+__device__ __forceinline__ void stage_copy_wave(float *const (&dst)[S], const float *const (&src)[S]) {
+  static_assert(N % 256 == 0, "whole float4 sweeps");
+  constexpr int IT = N / 256;
+  const int lane = int(threadIdx.x & 63);
+  float4 v[S][IT];
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int it = 0; it < IT; ++it) v[s][it] = *reinterpret_cast<const float4 *>(src[s] + it * 256 + lane * 4);
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int it = 0; it < IT; ++it) *reinterpret_cast<float4 *>(dst[s] + it * 256 + lane * 4) = v[s][it];
+}
+
+// Window of one pair's h from the exponent ranges its exact phase-1 tiles
+// recorded (lo | hi << 16 per tile): the same range stage_x_wave would find
+// by scanning h.
+constexpr int kP1Tiles = kInter / kP1ExactRows;
+__device__ __forceinline__ CodeWindow h_window(const uint32_t *__restrict__ tiles) {
+  static_assert(kP1Tiles == 128, "two tile words per lane");
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t a = tiles[lane], b = tiles[lane + 64];
+  const int lo = min(int(a & 0xffffu), int(b & 0xffffu)), hi = max(int(a >> 16), int(b >> 16));
+  return mx_window(wave_min_i(lo), wave_max_i(hi));
+}
+
 // Copy n f32 (n % 4 == 0) into LDS with the calling wavefront, eight float4
 // loads in flight per lane.
 __device__ __forceinline__ void stage_chunk_wave(float *dst, const float *__restrict__ src, uint32_t n) {
@@ -1168,7 +1197,18 @@ __global__ __launch_bounds__(64) void k_phase1_exact(PairTable plan, Workspace w
     acc = fp8_row_pair(0.0f, src, woff, soff, 0, kHidden / 32, xs + 16 * h);
   }
   const float other = __shfl_xor(acc, 32);
-  if (!upper && h == 0) ws.h[size_t(p) * kInter + row] = swiglu_exact(acc, other);
+  const bool writer = !upper && h == 0;
+  int lo = 255, hi = 0;
+  if (writer) {
+    const float hv = swiglu_exact(acc, other);
+    ws.h[size_t(p) * kInter + row] = hv;
+    exp_range_acc(hv, lo, hi);
+  }
+  // the tile's exponent range, so that phase 2 gets h's decode window
+  // without scanning h
+  lo = wave_min_i(lo);
+  hi = wave_max_i(hi);
+  if (lane == 0) ws.hwin[size_t(p) * kP1Tiles + blockIdx.x] = uint32_t(lo) | (uint32_t(hi) << 16);
 }
 
 // Phase 1 FAST: 4 wavefronts per workgroup; each streams kP1FastRowsPerWave
@@ -1274,6 +1314,7 @@ constexpr int kHStride = kInter + 8;
 template <int kTier>
 __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairTable *__restrict__ tab,
                                                                      const float *__restrict__ H,
+                                                                     const uint32_t *__restrict__ hwin,
                                                                      float *__restrict__ Y, PageOffsets mx,
                                                                      PageOffsets f8) {
   __shared__ float hs[kSlots][kHStride];
@@ -1309,13 +1350,14 @@ __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairT
   if (has_b) {
     float *const dst[2] = {hs[sa], hs[sb]};
     const float *const srch[2] = {H + size_t(pa) * kInter, H + size_t(pb) * kInter};
-    stage_x_wave<kInter, 2>(dst, srch, win);
+    win[0] = h_window(hwin + size_t(pa) * kP1Tiles);
+    win[1] = h_window(hwin + size_t(pb) * kP1Tiles);
+    stage_copy_wave<kInter, 2>(dst, srch);
   } else if (has_a) {
     float *const dst[1] = {hs[sa]};
     const float *const srch[1] = {H + size_t(pa) * kInter};
-    CodeWindow w1[1];
-    stage_x_wave<kInter, 1>(dst, srch, w1);
-    win[0] = win[1] = w1[0];
+    win[0] = win[1] = h_window(hwin + size_t(pa) * kP1Tiles);
+    stage_copy_wave<kInter, 1>(dst, srch);
   }
   __syncthreads();
   if (has_a) {
@@ -1522,7 +1564,7 @@ void phase2_tier(hipStream_t s, const Workspace &ws, uint32_t tokens, const Page
                           ev.start, ev.stop, 0, tab, h, y, mx, fp8);
   else
     hipExtLaunchKernelGGL(k_phase2_exact<kTier>, dim3(kHidden / kP2ExactRows, tokens), dim3(64 * kP2ExactWaves), 0,
-                          s, ev.start, ev.stop, 0, tab, h, y, mx, fp8);
+                          s, ev.start, ev.stop, 0, tab, h, ws.hwin, y, mx, fp8);
 }
 }  // namespace
 

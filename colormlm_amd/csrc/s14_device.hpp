@@ -78,6 +78,7 @@ struct Workspace {
   float *scores;  // [kMaxTokens][kMaxExperts]
   float *biased;  // [kMaxTokens][kMaxExperts]
   uint32_t *route_count;  // [1 + kMaxTokens]: tokens, then per-token workgroups, of the running route launch that are done
+  uint32_t *hwin;         // [kMaxPairs][kInter / kP1ExactRows]: exponent range (lo | hi << 16) of each exact phase-1 tile's h
   size_t bytes;
 };
 
