@@ -191,14 +191,16 @@ struct TopK {
 __device__ __forceinline__ TopK select_topk(const float *__restrict__ biased, const float *__restrict__ scores,
                                             const uint64_t *__restrict__ pages, uint32_t n_experts, uint32_t k) {
   const uint32_t lane = threadIdx.x & 63;
-  // key 0 marks an absent or already chosen expert; a real score's key is
-  // >= 1 unless it is NaN
+  // lane l holds experts 4l .. 4l+3, so a lower lane holds only lower
+  // indices: the lowest lane with the maximum key, then its lowest slot, is
+  // the lowest expert index among the ties.  Key 0 marks an absent or
+  // already chosen expert; a real score's key is >= 1 unless it is NaN.
   uint32_t kv[4];
   float sv[4];
   uint64_t pv[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint32_t ee = lane + 64u * j;
+    const uint32_t ee = 4u * lane + uint32_t(j);
     const bool absent = ee >= n_experts;
     kv[j] = absent ? 0u : max(score_key(biased[ee]), 1u);
     sv[j] = absent ? 0.0f : scores[ee];
@@ -209,34 +211,27 @@ __device__ __forceinline__ TopK select_topk(const float *__restrict__ biased, co
 #pragma unroll
   for (uint32_t i = 0; i < uint32_t(kTopK); ++i) {
     if (i >= k) break;
-    // max key over the wavefront, then the lowest expert index holding it:
-    // expert lane + 64 j, so the first j whose ballot is non-empty, at its
-    // lowest lane
     const uint32_t top = wave_max_u32(max(max(kv[0], kv[1]), max(kv[2], kv[3])));
-    // (scalar selects, no branches: the masks are wavefront-uniform)
-    constexpr uint64_t kHi = 1ull << 63;
-    const uint64_t m0 = __ballot(kv[0] == top), m1 = __ballot(kv[1] == top);
-    const uint64_t m2 = __ballot(kv[2] == top), m3 = __ballot(kv[3] == top);
-    int best = 192 + __builtin_ctzll(m3 | kHi);
-    best = m2 ? 128 + __builtin_ctzll(m2 | kHi) : best;
-    best = m1 ? 64 + __builtin_ctzll(m1 | kHi) : best;
-    best = m0 ? __builtin_ctzll(m0 | kHi) : best;
+    const uint32_t jl = kv[0] == top ? 0u : kv[1] == top ? 1u : kv[2] == top ? 2u : 3u;  // this lane's first hit
+    const uint64_t hit = __ballot(kv[0] == top || kv[1] == top || kv[2] == top || kv[3] == top);
+    const int wl = __builtin_ctzll(hit | (1ull << 63));  // lowest lane holding the maximum
+    const uint32_t wj = uint32_t(__builtin_amdgcn_readlane(int(jl), wl));
     float cand = sv[0];
     uint64_t cpg = pv[0];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (int(lane + 64u * j) == best) kv[j] = 0u;
-      if ((best >> 6) == j) {
-        cand = sv[j];
-        cpg = pv[j];
-      }
+    for (int j = 1; j < 4; ++j) {
+      cand = wj == uint32_t(j) ? sv[j] : cand;
+      cpg = wj == uint32_t(j) ? pv[j] : cpg;
     }
-    const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cand), best & 63));
-    const uint64_t pg = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(cpg >> 32), best & 63))) << 32) |
-                        uint32_t(__builtin_amdgcn_readlane(int(uint32_t(cpg)), best & 63));
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (int(lane) == wl && wj == uint32_t(j)) kv[j] = 0u;
+    const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cand), wl));
+    const uint64_t pg = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(cpg >> 32), wl))) << 32) |
+                        uint32_t(__builtin_amdgcn_readlane(int(uint32_t(cpg)), wl));
     sum = __fadd_rn(sum, s);
     if (lane == i) {
-      mine.id = uint32_t(best);
+      mine.id = 4u * uint32_t(wl) + wj;
       mine.s = s;
       mine.page = pg;
     }
