@@ -1170,6 +1170,8 @@ template <bool kHostPlan, int kTier>
 __global__ __launch_bounds__(64) void k_phase1_exact(PairTable plan, Workspace ws, const float *__restrict__ X,
                                                      PageOffsets mx, PageOffsets f8) {
   __shared__ float xs[kHidden];
+  __shared__ double exptab[32];
+  exp_table_fill(exptab);  // published by the barrier after the x copy
   const uint32_t p = blockIdx.y;
   const PairRef pr = phase1_pair<kHostPlan>(plan, ws.table, p);
   const uint32_t lane = threadIdx.x, h = lane & 1u;
@@ -1200,7 +1202,7 @@ __global__ __launch_bounds__(64) void k_phase1_exact(PairTable plan, Workspace w
   const bool writer = !upper && h == 0;
   int lo = 255, hi = 0;
   if (writer) {
-    const float hv = swiglu_exact(acc, other);
+    const float hv = swiglu_exact(acc, other, exptab);
     ws.h[size_t(p) * kInter + row] = hv;
     exp_range_acc(hv, lo, hi);
   }

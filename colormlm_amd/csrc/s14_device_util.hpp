@@ -99,15 +99,33 @@ __device__ __forceinline__ float e4m3_f32(uint32_t code) {
 
 __device__ __forceinline__ float bf16_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
-__device__ __forceinline__ float swiglu_exact(float gate, float up) {
+// expf's 32 table entries in LDS (see s14x::expf_glibc_with): filled by the
+// first 32 lanes of a wavefront, then a barrier before any use.
+struct LdsExpTable {
+  const double *t;
+  __device__ double operator()(uint32_t i) const { return t[i]; }
+};
+__device__ __forceinline__ void exp_table_fill(double *lds) {
+  const uint32_t lane = threadIdx.x & 63;
+  if (threadIdx.x < 32) lds[lane] = s14x::exp_table_entry(lane);
+}
+
+template <class Tab>
+__device__ __forceinline__ float swiglu_exact_with(float gate, float up, const Tab &tab) {
   // s14_vulkan_numeric.rs:1543-1556: gate.min(10) keeps -0 and maps NaN to
   // 10; clamp passes NaN through.
   const float g = (gate <= 10.0f) ? gate : 10.0f;
   float u = up;
   if (u < -10.0f) u = -10.0f;
   if (u > 10.0f) u = 10.0f;
-  const float e = s14x::expf_glibc(-g);
+  const float e = s14x::expf_glibc_with(-g, tab);
   return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
+}
+__device__ __forceinline__ float swiglu_exact(float gate, float up) {
+  return swiglu_exact_with(gate, up, s14x::ConstExpTable{});
+}
+__device__ __forceinline__ float swiglu_exact(float gate, float up, const double *lds_table) {
+  return swiglu_exact_with(gate, up, LdsExpTable{lds_table});
 }
 
 // ---------------------------------------------------------------------------

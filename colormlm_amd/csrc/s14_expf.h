@@ -94,7 +94,12 @@ S14_HD double f64_from_bits(uint64_t u) {
 #endif
 }
 
-S14_HD float expf_glibc(float x) {
+// The method with the table lookup supplied by the caller: tab(i) must return
+// exp_table_entry(i).  Device kernels that call it many times keep the 32
+// entries in LDS; read from the constant table each call is a dependent
+// global load.
+template <class Tab>
+S14_HD float expf_glibc_with(float x, const Tab &tab) {
   const double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;  // 32/ln(2)
   const double kShift = 0x1.8p+52;
   // cubic coefficients of 2^(r/32), pre-divided by 32^3, 32^2, 32
@@ -115,7 +120,7 @@ S14_HD float expf_glibc(float x) {
   const uint64_t ki = f64_bits(kd);
   kd = kd - kShift;
   const double r = fma(kInvLn2N, xd, -kd);
-  uint64_t t = f64_bits(exp_table_entry((uint32_t)(ki % 32)));
+  uint64_t t = f64_bits(tab((uint32_t)(ki % 32)));
   t += ki << 47;
   const double s = f64_from_bits(t);
   z = kC0 * r + kC1;
@@ -125,5 +130,14 @@ S14_HD float expf_glibc(float x) {
   y = y * s;
   return (float)y;
 }
+
+struct ConstExpTable {
+#if defined(__HIPCC__)
+  __host__ __device__
+#endif
+  double operator()(uint32_t i) const { return exp_table_entry(i); }
+};
+
+S14_HD float expf_glibc(float x) { return expf_glibc_with(x, ConstExpTable{}); }
 
 }  // namespace s14x

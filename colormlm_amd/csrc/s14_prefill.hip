@@ -398,6 +398,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   }
   const Rsrc xt = make_rsrc(ws.xt + size_t(item) * kXTileBytes, kXTileBytes);
   const Rsrc xts = make_rsrc(ws.xts + size_t(item) * kXScaleBytes, kXScaleBytes);
+  // expf's table for the epilogue's 16 SwiGLUs per lane: one entry per lane
+  // now, written to a free ring slot after the K loop (an LDS array of its
+  // own would cost this kernel its fourth wavefront per CU)
+  const double exp_entry = s14x::exp_table_entry(lane & 31u);
   BChunk rb[kRing];
   issue(Slot<0>{}, 0);
   issue(Slot<1>{}, 1);
@@ -456,11 +460,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   g = acc[0];
   u = acc[1];
   // epilogue: lane (col, h) holds rows 8q + 4h + v (q, v = 0..3) of column col
+  double *exptab = reinterpret_cast<double *>(up_slot0);  // slot 0's last chunk is consumed
+  if (lane < 32) exptab[lane] = exp_entry;
+  __syncthreads();  // one wavefront: orders the table writes before the lookups
   float hv[16];
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    hv[i] = swiglu_exact(g[i], u[i]);
+    hv[i] = swiglu_exact(g[i], u[i], exptab);
     amax = fabsf(hv[i]) > amax ? fabsf(hv[i]) : amax;
   }
   const float other = __shfl_xor(amax, 32);  // the other 16 rows of the column
