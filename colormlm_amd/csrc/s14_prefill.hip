@@ -33,6 +33,7 @@
 
 #include "s14_device.hpp"
 #include "s14_device_util.hpp"
+#include "s14_e4m3.h"
 #include "s14_prefill.hpp"
 
 namespace s14 {
@@ -58,25 +59,7 @@ __device__ __forceinline__ uint32_t requant_code(float amax) {
   return uint32_t(c + 127);
 }
 
-// OCP e4m3fn, round to nearest even, saturating to +-448 (NaN -> 0x7f).
-__device__ __forceinline__ uint32_t e4m3_rne_sat(float v) {
-  if (v != v) return 0x7fu;
-  const uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
-  const float a = fabsf(v);
-  if (a >= 448.0f) return sign | 0x7eu;
-  if (a < 0x1p-6f) return sign | uint32_t(__builtin_rintf(__fmul_rn(a, 512.0f)));  // m * 2^-9 grid
-  const uint32_t u = __float_as_uint(a);
-  int e = int((u >> 23) & 255u) - 127;                     // a = m * 2^e, m in [1, 2)
-  const float m = __uint_as_float((u & 0x7fffffu) | 0x3f800000u);
-  float mant = __builtin_rintf(__fmul_rn(__fsub_rn(m, 1.0f), 8.0f));
-  if (mant >= 8.0f) {
-    mant = 0.0f;
-    e += 1;
-  }
-  const int biased = e + 7;
-  if (biased > 15 || (biased == 15 && mant >= 7.0f)) return sign | 0x7eu;
-  return sign | uint32_t((biased << 3) | int(mant));
-}
+using s14x::e4m3_rne_sat;  // s14_e4m3.h: straight-line, checked against the oracle on the CPU
 
 // X [T, 4096] f32 -> Q [T, 4096] e4m3 in MFMA order + S [T, 128] E8M0.
 // One thread per 32-value group.
