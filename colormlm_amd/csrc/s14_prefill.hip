@@ -329,14 +329,21 @@ struct BChunk {
   uint4 lo[kChunkSteps], hi[kChunkSteps];
   uint32_t sc;  // byte k: scale of step k for this lane's half
 };
-__device__ __forceinline__ void load_bchunk(BChunk &b, Rsrc tile, Rsrc scales, uint32_t c, uint32_t lane) {
+// Lanes of columns past the item's count read from past the descriptor's
+// range: the buffer load returns zeros without a memory access, so a work
+// item moves only its pairs' activations (items average ~13 of 32 columns).
+constexpr uint32_t kOffRange = 0x40000000u;
+__device__ __forceinline__ uint32_t bcol_base(uint32_t lane, bool live) { return live ? 16u * lane : kOffRange; }
+__device__ __forceinline__ uint32_t bscale_base(uint32_t lane, bool live) { return live ? 4u * lane : kOffRange; }
+__device__ __forceinline__ void load_bchunk(BChunk &b, Rsrc tile, Rsrc scales, uint32_t c, uint32_t tbase,
+                                            uint32_t sbase) {
 #pragma unroll
   for (uint32_t k = 0; k < kChunkSteps; ++k) {
     const uint32_t s = c * kChunkSteps + k;
-    b.lo[k] = ld16(tile, 2048u * s + 16u * lane);
-    b.hi[k] = ld16(tile, 2048u * s + 1024u + 16u * lane);
+    b.lo[k] = ld16(tile, tbase + 2048u * s);
+    b.hi[k] = ld16(tile, tbase + 2048u * s + 1024u);
   }
-  b.sc = ld4(scales, (c * 64u + lane) * 4u);
+  b.sc = ld4(scales, sbase + c * 256u);
 }
 
 // Phase 1: one wavefront per (32-row tile of w1/w3, work item of <= 32
@@ -381,6 +388,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   }
   const Rsrc xt = make_rsrc(ws.xt + size_t(item) * kXTileBytes, kXTileBytes);
   const Rsrc xts = make_rsrc(ws.xts + size_t(item) * kXScaleBytes, kXScaleBytes);
+  const bool live = col < it.count;
+  const uint32_t tb = bcol_base(lane, live), sbb = bscale_base(lane, live);
   // expf's table for the epilogue's 16 SwiGLUs per lane: one entry per lane
   // now, written to a free ring slot after the K loop (an LDS array of its
   // own would cost this kernel its fourth wavefront per CU)
@@ -391,7 +400,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   issue(Slot<2>{}, 2);
 #pragma unroll
   for (int j = 0; j < kRing; ++j) {
-    load_bchunk(rb[j], xt, xts, uint32_t(j), lane);
+    load_bchunk(rb[j], xt, xts, uint32_t(j), tb, sbb);
     __builtin_amdgcn_sched_barrier(0);  // chunk order, so the loop's waits count the ring right
   }
   v16f g, u;
@@ -414,7 +423,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       g = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a_operand(a1), B, g, 4, 0, 0, int(c1), 0, int(cb));
       u = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a_operand(a3), B, u, 4, 0, 0, int(c3), 0, int(cb));
     }
-    if (refill) load_bchunk(rb[S], xt, xts, c + kRing, lane);
+    if (refill) load_bchunk(rb[S], xt, xts, c + kRing, tb, sbb);
     // keep the refill here: left free, the scheduler sinks loads to the end
     // of the loop body, and the next round's first wait then drains the ring
     __builtin_amdgcn_sched_barrier(0);
@@ -508,13 +517,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
   }
   const Rsrc ht = make_rsrc(ws.ht + size_t(item) * kHTileBytes, kHTileBytes);
   const Rsrc hts = make_rsrc(ws.hts + size_t(item) * kHScaleBytes, kHScaleBytes);
+  const bool live = col < it.count;
+  const uint32_t tb = bcol_base(lane, live), sbb = bscale_base(lane, live);
   BChunk rb[kRing];
   issue(Slot<0>{}, 0);
   issue(Slot<1>{}, 1);
   issue(Slot<2>{}, 2);
 #pragma unroll
   for (int j = 0; j < kRing; ++j) {
-    load_bchunk(rb[j], ht, hts, uint32_t(j), lane);
+    load_bchunk(rb[j], ht, hts, uint32_t(j), tb, sbb);
     __builtin_amdgcn_sched_barrier(0);  // chunk order, so the loop's waits count the ring right
   }
   v16f d[1];
@@ -534,7 +545,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
       d[0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a_operand(aw), b_operand(rb[S].lo[k], rb[S].hi[k]), d[0],
                                                               4, 0, 0, int(ca), 0, int(cb));
     }
-    if (refill) load_bchunk(rb[S], ht, hts, c + kRing, lane);
+    if (refill) load_bchunk(rb[S], ht, hts, c + kRing, tb, sbb);
     __builtin_amdgcn_sched_barrier(0);  // as in phase 1
   };
   static_assert(kRing == 4 && kChunks % 4 == 0 && kChunks >= 8, "four ring slots, whole rounds");
