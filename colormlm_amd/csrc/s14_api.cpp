@@ -539,6 +539,11 @@ int prefill_workspace(s14_ctx *ctx) {
   const size_t o_down = take(sizeof(float) * size_t(P) * kHidden);
   S14_HIP(hipSetDevice(ctx->device), "hipSetDevice");
   S14_HIP(hipMalloc(&ctx->prefill_base, off), "hipMalloc(prefill workspace)");
+  // the token bitmaps start clear; every prefill's grouping step clears them again
+  S14_HIP(hipMemset(static_cast<uint8_t *>(ctx->prefill_base) + o_bits, 0,
+                    sizeof(uint32_t) * kMaxExperts * kPrefillBitWords),
+          "hipMemset(prefill bitmaps)");
+  S14_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
   uint8_t *b = static_cast<uint8_t *>(ctx->prefill_base);
   PrefillWorkspace &w = ctx->pws;
   w.scores = reinterpret_cast<float *>(b + o_scores);

@@ -120,11 +120,6 @@ __global__ __launch_bounds__(256) void k_requant_rows(uint32_t rows, uint32_t k,
 // routing and grouping
 // ---------------------------------------------------------------------------
 
-__global__ void k_zero_u32(uint32_t n, uint32_t *__restrict__ p) {
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
-}
-
 // One wavefront per token: top-k, route weights, and the expert's token bit.
 __global__ __launch_bounds__(256) void k_prefill_topk(PrefillArgs a, PrefillWorkspace ws) {
   const uint32_t lane = threadIdx.x & 63;
@@ -148,40 +143,90 @@ __global__ __launch_bounds__(256) void k_prefill_topk(PrefillArgs a, PrefillWork
 // order within its expert, and the GEMM work items (<= kItemTokens tokens of
 // one expert each).  Deterministic: positions come from bit counts.
 __global__ __launch_bounds__(1024) void k_prefill_group(PrefillArgs a, PrefillWorkspace ws) {
+  __shared__ uint32_t bits[kMaxExperts][kPrefillBitWords];  // the token bitmaps, read once
+  __shared__ uint16_t below[kMaxExperts][kPrefillBitWords];  // tokens of the expert in words < w
   __shared__ uint32_t cnt[kMaxExperts + 1];
   __shared__ uint32_t off[kMaxExperts + 2];
   __shared__ uint32_t items_of[kMaxExperts + 1];
   __shared__ uint32_t item_off[kMaxExperts + 2];
   const uint32_t tid = threadIdx.x;
   const uint32_t T = a.tokens, words = (T + 31) / 32;
+  // read the bitmaps and leave them clear for the next call's top-k (the
+  // workspace starts clear), which saves a clearing launch per call
+  for (uint32_t i = tid; i < kMaxExperts * kPrefillBitWords; i += blockDim.x) {
+    const uint32_t w = i % kPrefillBitWords;
+    uint32_t v = 0u;
+    if (w < words) {
+      v = ws.token_bits[i];
+      ws.token_bits[i] = 0u;
+    }
+    bits[i / kPrefillBitWords][w] = v;
+  }
+  __syncthreads();
   for (uint32_t e = tid; e <= kMaxExperts; e += blockDim.x) {
     uint32_t c = 0;
-    if (e < kMaxExperts)
-      for (uint32_t w = 0; w < words; ++w) c += __popc(ws.token_bits[e * kPrefillBitWords + w]);
-    else
+    if (e < kMaxExperts) {
+      for (uint32_t w = 0; w < words; ++w) {
+        below[e][w] = uint16_t(c);
+        c += __popc(bits[e][w]);
+      }
+    } else {
       c = T;  // shared expert: every token
+    }
     cnt[e] = c;
     items_of[e] = (c + kItemTokens - 1) / kItemTokens;
   }
   __syncthreads();
-  if (tid == 0) {  // 257 entries: a serial scan is cheaper than a barrier tree
-    uint32_t o = 0, io = 0, distinct = 0, mx = 0;
-    for (uint32_t e = 0; e <= kMaxExperts; ++e) {
-      off[e] = o;
-      item_off[e] = io;
-      o += cnt[e];
-      io += items_of[e];
-      if (e < kMaxExperts && cnt[e]) {
+  if (tid < 64) {
+    // exclusive scans of the 257 counts and item counts by one wavefront:
+    // lane l sums experts 5l .. 5l+4, then an inclusive scan over lanes
+    constexpr uint32_t kPer = (kMaxExperts + 1 + 63) / 64;  // 5
+    uint32_t c[kPer], n[kPer], sc = 0, sn = 0, distinct = 0, mx = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; ++j) {
+      const uint32_t e = kPer * tid + j;
+      c[j] = e <= kMaxExperts ? cnt[e] : 0u;
+      n[j] = e <= kMaxExperts ? items_of[e] : 0u;
+      sc += c[j];
+      sn += n[j];
+      if (e < kMaxExperts && c[j]) {
         ++distinct;
-        mx = cnt[e] > mx ? cnt[e] : mx;
+        mx = c[j] > mx ? c[j] : mx;
       }
     }
-    off[kMaxExperts + 1] = o;
-    item_off[kMaxExperts + 1] = io;
-    ws.stats[0] = io;  // number of work items
-    ws.stats[1] = distinct;
-    ws.stats[2] = mx;
-    ws.stats[3] = o;  // number of pairs
+    uint32_t ic = sc, in = sn;
+#pragma unroll
+    for (uint32_t d = 1; d < 64; d <<= 1) {
+      const uint32_t pc = __shfl_up(ic, d), pn = __shfl_up(in, d);
+      if (tid >= d) {
+        ic += pc;
+        in += pn;
+      }
+    }
+    uint32_t oc = ic - sc, on = in - sn;  // exclusive starts of this lane's experts
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; ++j) {
+      const uint32_t e = kPer * tid + j;
+      if (e <= kMaxExperts) {
+        off[e] = oc;
+        item_off[e] = on;
+      }
+      oc += c[j];
+      on += n[j];
+    }
+    for (uint32_t m = 32; m >= 1; m >>= 1) {
+      distinct += __shfl_xor(distinct, m);
+      const uint32_t o = __shfl_xor(mx, m);
+      mx = o > mx ? o : mx;
+    }
+    if (tid == 63) {
+      off[kMaxExperts + 1] = ic;
+      item_off[kMaxExperts + 1] = in;
+      ws.stats[0] = in;  // number of work items
+      ws.stats[1] = distinct;
+      ws.stats[2] = mx;
+      ws.stats[3] = ic;  // number of pairs
+    }
   }
   __syncthreads();
   // work items
@@ -196,10 +241,7 @@ __global__ __launch_bounds__(1024) void k_prefill_group(PrefillArgs a, PrefillWo
   for (uint32_t t = tid; t < T; t += blockDim.x) {
     for (uint32_t s = 0; s < a.r.topk; ++s) {
       const uint32_t e = ws.ids[t * kTopK + s];
-      const uint32_t *bits = ws.token_bits + e * kPrefillBitWords;
-      uint32_t rank = 0;
-      for (uint32_t w = 0; w < (t >> 5); ++w) rank += __popc(bits[w]);
-      rank += __popc(bits[t >> 5] & ((1u << (t & 31)) - 1u));
+      const uint32_t rank = below[e][t >> 5] + __popc(bits[e][t >> 5] & ((1u << (t & 31)) - 1u));
       const uint32_t p = off[e] + rank;
       ws.pair_token[p] = t;
       ws.token_pair[t * kSlots + s] = p;
@@ -214,9 +256,10 @@ __global__ __launch_bounds__(1024) void k_prefill_group(PrefillArgs a, PrefillWo
 // grouped GEMMs
 // ---------------------------------------------------------------------------
 
-// Each work item's x rows (MFMA order, from requant_x) into the item's tile,
-// zero past its count.  One thread per 16 tile bytes; the thread holding
-// part 0 of the first step of a chunk also writes that chunk's scale word.
+// Each work item's x rows (MFMA order, from requant_x) into the item's tile.
+// Columns past the item's count are not written: the GEMMs never read them.
+// One thread per 16 tile bytes; the thread holding part 0 of the first step
+// of a chunk also writes that chunk's scale word.
 __global__ __launch_bounds__(256) void k_tile_x(PrefillWorkspace ws) {
   constexpr uint32_t kPerItem = kXTileBytes / 16;
   const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
@@ -226,18 +269,15 @@ __global__ __launch_bounds__(256) void k_tile_x(PrefillWorkspace ws) {
   const uint32_t lane = r & 63u, part = (r >> 6) & 1u, s = r >> 7;
   const uint32_t col = lane & 31u, h = lane >> 5;
   const PrefillItem it = ws.items[i];
-  const bool live = col < it.count;
-  const uint32_t t = live ? ws.pair_token[it.first + col] : 0u;
-  uint4 v = make_uint4(0u, 0u, 0u, 0u);
-  if (live) v = *reinterpret_cast<const uint4 *>(ws.xq + size_t(t) * kHidden + 64u * s + 32u * h + 16u * part);
-  *reinterpret_cast<uint4 *>(ws.xt + size_t(i) * kXTileBytes + 16u * r) = v;
+  if (col >= it.count) return;
+  const uint32_t t = ws.pair_token[it.first + col];
+  *reinterpret_cast<uint4 *>(ws.xt + size_t(i) * kXTileBytes + 16u * r) =
+      *reinterpret_cast<const uint4 *>(ws.xq + size_t(t) * kHidden + 64u * s + 32u * h + 16u * part);
   if (part == 0 && s % kChunkSteps == 0) {
     uint32_t word = 0;
-    if (live) {
-      const uint8_t *sc = ws.xs + size_t(t) * (kHidden / kQGroup) + 2u * s + h;  // group 2 (s + k) + h
+    const uint8_t *sc = ws.xs + size_t(t) * (kHidden / kQGroup) + 2u * s + h;  // group 2 (s + k) + h
 #pragma unroll
-      for (uint32_t k = 0; k < kChunkSteps; ++k) word |= uint32_t(sc[2u * k]) << (8u * k);
-    }
+    for (uint32_t k = 0; k < kChunkSteps; ++k) word |= uint32_t(sc[2u * k]) << (8u * k);
     reinterpret_cast<uint32_t *>(ws.xts + size_t(i) * kXScaleBytes)[(s / kChunkSteps) * 64u + lane] = word;
   }
 }
@@ -466,6 +506,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   amax = other > amax ? other : amax;
   const uint32_t code = requant_code(amax);
   const float inv = __uint_as_float((254u - code) << 23);
+  if (col >= it.count) return;  // phase 2 never reads absent columns
   // this tile's 32 rows are half blk of phase 2's K step s2 (group rt)
   const uint32_t s2 = rt >> 1, blk = rt & 1u;
   uint8_t *tile = ws.ht + size_t(item) * kHTileBytes + 2048u * s2;
@@ -617,8 +658,6 @@ hipError_t launch_prefill(hipStream_t s, const PrefillArgs &a, const PrefillWork
   rws.biased = ws.biased;
   hipError_t e = launch_router_scores(s, rws, a.r, T, a.x);
   if (e != hipSuccess) return e;
-  const uint32_t nbits = kMaxExperts * kPrefillBitWords;
-  k_zero_u32<<<(nbits + 255) / 256, 256, 0, s>>>(nbits, ws.token_bits);
   k_prefill_topk<<<(T + 3) / 4, 256, 0, s>>>(a, ws);
   k_prefill_group<<<1, 1024, 0, s>>>(a, ws);
   k_requant_x<<<(T * (kHidden / kQGroup) + 255) / 256, 256, 0, s>>>(T, a.x, ws.xq, ws.xs);

@@ -25,7 +25,7 @@ struct PrefillItem {
 // K step is two coalesced 1 KiB loads: tile[step][part][lane][16 bytes],
 // lane = column + 32 h holding bytes 32 h + 16 part .. +15 of the column's
 // 64-byte step block in MFMA order (columns past the item's count are
-// zero).  Scales: [chunk of kChunkSteps steps][lane] u32, byte k = the E8M0
+// neither written nor read).  Scales: [chunk of kChunkSteps steps][lane] u32, byte k = the E8M0
 // of step kChunkSteps * chunk + k for the lane's half.
 constexpr uint32_t kChunkSteps = 4;
 constexpr uint32_t kXTileBytes = (kHidden / 64) * 2048;                      // phase 1: 128 KiB
