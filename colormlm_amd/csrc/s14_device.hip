@@ -6,10 +6,12 @@
 //          (scheduler/ssd_inference/examples/s14_vulkan_numeric.rs:1669-1714),
 //          so outputs are bit-identical to it.  Each row is owned by a lane
 //          pair: in every group of 32 k the even lane forms the products of
-//          k 0..15 and the odd lane those of k 16..31; the even lane then adds
-//          its own 16 products and the odd lane's 16 (read through a DPP
-//          quad_perm operand of v_add) in k order.  The per-row dependent add
-//          chain, not HBM, bounds this order at batch 1.
+//          k 0..15 and the odd lane those of k 16..31; the running sum passes
+//          to the even lane, which adds its 16 products, then back to the odd
+//          lane, which adds its own 16, in k order (each hand-over a DPP
+//          quad_perm operand of v_add).  The per-row dependent add chain and
+//          the instruction issue around it, not HBM, bound this order at
+//          batch 1.
 //   FAST   K split across the 64 lanes of a wavefront, products fused
 //          (v_fma), DPP cross-lane reduction; HBM-bound.
 // The reference's five shaders (shaders/s14_*.comp) are one workgroup per
@@ -51,38 +53,6 @@ __device__ __forceinline__ CodeWindow mx_window(int emin, int emax) {
   return {max(2, 129 - emin), 252};
 }
 
-// Stage S vectors of N f32 (N % 256 == 0) from global memory into LDS with
-// the calling wavefront (lane-strided float4), returning each vector's
-// exponent window.  Every global load is issued before the first LDS store:
-// a generic source pointer may alias LDS, so the compiler would otherwise
-// wait for each load in turn.  The caller synchronises before reading the
-// LDS copies.
-template <int N, int S>
-__device__ __forceinline__ void stage_x_wave(float *const (&dst)[S], const float *const (&src)[S],
-                                             CodeWindow (&win)[S]) {
-  static_assert(N % 256 == 0, "whole float4 sweeps");
-  constexpr int IT = N / 256;
-  const int lane = int(threadIdx.x & 63);
-  float4 v[S][IT];
-#pragma unroll
-  for (int s = 0; s < S; ++s)
-#pragma unroll
-    for (int it = 0; it < IT; ++it) v[s][it] = *reinterpret_cast<const float4 *>(src[s] + it * 256 + lane * 4);
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    int lo = 255, hi = 0;
-#pragma unroll
-    for (int it = 0; it < IT; ++it) {
-      *reinterpret_cast<float4 *>(dst[s] + it * 256 + lane * 4) = v[s][it];
-      exp_range_acc(v[s][it].x, lo, hi);
-      exp_range_acc(v[s][it].y, lo, hi);
-      exp_range_acc(v[s][it].z, lo, hi);
-      exp_range_acc(v[s][it].w, lo, hi);
-    }
-    win[s] = mx_window(wave_min_i(lo), wave_max_i(hi));
-  }
-}
-
 // The copy alone, for vectors whose window is known (phase 2's h).
 template <int N, int S>
 __device__ __forceinline__ void stage_copy_wave(float *const (&dst)[S], const float *const (&src)[S]) {
@@ -100,8 +70,45 @@ __device__ __forceinline__ void stage_copy_wave(float *const (&dst)[S], const fl
     for (int it = 0; it < IT; ++it) *reinterpret_cast<float4 *>(dst[s] + it * 256 + lane * 4) = v[s][it];
 }
 
+// Stage one vector of N f32 into LDS with the whole workgroup of NT threads
+// (thread-strided float4) and return its exponent window to every thread;
+// red: LDS scratch of 2 NT / 64 ints.  Ends with a barrier, after which the
+// copy is visible to the workgroup.
+template <int N, int NT>
+__device__ __forceinline__ CodeWindow stage_x_block(float *dst, const float *__restrict__ src, int *red) {
+  static_assert(N % (4 * NT) == 0 && NT % 64 == 0, "whole float4 sweeps");
+  constexpr int IT = N / (4 * NT);
+  constexpr int W = NT / 64;
+  const int t = int(threadIdx.x);
+  float4 v[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) v[it] = *reinterpret_cast<const float4 *>(src + (it * NT + t) * 4);
+  int lo = 255, hi = 0;
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    *reinterpret_cast<float4 *>(dst + (it * NT + t) * 4) = v[it];
+    exp_range_acc(v[it].x, lo, hi);
+    exp_range_acc(v[it].y, lo, hi);
+    exp_range_acc(v[it].z, lo, hi);
+    exp_range_acc(v[it].w, lo, hi);
+  }
+  lo = wave_min_i(lo);
+  hi = wave_max_i(hi);
+  if ((t & 63) == 0) {
+    red[2 * (t >> 6)] = lo;
+    red[2 * (t >> 6) + 1] = hi;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    lo = min(lo, red[2 * w]);
+    hi = max(hi, red[2 * w + 1]);
+  }
+  return mx_window(lo, hi);
+}
+
 // Window of one pair's h from the exponent ranges its exact phase-1 tiles
-// recorded (lo | hi << 16 per tile): the same range stage_x_wave would find
+// recorded (lo | hi << 16 per tile): the same range stage_x_block would find
 // by scanning h.
 constexpr int kP1Tiles = kInter / kP1ExactRows;
 __device__ __forceinline__ CodeWindow h_window(const uint32_t *__restrict__ tiles) {
@@ -148,13 +155,20 @@ __device__ __forceinline__ void load_x16(X16 &x, const float *__restrict__ xs) {
   }
 }
 
-// acc = acc + p for the even lane's 16 products, then for the odd lane's 16,
-// in k order (the odd lane's result is not used).
+// One group of a lane pair's row chain, in k order: the running sum, held by
+// the odd lane between groups, passes to the even lane, which adds its 16
+// products; it passes back to the odd lane, which adds its own 16.  Each
+// hand-over is a DPP operand of the add that follows it (the other lane's
+// adds in each half are discarded), so a group costs 32 adds of which only
+// the two hand-overs read a just-written register across lanes and need
+// wait states.  A row starts from 0 in both lanes and ends with from_odd.
 __device__ __forceinline__ float pair_chain16(float acc, const float (&p)[16]) {
+  acc = __fadd_rn(from_odd(acc), p[0]);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) acc = __fadd_rn(acc, p[j]);
+  for (int j = 1; j < 16; ++j) acc = __fadd_rn(acc, p[j]);
+  acc = __fadd_rn(from_even(acc), p[0]);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) acc = __fadd_rn(acc, from_odd(p[j]));
+  for (int j = 1; j < 16; ++j) acc = __fadd_rn(acc, p[j]);
   return acc;
 }
 
@@ -177,45 +191,6 @@ __device__ __forceinline__ void mx_products_scaled(float (&p)[16], uint2 w, uint
     }
   }
 }
-// pair_chain16 of group g's products p with group g+1's products q formed
-// in between.  Each DPP add reads the accumulator the previous add wrote,
-// and a DPP read needs two wait states after that write: issued back to
-// back (as the scheduler otherwise leaves them) every DPP add waits behind
-// an s_nop.  Here q's 8 conversions and 16 multiplies sit between the DPP
-// adds, two before each while they last, and the scheduling barriers hold
-// that order; the 16 plain adds need no spacing and go first.
-__device__ __forceinline__ float pair_chain16_next(float acc, const float (&p)[16], float (&q)[16], uint2 w,
-                                                   uint32_t c, const X16 &x) {
-  const float sc = __uint_as_float(c << 23);
-  const uint32_t words[2] = {w.x, w.y};
-  v2f d[8];  // d[i]: byte i % 4 of word i / 4, scaled; q[2i], q[2i+1] use it
-#pragma unroll
-  for (int j = 0; j < 16; ++j) acc = __fadd_rn(acc, p[j]);
-#define S14_CVT(i) d[i] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[(i) >> 2], sc, (i)&3);
-#define S14_MUL(m) q[m] = __fmul_rn(x.v[m], ((m)&1) ? d[(m) >> 1].y : d[(m) >> 1].x);
-#define S14_DPP_ADD(j)                         \
-  __builtin_amdgcn_sched_barrier(0);           \
-  acc = __fadd_rn(acc, from_odd(p[j]));        \
-  __builtin_amdgcn_sched_barrier(0);
-  S14_CVT(0) S14_CVT(1) S14_DPP_ADD(0)
-  S14_MUL(0) S14_MUL(1) S14_DPP_ADD(1)
-  S14_CVT(2) S14_MUL(2) S14_DPP_ADD(2)
-  S14_MUL(3) S14_CVT(3) S14_DPP_ADD(3)
-  S14_MUL(4) S14_MUL(5) S14_DPP_ADD(4)
-  S14_CVT(4) S14_MUL(6) S14_DPP_ADD(5)
-  S14_MUL(7) S14_CVT(5) S14_DPP_ADD(6)
-  S14_MUL(8) S14_MUL(9) S14_DPP_ADD(7)
-  S14_CVT(6) S14_MUL(10) S14_DPP_ADD(8)
-  S14_MUL(11) S14_CVT(7) S14_DPP_ADD(9)
-  S14_MUL(12) S14_MUL(13) S14_DPP_ADD(10)
-  S14_MUL(14) S14_MUL(15) S14_DPP_ADD(11)
-  S14_DPP_ADD(12) S14_DPP_ADD(13) S14_DPP_ADD(14) S14_DPP_ADD(15)
-#undef S14_CVT
-#undef S14_MUL
-#undef S14_DPP_ADD
-  return acc;
-}
-
 // Literal: p = (x * e2m1) * ue8m0(c), any code.
 __device__ __forceinline__ void mx_products_literal(float (&p)[16], uint2 w, uint32_t c, const X16 &x) {
   const float s = ue8m0_f32(c);
@@ -320,12 +295,11 @@ __device__ __forceinline__ float mx_consume(float acc, const MxBatch<PF> &b, con
     for (int i = 0; i < PF; i += 2) {
       // p holds group i's products; xb holds group i+1's x
       if (i + 2 < PF) load_x16(xa, xh + (g0 + i + 2) * 32);
-      acc = pair_chain16_next(acc, p, q, b.w[i + 1], batch_code(b, i + 1), xb);
+      mx_products_scaled(q, b.w[i + 1], batch_code(b, i + 1), xb);
+      acc = pair_chain16(acc, p);
       if (i + 3 < PF) load_x16(xb, xh + (g0 + i + 3) * 32);
-      if (i + 2 < PF)
-        acc = pair_chain16_next(acc, q, p, b.w[i + 2], batch_code(b, i + 2), xa);
-      else
-        acc = pair_chain16(acc, q);
+      if (i + 2 < PF) mx_products_scaled(p, b.w[i + 2], batch_code(b, i + 2), xa);
+      acc = pair_chain16(acc, q);
     }
   } else {
 #pragma unroll 1
@@ -341,7 +315,7 @@ __device__ __forceinline__ float mx_consume(float acc, const MxBatch<PF> &b, con
 }
 
 // Dot of one MXFP4 row of G groups (G % PF == 0) with x in LDS (xh = x +
-// 16 * (lane & 1)); result in the even lane.  `ba` arrives holding groups
+// 16 * (lane & 1)); result in both lanes.  `ba` arrives holding groups
 // [0, PF) (loaded by the caller with mx_load, ahead of its own set-up work);
 // two register batches of PF groups then ping-pong so that batch b+1 is in
 // flight while batch b is consumed.  (The loop prefetches one batch past
@@ -359,7 +333,7 @@ __device__ __forceinline__ float mx_row_pair(float acc, MxBatch<PF> &ba, const S
     acc = mx_consume<PF>(acc, bb, src, woff, soff, xh, g0 + PF, win);
   }
   if (g0 < G) acc = mx_consume<PF>(acc, ba, src, woff, soff, xh, g0, win);  // one batch left
-  return acc;
+  return from_odd(acc);
 }
 
 // The same for a compile-time group count G (G % (2 PF) == 0), with the
@@ -379,7 +353,7 @@ __device__ __forceinline__ float mx_row_pair_fixed(float acc, MxBatch<PF> &ba, c
   mx_load<PF>(bb, src, woff, soff, G - PF);
   acc = mx_consume<PF>(acc, ba, src, woff, soff, xh, G - 2 * PF, win);
   acc = mx_consume<PF>(acc, bb, src, woff, soff, xh, G - PF, win);
-  return acc;
+  return from_odd(acc);
 }
 
 // FP8 products of the lane's 16 code bytes: p = (x * e4m3) * s
@@ -439,7 +413,7 @@ __device__ __forceinline__ float fp8_consume(float acc, const Fp8Batch &b, const
 
 // Dot of one FP8 row of G groups of 32 k with x in LDS (woff includes the
 // lane's 16-byte half-group offset; soff is the byte offset of the row's
-// first tile scale); result in the even lane.
+// first tile scale); result in both lanes.
 template <class Src>
 __device__ __forceinline__ float fp8_row_pair(float acc, const Src &src, uint32_t woff, uint32_t soff,
                                               int scale_f32, int G, const float *__restrict__ xh) {
@@ -466,7 +440,7 @@ __device__ __forceinline__ float fp8_row_pair(float acc, const Src &src, uint32_
     fp8_products(p, t.w[0], t.s, x);
     acc = pair_chain16(acc, p);
   }
-  return acc;
+  return from_odd(acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -1161,41 +1135,41 @@ __device__ __forceinline__ uint32_t page_bytes(uint32_t fmt) {
   return fmt == S14_PAGE_MXFP4 ? uint32_t(S14_EXPERT_PAGE_BYTES) : uint32_t(S14_SHARED_EXPERT_PAGE_BYTES);
 }
 
-// Phase 1 EXACT: one wavefront per (16-row tile, pair); lanes 0-31 take the
-// tile's rows of w1, lanes 32-63 the same rows of w3, one row per lane pair;
-// h = swiglu(g, u) after a half swap.
+// Phase 1 EXACT: one workgroup of kP1ExactWaves wavefronts per (tile group,
+// pair), the pair's x staged in LDS once for all of them; each wavefront
+// takes one 16-row tile: lanes 0-31 its rows of w1, lanes 32-63 the same
+// rows of w3, one row per lane pair; h = swiglu(g, u) after a half swap.
 // kTier (1: single-token launch, 8: block launch) only names the
 // instantiation, so traces and profiles keep the two workloads apart.
 template <bool kHostPlan, int kTier>
-__global__ __launch_bounds__(64) void k_phase1_exact(PairTable plan, Workspace ws, const float *__restrict__ X,
-                                                     PageOffsets mx, PageOffsets f8) {
+__global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable plan, Workspace ws,
+                                                                     const float *__restrict__ X, PageOffsets mx,
+                                                                     PageOffsets f8) {
   __shared__ float xs[kHidden];
   __shared__ double exptab[32];
-  exp_table_fill(exptab);  // published by the barrier after the x copy
+  __shared__ int red[2 * kP1ExactWaves];
+  exp_table_fill(exptab);  // published by the barrier in the x copy
   const uint32_t p = blockIdx.y;
   const PairRef pr = phase1_pair<kHostPlan>(plan, ws.table, p);
-  const uint32_t lane = threadIdx.x, h = lane & 1u;
+  const uint32_t lane = threadIdx.x & 63, h = lane & 1u;
+  const uint32_t tile = blockIdx.x * kP1ExactWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool upper = lane >= 32;
-  const uint32_t row = blockIdx.x * kP1ExactRows + ((lane & 31u) >> 1);
+  const uint32_t row = tile * kP1ExactRows + ((lane & 31u) >> 1);
   const Rsrc r = make_rsrc(pr.page, page_bytes(pr.fmt));
   const Src1 src{r, r};
-  float *const dst[1] = {xs};
-  const float *const srcx[1] = {X + size_t(pr.token) * kHidden};
-  CodeWindow win[1];
+  const float *const srcx = X + size_t(pr.token) * kHidden;
   float acc;
   if (pr.fmt == S14_PAGE_MXFP4) {
     const uint32_t woff = uint32_t(upper ? mx.w3 : mx.w1) + row * (kHidden / 2) + 8u * h;
     const uint32_t soff = uint32_t(upper ? mx.s3 : mx.s1) + row * (kHidden / 32);
     MxBatch<kPF> ba;
     mx_load<kPF>(ba, src, woff, soff, 0);  // first weights in flight during the x copy
-    stage_x_wave<kHidden, 1>(dst, srcx, win);
-    __syncthreads();
-    acc = mx_row_pair_fixed<kPF, kHidden / 32>(0.0f, ba, src, woff, soff, xs + 16 * h, win[0]);
+    const CodeWindow win = stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
+    acc = mx_row_pair_fixed<kPF, kHidden / 32>(0.0f, ba, src, woff, soff, xs + 16 * h, win);
   } else {
     const uint32_t woff = uint32_t(upper ? f8.w3 : f8.w1) + row * kHidden + 16u * h;
     const uint32_t soff = uint32_t(upper ? f8.s3 : f8.s1) + (row / 128) * (kHidden / 128);
-    stage_x_wave<kHidden, 1>(dst, srcx, win);
-    __syncthreads();
+    stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
     acc = fp8_row_pair(0.0f, src, woff, soff, 0, kHidden / 32, xs + 16 * h);
   }
   const float other = __shfl_xor(acc, 32);
@@ -1210,7 +1184,7 @@ __global__ __launch_bounds__(64) void k_phase1_exact(PairTable plan, Workspace w
   // without scanning h
   lo = wave_min_i(lo);
   hi = wave_max_i(hi);
-  if (lane == 0) ws.hwin[size_t(p) * kP1Tiles + blockIdx.x] = uint32_t(lo) | (uint32_t(hi) << 16);
+  if (lane == 0) ws.hwin[size_t(p) * kP1Tiles + tile] = uint32_t(lo) | (uint32_t(hi) << 16);
 }
 
 // Phase 1 FAST: 4 wavefronts per workgroup; each streams kP1FastRowsPerWave
@@ -1546,13 +1520,13 @@ void phase1_tier(hipStream_t s, const Workspace &ws, const PairTable *host_plan,
       hipExtLaunchKernelGGL(k_phase1_fast<false, kTier>, grid, dim3(256), 0, s, ev.start, ev.stop, 0, plan, ws, x,
                             mx, fp8);
   } else {
-    const dim3 grid(kInter / kP1ExactRows, n_pairs);
+    const dim3 grid(kInter / (kP1ExactRows * kP1ExactWaves), n_pairs);
     if (host_plan)
-      hipExtLaunchKernelGGL(k_phase1_exact<true, kTier>, grid, dim3(64), 0, s, ev.start, ev.stop, 0, plan, ws, x, mx,
-                            fp8);
+      hipExtLaunchKernelGGL(k_phase1_exact<true, kTier>, grid, dim3(64 * kP1ExactWaves), 0, s, ev.start, ev.stop, 0,
+                            plan, ws, x, mx, fp8);
     else
-      hipExtLaunchKernelGGL(k_phase1_exact<false, kTier>, grid, dim3(64), 0, s, ev.start, ev.stop, 0, plan, ws, x,
-                            mx, fp8);
+      hipExtLaunchKernelGGL(k_phase1_exact<false, kTier>, grid, dim3(64 * kP1ExactWaves), 0, s, ev.start, ev.stop, 0,
+                            plan, ws, x, mx, fp8);
   }
 }
 

@@ -21,6 +21,7 @@ constexpr int kMaxExperts = 256;
 // same 16 rows of w3 per wavefront; phase 2 = 16 rows of w2 for each of the
 // token's pairs, two pairs per wavefront.
 constexpr int kP1ExactRows = 16;
+constexpr int kP1ExactWaves = 4;  // phase-1 row tiles per workgroup, sharing one staged x
 constexpr int kP2ExactRows = 16;
 constexpr int kP2ExactWaves = 4;
 // Fast-mode tiles: phase 1 = 4 wavefronts x 8 rows of w1 and w3 (streamed); phase 2 =

@@ -160,6 +160,10 @@ __device__ __forceinline__ int dpp_i(int old, int v) {
 __device__ __forceinline__ float from_odd(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xF5, 0xf, 0xf, true));
 }
+// Value of the even lane of each lane pair (quad_perm [0,0,2,2]).
+__device__ __forceinline__ float from_even(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xA0, 0xf, 0xf, true));
+}
 
 // Full-wavefront sum (order-changing; FAST mode only), returned to every lane.
 __device__ __forceinline__ float wave_sum_dpp(float v) {
