@@ -273,19 +273,67 @@ __device__ __forceinline__ uint32_t src_ld1(const Src2 &s, uint32_t off) {
   return v;
 }
 
+// The scale codes of a lane pair's row, split between its lanes (the even
+// lane holds groups [0, G/2), the odd lane [G/2, G)), loaded ahead of the
+// row so that one check decides the decode of the whole row.
+template <int G>
+struct RowCodes {
+  uint4 v[G / 32];
+};
+template <int G>
+__device__ __forceinline__ void load_row_codes(RowCodes<G> &rc, const Src1 &src, uint32_t soff) {
+  const uint32_t base = soff + (threadIdx.x & 1u) * uint32_t(G / 2);
+#pragma unroll
+  for (int i = 0; i < G / 32; ++i) rc.v[i] = ld16(src.s, base + 16u * i);
+}
+template <int G>
+__device__ __forceinline__ void load_row_codes(RowCodes<G> &rc, const SrcP &src, uint32_t soff) {
+  const uint32_t base = soff + (threadIdx.x & 1u) * uint32_t(G / 2);
+#pragma unroll
+  for (int i = 0; i < G / 32; ++i) {
+    const v4u v = *(const __attribute__((address_space(1))) v4u *)(src.p + base + 16u * i);
+    rc.v[i] = make_uint4(v.x, v.y, v.z, v.w);
+  }
+}
+
+// True (in every lane) when every scale code of every row of the wavefront
+// lies in its lane's window: byte minimum and maximum through packed 16-bit
+// min/max of the even and odd bytes.
+template <int G>
+__device__ __forceinline__ bool row_codes_in(const RowCodes<G> &rc, CodeWindow win) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  u16x2 mn = {255, 255}, mx = {0, 0};
+#pragma unroll
+  for (int i = 0; i < G / 32; ++i) {
+    const uint32_t w[4] = {rc.v[i].x, rc.v[i].y, rc.v[i].z, rc.v[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u16x2 lo = __builtin_bit_cast(u16x2, w[j] & 0x00ff00ffu);
+      const u16x2 hi = __builtin_bit_cast(u16x2, (w[j] >> 8) & 0x00ff00ffu);
+      mn = __builtin_elementwise_min(mn, __builtin_elementwise_min(lo, hi));
+      mx = __builtin_elementwise_max(mx, __builtin_elementwise_max(lo, hi));
+    }
+  }
+  const int cmin = min(int(mn.x), int(mn.y)), cmax = max(int(mx.x), int(mx.y));
+  const bool ok = cmin >= win.cmin && cmax <= win.cmax;
+  return __builtin_amdgcn_ballot_w64(!ok) == 0;
+}
+
 // One batch: if every lane's codes are inside its window the batch runs the
 // scaled decode as straight-line code, software-pipelined: group i+1's x
 // reads and products are issued ahead of group i's add chain, so LDS latency
 // and the chain's DPP read-after-write waits overlap independent work.
 // Otherwise the batch takes the literal decode, group by group, re-reading
 // its codes (compact code for a path real scale codes do not take).
-template <int PF, class Src>
+template <int PF, bool kCheck = true, class Src>
 __device__ __forceinline__ float mx_consume(float acc, const MxBatch<PF> &b, const Src &src, uint32_t woff,
                                             uint32_t soff, const float *__restrict__ xh, int g0, CodeWindow win) {
   bool ok = true;
+  if constexpr (kCheck) {
 #pragma unroll
-  for (int j = 0; j < PF / 4; ++j) ok = ok && codes_in(b.c[j], win);
-  if (__builtin_amdgcn_ballot_w64(!ok) == 0) {
+    for (int j = 0; j < PF / 4; ++j) ok = ok && codes_in(b.c[j], win);
+  }
+  if (!kCheck || __builtin_amdgcn_ballot_w64(!ok) == 0) {
     X16 xa, xb;
     float p[16], q[16];
     load_x16(xa, xh + g0 * 32);
@@ -337,7 +385,8 @@ __device__ __forceinline__ float mx_row_pair(float acc, MxBatch<PF> &ba, const S
 }
 
 // The same for a compile-time group count G (G % (2 PF) == 0), with the
-// last two batches peeled so that no load reaches past the row.
+// last two batches peeled so that no load reaches past the row (decode
+// chosen batch by batch).
 template <int PF, int G, class Src>
 __device__ __forceinline__ float mx_row_pair_fixed(float acc, MxBatch<PF> &ba, const Src &src, uint32_t woff,
                                                    uint32_t soff, const float *__restrict__ xh, CodeWindow win) {
@@ -353,6 +402,39 @@ __device__ __forceinline__ float mx_row_pair_fixed(float acc, MxBatch<PF> &ba, c
   mx_load<PF>(bb, src, woff, soff, G - PF);
   acc = mx_consume<PF>(acc, ba, src, woff, soff, xh, G - 2 * PF, win);
   acc = mx_consume<PF>(acc, bb, src, woff, soff, xh, G - PF, win);
+  return from_odd(acc);
+}
+
+// The same with the decode chosen once for the whole row from its codes (rc,
+// loaded by the caller with load_row_codes): the scaled batches with no
+// per-batch check, or the literal decode group by group.
+template <int PF, int G, class Src>
+__device__ __forceinline__ float mx_row_pair_fixed(float acc, MxBatch<PF> &ba, const Src &src, uint32_t woff,
+                                                   uint32_t soff, const float *__restrict__ xh, CodeWindow win,
+                                                   const RowCodes<G> &rc) {
+  static_assert(PF % 4 == 0 && G % (2 * PF) == 0, "whole batch pairs");
+  if (row_codes_in<G>(rc, win)) {
+    MxBatch<PF> bb;
+#pragma unroll 1
+    for (int g0 = 0; g0 < G - 2 * PF; g0 += 2 * PF) {
+      mx_load<PF>(bb, src, woff, soff, g0 + PF);
+      acc = mx_consume<PF, false>(acc, ba, src, woff, soff, xh, g0, win);
+      mx_load<PF>(ba, src, woff, soff, g0 + 2 * PF);
+      acc = mx_consume<PF, false>(acc, bb, src, woff, soff, xh, g0 + PF, win);
+    }
+    mx_load<PF>(bb, src, woff, soff, G - PF);
+    acc = mx_consume<PF, false>(acc, ba, src, woff, soff, xh, G - 2 * PF, win);
+    acc = mx_consume<PF, false>(acc, bb, src, woff, soff, xh, G - PF, win);
+  } else {
+#pragma unroll 1
+    for (int g = 0; g < G; ++g) {
+      float p[16];
+      X16 x;
+      load_x16(x, xh + g * 32);
+      mx_products_literal(p, src_ld8(src, woff + 16u * uint32_t(g)), src_ld1(src, soff + uint32_t(g)), x);
+      acc = pair_chain16(acc, p);
+    }
+  }
   return from_odd(acc);
 }
 
@@ -1139,8 +1221,9 @@ __device__ __forceinline__ uint32_t page_bytes(uint32_t fmt) {
 // pair), the pair's x staged in LDS once for all of them; each wavefront
 // takes one 16-row tile: lanes 0-31 its rows of w1, lanes 32-63 the same
 // rows of w3, one row per lane pair; h = swiglu(g, u) after a half swap.
-// kTier (1: single-token launch, 8: block launch) only names the
-// instantiation, so traces and profiles keep the two workloads apart.
+// kTier (1: single-token launch, 8: block launch) names the instantiation,
+// so traces and profiles keep the two workloads apart, and picks the code
+// check (per row at batch 1, per batch of groups for blocks).
 template <bool kHostPlan, int kTier>
 __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable plan, Workspace ws,
                                                                      const float *__restrict__ X, PageOffsets mx,
@@ -1164,8 +1247,17 @@ __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable p
     const uint32_t soff = uint32_t(upper ? mx.s3 : mx.s1) + row * (kHidden / 32);
     MxBatch<kPF> ba;
     mx_load<kPF>(ba, src, woff, soff, 0);  // first weights in flight during the x copy
-    const CodeWindow win = stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
-    acc = mx_row_pair_fixed<kPF, kHidden / 32>(0.0f, ba, src, woff, soff, xs + 16 * h, win);
+    if constexpr (kTier == 1) {
+      // batch 1 (one wavefront per SIMD, issue-bound): one code check per row
+      RowCodes<kHidden / 32> rc;
+      load_row_codes<kHidden / 32>(rc, src, soff);
+      const CodeWindow win = stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
+      acc = mx_row_pair_fixed<kPF, kHidden / 32>(0.0f, ba, src, woff, soff, xs + 16 * h, win, rc);
+    } else {
+      // blocks: per-batch code checks measured faster here
+      const CodeWindow win = stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
+      acc = mx_row_pair_fixed<kPF, kHidden / 32>(0.0f, ba, src, woff, soff, xs + 16 * h, win);
+    }
   } else {
     const uint32_t woff = uint32_t(upper ? f8.w3 : f8.w1) + row * kHidden + 16u * h;
     const uint32_t soff = uint32_t(upper ? f8.s3 : f8.s1) + (row / 128) * (kHidden / 128);
@@ -1320,8 +1412,11 @@ __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairT
   // both halves MXFP4 (the normal case): per-lane page pointers
   const SrcP srcp{(GPtr)(hi && has_b ? ub : ua)};
   MxBatch<kPF> ba;
-  if (has_a && fa == S14_PAGE_MXFP4 && fb == S14_PAGE_MXFP4)
-    mx_load<kPF>(ba, srcp, mx_woff, mx_soff, 0);  // first weights in flight during the h copy
+  RowCodes<kInter / 32> rc;
+  if (has_a && fa == S14_PAGE_MXFP4 && fb == S14_PAGE_MXFP4) {
+    mx_load<kPF>(ba, srcp, mx_woff, mx_soff, 0);  // first weights and the row's codes in flight during the h copy
+    load_row_codes<kInter / 32>(rc, srcp, mx_soff);
+  }
   CodeWindow win[2] = {{256, 0}, {256, 0}};
   if (has_b) {
     float *const dst[2] = {hs[sa], hs[sb]};
@@ -1340,11 +1435,11 @@ __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairT
     const float *xh = hs[slot] + 16 * h;
     float acc;
     if (fa == S14_PAGE_MXFP4 && fb == S14_PAGE_MXFP4) {
-      acc = mx_row_pair_fixed<kPF, kInter / 32>(0.0f, ba, srcp, mx_woff, mx_soff, xh, (hi ? win[1] : win[0]));
+      acc = mx_row_pair_fixed<kPF, kInter / 32>(0.0f, ba, srcp, mx_woff, mx_soff, xh, (hi ? win[1] : win[0]), rc);
     } else if (mine_mx) {  // formats differ between the halves
       MxBatch<kPF> bm;
       mx_load<kPF>(bm, src, mx_woff, mx_soff, 0);
-      acc = mx_row_pair_fixed<kPF, kInter / 32>(0.0f, bm, src, mx_woff, mx_soff, xh, (hi ? win[1] : win[0]));
+      acc = mx_row_pair<kPF>(0.0f, bm, src, mx_woff, mx_soff, kInter / 32, xh, (hi ? win[1] : win[0]));
     } else {
       acc = fp8_row_pair(0.0f, src, uint32_t(f8.w2) + row * kInter + 16u * h,
                          uint32_t(f8.s2) + (row / 128) * (kInter / 128), 0, kInter / 32, xh);

@@ -239,6 +239,31 @@ def test_expert_chain_config0(ctx, oracle):
     assert st["max_abs"] <= 2e-4 and st["rmse"] <= 2.5e-5
 
 
+@pytest.mark.parametrize("tiny_x", [False, True])
+def test_expert_chain_edge_scale_codes(ctx, oracle, tiny_x):
+    """Rows whose scale codes leave the scaled-decode window (tiny scales:
+    subnormal products) in w1, w3 and w2, among rows that stay inside, so
+    that some wavefronts take the literal decode for all their rows; with
+    tiny_x a subnormal activation narrows the window for every row."""
+    say(f"expert chain edge codes tiny_x={tiny_x}")
+    cfg = synth.config0(seed=3)
+    page = cfg["page"].copy()
+    o = synth.page_offsets("mxfp4")
+    g_up, g_dn = HIDDEN // 32, INTER // 32
+    page[o["s1"] + 5 * g_up: o["s1"] + 5 * g_up + 7] = [0, 1, 2, 3, 4, 5, 6]
+    page[o["s3"] + 40 * g_up + 100] = 9
+    page[o["s1"] + 2047 * g_up + 127] = 1
+    page[o["s2"] + 77 * g_dn: o["s2"] + 77 * g_dn + 3] = [3, 0, 8]
+    page[o["s2"] + 4095 * g_dn + 63] = 2
+    x = cfg["x"].copy()
+    if tiny_x:
+        x[11] = np.float32(1e-39)
+    want = oracle.expert_chain(x, page, float(cfg["route_w"]))
+    y = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    s14.expert_chain(ctx, dev(page), dev(x), float(cfg["route_w"]), y, mode=s14.EXACT)
+    assert_bit_exact(host(y), want, "chain exact edge codes")
+
+
 @pytest.fixture(scope="module")
 def bank(ctx):
     """256 routed MXFP4 pages + 1 MXFP4 shared page of layer 0, on device."""
