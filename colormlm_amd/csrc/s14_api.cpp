@@ -117,7 +117,7 @@ extern "C" int s14_ctx_create(int device, s14_ctx **out) {
   const size_t o_biased = off;
   off = align_up(off + sizeof(float) * s14::kMaxTokens * s14::kMaxExperts, 256);
   const size_t o_count = off;
-  off = align_up(off + sizeof(uint32_t) * (1 + s14::kMaxTokens), 256);
+  off = align_up(off + sizeof(uint32_t) * s14::kRouteCounters, 256);
   const size_t o_hwin = off;
   off = align_up(off + sizeof(uint32_t) * s14::kMaxPairs * (s14::kInter / s14::kP1ExactRows), 256);
   e = hipMalloc(&ctx->ws_base, off);

@@ -53,21 +53,30 @@ __device__ __forceinline__ CodeWindow mx_window(int emin, int emax) {
   return {max(2, 129 - emin), 252};
 }
 
-// The copy alone, for vectors whose window is known (phase 2's h).
+// The copy alone, for vectors whose window is known (phase 2's h), in two
+// steps so that other loads can go out while the copy's are in flight:
+// stage_load_wave issues the calling wavefront's loads (lane-strided
+// float4), stage_store_wave writes them to LDS.
 template <int N, int S>
-__device__ __forceinline__ void stage_copy_wave(float *const (&dst)[S], const float *const (&src)[S]) {
+struct StageRegs {
+  float4 v[S][N / 256];
+};
+template <int N, int S>
+__device__ __forceinline__ void stage_load_wave(StageRegs<N, S> &r, const float *const (&src)[S]) {
   static_assert(N % 256 == 0, "whole float4 sweeps");
-  constexpr int IT = N / 256;
   const int lane = int(threadIdx.x & 63);
-  float4 v[S][IT];
 #pragma unroll
   for (int s = 0; s < S; ++s)
 #pragma unroll
-    for (int it = 0; it < IT; ++it) v[s][it] = *reinterpret_cast<const float4 *>(src[s] + it * 256 + lane * 4);
+    for (int it = 0; it < N / 256; ++it) r.v[s][it] = *reinterpret_cast<const float4 *>(src[s] + it * 256 + lane * 4);
+}
+template <int N, int S>
+__device__ __forceinline__ void stage_store_wave(float *const (&dst)[S], const StageRegs<N, S> &r) {
+  const int lane = int(threadIdx.x & 63);
 #pragma unroll
   for (int s = 0; s < S; ++s)
 #pragma unroll
-    for (int it = 0; it < IT; ++it) *reinterpret_cast<float4 *>(dst[s] + it * 256 + lane * 4) = v[s][it];
+    for (int it = 0; it < N / 256; ++it) *reinterpret_cast<float4 *>(dst[s] + it * 256 + lane * 4) = r.v[s][it];
 }
 
 // Stage one vector of N f32 into LDS with the whole workgroup of NT threads
@@ -1121,23 +1130,27 @@ __device__ __forceinline__ void plan_publish(const RouteSpec &rs, PairTable *tab
   }
 }
 
-// Router and plan in one launch.  Every workgroup scores kRouteWaves experts
-// of one token; the last workgroup to finish (a device-scope counter in the
-// workspace, which that workgroup resets) gathers all scores, selects every
-// token's top-k (one wavefront per token) and publishes the pair table.
-// expert_pages == NULL: route only.  Saves a dependent kernel launch per
-// layer.
-constexpr int kRouteWaves = kMaxTokens;
-__global__ __launch_bounds__(64 * kRouteWaves) void k_route(RouteSpec rs, Workspace ws, const float *__restrict__ X) {
+// Router and plan in one launch.  Every workgroup (W = blockDim.x / 64
+// wavefronts, W = route_waves(T)) scores W experts of one token, one
+// wavefront each; the last workgroup to finish gathers all scores, selects
+// every token's top-k (wavefront w takes tokens w, w + W, ...) and publishes
+// the pair table.  Completion is counted in two levels so that no counter
+// takes more than kRouteGroup increments: workgroups in groups of
+// kRouteGroup (by linear index), then groups; each level's last arrival
+// resets its counter.  expert_pages == NULL: route only.  Saves a dependent
+// kernel launch per layer.
+constexpr uint32_t kRouteGroup = 16;
+__global__ __launch_bounds__(64 * kMaxTokens) void k_route(RouteSpec rs, Workspace ws, const float *__restrict__ X) {
   __shared__ float sc[kMaxTokens][kMaxExperts];
   __shared__ float bs[kMaxTokens][kMaxExperts];
   __shared__ uint64_t pages[kMaxExperts];
   __shared__ PlanLds pl;
   __shared__ uint32_t is_last;
   const uint32_t lane = threadIdx.x & 63;
+  const uint32_t W = blockDim.x >> 6;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t t = blockIdx.y;
-  const uint32_t e = blockIdx.x * kRouteWaves + wave;
+  const uint32_t e = blockIdx.x * W + wave;
   if (e < rs.r.n_experts) {
     const float2 s = router_score(rs.r, X, t, e);
     if (lane == 0) {
@@ -1150,14 +1163,15 @@ __global__ __launch_bounds__(64 * kRouteWaves) void k_route(RouteSpec rs, Worksp
   // release fence would write the whole L2 back: measured several us)
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  // two-level count (per token, then tokens) so that no counter takes more
-  // than gridDim.x increments; each level's last workgroup resets its counter
   if (threadIdx.x == 0) {
-    uint32_t *tok = ws.route_count + 1 + t;
-    bool last = __hip_atomic_fetch_add(tok, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    const uint32_t n = gridDim.x * gridDim.y, id = blockIdx.y * gridDim.x + blockIdx.x;
+    const uint32_t g = id / kRouteGroup, ng = (n + kRouteGroup - 1) / kRouteGroup;
+    const uint32_t gsize = min(kRouteGroup, n - g * kRouteGroup);
+    uint32_t *grp = ws.route_count + kRouteCounterStride * (1 + g);
+    bool last = __hip_atomic_fetch_add(grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gsize - 1;
     if (last) {
-      __hip_atomic_store(tok, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last = __hip_atomic_fetch_add(ws.route_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.y - 1;
+      __hip_atomic_store(grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = __hip_atomic_fetch_add(ws.route_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ng - 1;
       if (last) __hip_atomic_store(ws.route_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     is_last = last;
@@ -1166,31 +1180,40 @@ __global__ __launch_bounds__(64 * kRouteWaves) void k_route(RouteSpec rs, Worksp
   if (!is_last) return;  // uniform per workgroup
   // gather every (token, expert) score and the page table: all loads issued
   // before any is used
-  constexpr int kPer = kMaxTokens * kMaxExperts / (64 * kRouteWaves);
+  constexpr int kPer = kMaxTokens * kMaxExperts / 64;
   const uint32_t T = rs.tokens;
+  const uint32_t nthr = blockDim.x, need = T * kMaxExperts;
   const bool with_pages = rs.expert_pages != nullptr;
-  const uint64_t pg = (with_pages && threadIdx.x < rs.r.n_experts) ? rs.expert_pages[threadIdx.x] : 0ull;
   float gs[kPer], gb[kPer];
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
-    const uint32_t i = threadIdx.x + j * 64u * kRouteWaves;  // token i / 256, expert i % 256
-    const bool in = i / kMaxExperts < T;
+    const uint32_t i = threadIdx.x + uint32_t(j) * nthr;  // token i / 256, expert i % 256
+    const bool in = i < need;
     gs[j] = in ? __hip_atomic_load(&ws.scores[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
     gb[j] = in ? __hip_atomic_load(&ws.biased[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+    if (uint32_t(j + 1) * nthr >= need) break;
   }
+  for (uint32_t i = threadIdx.x; i < kMaxExperts; i += nthr)
+    pages[i] = (with_pages && i < rs.r.n_experts) ? rs.expert_pages[i] : 0ull;
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
-    const uint32_t i = threadIdx.x + j * 64u * kRouteWaves;
-    sc[i / kMaxExperts][i % kMaxExperts] = gs[j];
-    bs[i / kMaxExperts][i % kMaxExperts] = gb[j];
+    const uint32_t i = threadIdx.x + uint32_t(j) * nthr;
+    if (i < need) {
+      sc[i / kMaxExperts][i % kMaxExperts] = gs[j];
+      bs[i / kMaxExperts][i % kMaxExperts] = gb[j];
+    }
+    if (uint32_t(j + 1) * nthr >= need) break;
   }
-  if (threadIdx.x < kMaxExperts) pages[threadIdx.x] = pg;
   __syncthreads();
-  if (wave < T) plan_token(rs, wave, bs[wave], sc[wave], with_pages ? pages : nullptr, pl);
+  for (uint32_t tt = wave; tt < T; tt += W) plan_token(rs, tt, bs[tt], sc[tt], with_pages ? pages : nullptr, pl);
   if (!rs.expert_pages) return;  // route only (uniform)
   __syncthreads();
   if (wave == 0) plan_publish(rs, ws.table, pl);
 }
+
+// Wavefronts per route workgroup for T tokens: the last workgroup plans the
+// tokens W at a time, and fewer wavefronts spread the scoring over more CUs.
+inline uint32_t route_waves(uint32_t tokens) { return tokens <= 4 ? 4u : 8u; }
 
 // Pair p of phase 1: from the host plan (by value; workgroup (0,0) also
 // publishes it for phase 2) or from the table the plan kernel wrote.
@@ -1417,18 +1440,23 @@ __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairT
     mx_load<kPF>(ba, srcp, mx_woff, mx_soff, 0);  // first weights and the row's codes in flight during the h copy
     load_row_codes<kInter / 32>(rc, srcp, mx_soff);
   }
+  // h loads first, then the window words (whose reduction waits for them)
   CodeWindow win[2] = {{256, 0}, {256, 0}};
   if (has_b) {
     float *const dst[2] = {hs[sa], hs[sb]};
     const float *const srch[2] = {H + size_t(pa) * kInter, H + size_t(pb) * kInter};
+    StageRegs<kInter, 2> hr;
+    stage_load_wave<kInter, 2>(hr, srch);
     win[0] = h_window(hwin + size_t(pa) * kP1Tiles);
     win[1] = h_window(hwin + size_t(pb) * kP1Tiles);
-    stage_copy_wave<kInter, 2>(dst, srch);
+    stage_store_wave<kInter, 2>(dst, hr);
   } else if (has_a) {
     float *const dst[1] = {hs[sa]};
     const float *const srch[1] = {H + size_t(pa) * kInter};
+    StageRegs<kInter, 1> hr;
+    stage_load_wave<kInter, 1>(hr, srch);
     win[0] = win[1] = h_window(hwin + size_t(pa) * kP1Tiles);
-    stage_copy_wave<kInter, 1>(dst, srch);
+    stage_store_wave<kInter, 1>(dst, hr);
   }
   __syncthreads();
   if (has_a) {
@@ -1595,8 +1623,9 @@ hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const Router
 }
 
 hipError_t launch_route(hipStream_t s, const Workspace &ws, const RouteSpec &rs, const float *x, KernelEvents ev) {
-  hipExtLaunchKernelGGL(k_route, dim3((rs.r.n_experts + kRouteWaves - 1) / kRouteWaves, rs.tokens),
-                        dim3(64 * kRouteWaves), 0, s, ev.start, ev.stop, 0, rs, ws, x);
+  const uint32_t w = route_waves(rs.tokens);
+  hipExtLaunchKernelGGL(k_route, dim3((rs.r.n_experts + w - 1) / w, rs.tokens), dim3(64 * w), 0, s, ev.start,
+                        ev.stop, 0, rs, ws, x);
   return hipGetLastError();
 }
 

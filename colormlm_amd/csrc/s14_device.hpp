@@ -33,6 +33,10 @@ constexpr int kP1FastRows = kP1FastRowsPerWave * kFastWaves;
 constexpr int kP2FastRows = 16;
 
 constexpr int kSlots = kTopK + 1;  // pairs of one token: routed + shared
+// Route completion counters: groups, then <= 16 groups of 16 workgroups,
+// each on its own 128-byte line (atomics to one line serialize).
+constexpr uint32_t kRouteCounterStride = 32;
+constexpr uint32_t kRouteCounters = (1 + 16) * kRouteCounterStride;
 
 // Work of a layer or block launch.  Phase 1 runs one grid row per
 // (token, expert) pair: routed pairs first, sorted by expert id so that all
@@ -78,7 +82,7 @@ struct Workspace {
   float *h;       // [kMaxPairs][kInter]
   float *scores;  // [kMaxTokens][kMaxExperts]
   float *biased;  // [kMaxTokens][kMaxExperts]
-  uint32_t *route_count;  // [1 + kMaxTokens]: tokens, then per-token workgroups, of the running route launch that are done
+  uint32_t *route_count;  // [kRouteCounters]: groups, then per-group workgroups, of the running route launch that are done (one per 128-byte line)
   uint32_t *hwin;         // [kMaxPairs][kInter / kP1ExactRows]: exponent range (lo | hi << 16) of each exact phase-1 tile's h
   size_t bytes;
 };
