@@ -1180,7 +1180,8 @@ __global__ __launch_bounds__(64 * kMaxTokens) void k_route(RouteSpec rs, Workspa
   if (!is_last) return;  // uniform per workgroup
   // gather every (token, expert) score and the page table: all loads issued
   // before any is used
-  constexpr int kPer = kMaxTokens * kMaxExperts / 64;
+  // route_waves(T) >= T, so the T x 256 scores take at most kPer sweeps of the workgroup
+  constexpr int kPer = kMaxExperts / 64;
   const uint32_t T = rs.tokens;
   const uint32_t nthr = blockDim.x, need = T * kMaxExperts;
   const bool with_pages = rs.expert_pages != nullptr;
@@ -1214,6 +1215,7 @@ __global__ __launch_bounds__(64 * kMaxTokens) void k_route(RouteSpec rs, Workspa
 // Wavefronts per route workgroup for T tokens: the last workgroup plans the
 // tokens W at a time, and fewer wavefronts spread the scoring over more CUs.
 inline uint32_t route_waves(uint32_t tokens) { return tokens <= 4 ? 4u : 8u; }
+static_assert(kMaxTokens <= 8, "route_waves covers at most 8 tokens");
 
 // Pair p of phase 1: from the host plan (by value; workgroup (0,0) also
 // publishes it for phase 2) or from the table the plan kernel wrote.
