@@ -1304,7 +1304,7 @@ __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable p
   if (lane == 0) ws.hwin[size_t(p) * kP1Tiles + tile] = uint32_t(lo) | (uint32_t(hi) << 16);
 }
 
-// Phase 1 FAST: 4 wavefronts per workgroup; each streams kP1FastRowsPerWave
+// Phase 1 FAST: 4 wavefronts per workgroup; each streams p1_fast_rows_per_wave
 // row pairs (the same row of w1 and of w3) with kP1FastDepth row pairs of
 // codes in flight, x for the lane's k slices held in registers throughout.
 // The grid stays within one round of resident workgroups: a workgroup that
@@ -1313,11 +1313,11 @@ template <bool kHostPlan, int kTier>
 __global__ __launch_bounds__(256) void k_phase1_fast(PairTable plan, Workspace ws, const float *__restrict__ X,
                                                      PageOffsets mx, PageOffsets f8) {
   constexpr int NSEG = kHidden / 2048;
-  constexpr int R = kP1FastRowsPerWave;
+  constexpr int R = p1_fast_rows_per_wave(kTier);
   constexpr int D = kP1FastDepth;
   const uint32_t p = blockIdx.y;
   const PairRef pr = phase1_pair<kHostPlan>(plan, ws.table, p);
-  const uint32_t row0 = blockIdx.x * kP1FastRows + (threadIdx.x >> 6) * R;
+  const uint32_t row0 = blockIdx.x * p1_fast_rows(kTier) + (threadIdx.x >> 6) * R;
   const Rsrc r = make_rsrc(pr.page, page_bytes(pr.fmt));
   const int lane = threadIdx.x & 63;
   float gv = 0.0f, uv = 0.0f;  // lane i keeps row pair i
@@ -1638,7 +1638,7 @@ void phase1_tier(hipStream_t s, const Workspace &ws, const PairTable *host_plan,
   PairTable plan{};
   if (host_plan) plan = *host_plan;
   if (mode == S14_MODE_FAST) {
-    const dim3 grid(kInter / kP1FastRows, n_pairs);
+    const dim3 grid(kInter / p1_fast_rows(kTier), n_pairs);
     if (host_plan)
       hipExtLaunchKernelGGL(k_phase1_fast<true, kTier>, grid, dim3(256), 0, s, ev.start, ev.stop, 0, plan, ws, x, mx,
                             fp8);

@@ -24,12 +24,14 @@ constexpr int kP1ExactRows = 16;
 constexpr int kP1ExactWaves = 4;  // phase-1 row tiles per workgroup, sharing one staged x
 constexpr int kP2ExactRows = 16;
 constexpr int kP2ExactWaves = 4;
-// Fast-mode tiles: phase 1 = 4 wavefronts x 8 rows of w1 and w3 (streamed); phase 2 =
-// 16 rows of w2 per wavefront (one wavefront per pair of the token).
-constexpr int kP1FastRowsPerWave = 8;
-constexpr int kP1FastDepth = 3;  // row pairs of codes in flight per wavefront
+// Fast-mode tiles: phase 1 = 4 wavefronts x R rows of w1 and w3 (streamed, two row
+// pairs of codes in flight per wavefront; R = 8 for single-token launches, 16 for blocks,
+// the measured best of 4 / 8 / 16 rows at depths 1-6); phase 2 = 16 rows of w2 per
+// wavefront (one wavefront per pair of the token).
+constexpr int p1_fast_rows_per_wave(int tier) { return tier == 1 ? 8 : 16; }
+constexpr int kP1FastDepth = 2;  // row pairs of codes in flight per wavefront
 constexpr int kFastWaves = 4;
-constexpr int kP1FastRows = kP1FastRowsPerWave * kFastWaves;
+constexpr int p1_fast_rows(int tier) { return p1_fast_rows_per_wave(tier) * kFastWaves; }
 constexpr int kP2FastRows = 16;
 
 constexpr int kSlots = kTopK + 1;  // pairs of one token: routed + shared
