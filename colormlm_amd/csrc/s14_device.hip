@@ -1306,7 +1306,8 @@ __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable p
 
 // Phase 1 FAST: 4 wavefronts per workgroup; each streams p1_fast_rows_per_wave
 // row pairs (the same row of w1 and of w3) with kP1FastDepth row pairs of
-// codes in flight, x for the lane's k slices held in registers throughout.
+// codes in flight, x for the lane's k slices held in registers throughout
+// (read from one LDS copy per workgroup).
 // The grid stays within one round of resident workgroups: a workgroup that
 // starts only when another finishes costs a whole extra load latency.
 template <bool kHostPlan, int kTier>
@@ -1321,8 +1322,8 @@ __global__ __launch_bounds__(256) void k_phase1_fast(PairTable plan, Workspace w
   const Rsrc r = make_rsrc(pr.page, page_bytes(pr.fmt));
   const int lane = threadIdx.x & 63;
   float gv = 0.0f, uv = 0.0f;  // lane i keeps row pair i
+  __shared__ float xs[kHidden];
   XReg<NSEG> xr;
-  load_x_mx<NSEG>(xr, X + size_t(pr.token) * kHidden, kHidden);
   if (pr.fmt == S14_PAGE_MXFP4) {
     MxRowFrag f1[D][NSEG], f3[D][NSEG];
     auto load = [&](int slot, uint32_t row) {
@@ -1333,6 +1334,19 @@ __global__ __launch_bounds__(256) void k_phase1_fast(PairTable plan, Workspace w
     };
 #pragma unroll
     for (int i = 0; i < D && i < R; ++i) load(i, row0 + i);
+    {
+      // x once per workgroup through LDS (each wavefront loading all 16 KiB of
+      // it from L2 cost 29 MB of L2 reads per K=1 launch), while the first
+      // row pairs are in flight
+      const float *src = X + size_t(pr.token) * kHidden;
+      float4 v[kHidden / 1024];
+#pragma unroll
+      for (int it = 0; it < kHidden / 1024; ++it) v[it] = *reinterpret_cast<const float4 *>(src + (it * 256 + threadIdx.x) * 4);
+#pragma unroll
+      for (int it = 0; it < kHidden / 1024; ++it) *reinterpret_cast<float4 *>(xs + (it * 256 + threadIdx.x) * 4) = v[it];
+      __syncthreads();
+      load_x_mx<NSEG>(xr, xs, kHidden);
+    }
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const int slot = i % D;
@@ -1345,6 +1359,7 @@ __global__ __launch_bounds__(256) void k_phase1_fast(PairTable plan, Workspace w
       }
     }
   } else {
+    load_x_mx<NSEG>(xr, X + size_t(pr.token) * kHidden, kHidden);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const uint32_t row = row0 + i;
