@@ -414,6 +414,59 @@ def test_moe_block_route_config3(ctx, oracle, bank, tokens):
         assert np.max(np.abs(fast[t] - got[t])) <= 1e-3
 
 
+def test_moe_block_fp8_shared_and_edge_codes(ctx, oracle, bank):
+    """Block launches (T=4) with the reference's FP8 shared page, so every
+    phase-2 wavefront that serves a routed slot beside the shared one mixes
+    MXFP4 and FP8 halves; exact mode against the oracle token by token."""
+    tokens = 4
+    say(f"config 3 block T={tokens} with FP8 shared page, exact")
+    sh = synth.gen_fp8_page(0, 0)
+    xs = synth.block_tokens(seed=7, tokens=tokens)
+    router = s14.Router(bank["wr_d"], bank["bias_d"])
+    y = torch.empty((tokens, HIDDEN), dtype=torch.float32, device="cuda")
+    ids = torch.empty((tokens, 6), dtype=torch.int16, device="cuda")
+    s14.moe_block_route(ctx, tokens, router, bank["table"], dev(sh), dev(xs), y, ids,
+                        shared_format=N.S14_PAGE_FP8, mode=s14.EXACT)
+    got, ids_h = host(y), host(ids).astype(np.uint16)
+    for t in range(tokens):
+        _, i_o, w_o = oracle.route(bank["wr"], bank["bias"], xs[t])
+        assert ids_h[t].tolist() == i_o.tolist()
+        want = oracle.moe_layer(xs[t], [page_host(bank, int(e)) for e in i_o], w_o, sh, shared_fmt="fp8")
+        assert_bit_exact(got[t], want, f"block fp8-shared token {t}")
+
+
+def test_moe_block_edge_scale_codes(ctx, oracle, bank):
+    """Block launches (T=3) whose routed pages carry scale codes outside the
+    scaled-decode window in w1, w3 and w2 rows (copies of the chosen pages,
+    substituted in the page table), against the oracle on the same pages."""
+    tokens = 3
+    say(f"config 3 block T={tokens} with out-of-window scale codes, exact")
+    xs = synth.block_tokens(seed=9, tokens=tokens)
+    routes = [oracle.route(bank["wr"], bank["bias"], xs[t]) for t in range(tokens)]
+    chosen = sorted({int(e) for _, i_o, _ in routes for e in i_o})
+    o = synth.page_offsets("mxfp4")
+    g_up, g_dn = HIDDEN // 32, INTER // 32
+    edited, keep = {}, []
+    table = bank["table"].clone()
+    for n, e in enumerate(chosen[:4]):
+        pg = page_host(bank, e).copy()
+        pg[o["s1"] + (3 + 40 * n) * g_up + 5] = 1
+        pg[o["s3"] + (700 + n) * g_up: o["s3"] + (700 + n) * g_up + 3] = [0, 2, 4]
+        pg[o["s2"] + (33 * n + 1) * g_dn + 60] = 3
+        d = dev(pg)
+        keep.append(d)
+        table[e] = d.data_ptr()
+        edited[e] = pg
+    router = s14.Router(bank["wr_d"], bank["bias_d"])
+    y = torch.empty((tokens, HIDDEN), dtype=torch.float32, device="cuda")
+    s14.moe_block_route(ctx, tokens, router, table, bank["pages"][256], dev(xs), y, mode=s14.EXACT)
+    got = host(y)
+    shared = page_host(bank, 256)
+    for t, (_, i_o, w_o) in enumerate(routes):
+        pages = [edited[int(e)] if int(e) in edited else page_host(bank, int(e)) for e in i_o]
+        assert_bit_exact(got[t], oracle.moe_layer(xs[t], pages, w_o, shared), f"block edge codes token {t}")
+
+
 def test_pool_upload_publish_compute_release(ctx, oracle, bank):
     """The page contract end to end on the device: reserve, upload on the copy
     stream, wait the transfer fence, publish, compute from slot addresses,
