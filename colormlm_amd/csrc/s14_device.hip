@@ -1070,7 +1070,7 @@ __device__ __forceinline__ void plan_token(const RouteSpec &rs, uint32_t t, cons
                                            const uint64_t *pages, PlanLds &pl) {
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t k = rs.r.topk;
-  const TopK c = select_topk(biased, scores, pages, rs.r.n_experts, k);
+  const TopK c = select_topk_lds(biased, scores, pages, rs.r.n_experts, k);
   if (lane < k) {
     const float wgt = route_weight(c, rs.r.route_scale);
     pl.ids[t][lane] = c.id;
