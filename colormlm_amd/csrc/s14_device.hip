@@ -1641,6 +1641,9 @@ hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const Router
 
 hipError_t launch_route(hipStream_t s, const Workspace &ws, const RouteSpec &rs, const float *x, KernelEvents ev) {
   const uint32_t w = route_waves(rs.tokens);
+  const uint32_t blocks = (rs.r.n_experts + w - 1) / w * rs.tokens;
+  // the workspace holds counters for at most kRouteCounters / kRouteCounterStride - 1 groups
+  if ((blocks + kRouteGroup - 1) / kRouteGroup > kRouteCounters / kRouteCounterStride - 1) return hipErrorInvalidValue;
   hipExtLaunchKernelGGL(k_route, dim3((rs.r.n_experts + w - 1) / w, rs.tokens), dim3(64 * w), 0, s, ev.start,
                         ev.stop, 0, rs, ws, x);
   return hipGetLastError();
