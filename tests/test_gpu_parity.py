@@ -433,6 +433,12 @@ def test_moe_block_fp8_shared_and_edge_codes(ctx, oracle, bank):
         assert ids_h[t].tolist() == i_o.tolist()
         want = oracle.moe_layer(xs[t], [page_host(bank, int(e)) for e in i_o], w_o, sh, shared_fmt="fp8")
         assert_bit_exact(got[t], want, f"block fp8-shared token {t}")
+    # FAST mode's block kernels on the same inputs (FP8 rows in both phases), against the exact result
+    s14.moe_block_route(ctx, tokens, router, bank["table"], dev(sh), dev(xs), y, shared_format=N.S14_PAGE_FP8,
+                        mode=s14.FAST)
+    fast = host(y)
+    for t in range(tokens):
+        assert np.max(np.abs(fast[t] - got[t])) <= 1e-3
 
 
 def test_moe_block_edge_scale_codes(ctx, oracle, bank):
