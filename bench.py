@@ -4,14 +4,18 @@
 Metric: MoE layer us/token and achieved HBM GB/s (% of the
 8 TB/s peak) at K=1 and K=8.  A step is one pass of the hot path over one
 batch: K=1 is one token through router + top-6 routed + shared MXFP4 experts
-(config 2); K=8 is one speculative-verify block of 8 tokens (config 3).
+(config 2, the headline); K=8 is one speculative-verify block of 8 tokens
+(config 3).  Beside them: config 0 (one expert chain), config 1 (the FP8
+wq_a matvec) and config 4 (the 512-token prefill).
 
-The timed path is the EXACT (oracle-order, bit-identical) kernel set unless
---mode fast.  Inputs are resident in HBM before timing: `--layers` layer
-banks of 257 expert pages each live in one device arena (a VramPool), and
-consecutive steps rotate banks and tokens so the working set between reuses
-(> 1 GB) exceeds the 256 MB MALL.  Stage durations come from hipEvents the
-library records between its kernels (Context.enable_stage_timing).
+Every leg times the EXACT (oracle-order, bit-identical) kernels and the FAST
+(order-changed) ones.  Each leg's figure is the median of --trials trials;
+a trial times exactly --steps steps (after --warmup untimed ones) between
+two device synchronisations with events on the launch stream.  Inputs are
+resident in HBM before timing: `--layers` layer banks of 257 expert pages
+live in one device arena (a VramPool), and consecutive steps rotate banks,
+pages and tokens so that the working set between reuses (> 1 GB) exceeds the
+256 MB MALL; config 1 rotates 96 copies of its 4 MiB weight.
 
 Prints one JSON line.
 """
@@ -21,6 +25,8 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -37,6 +43,10 @@ DOWN = 4_194_304 + 262_144  # w2 + s2
 ROUTER = 256 * 4096 * 4 + 256 * 4
 X_BYTES = 4096 * 4
 H_BYTES = 2048 * 4
+CHAIN_BYTES = PAGE + 2 * X_BYTES  # config 0: page, x in, y out
+WQA_N, WQA_K = 1024, 4096
+WQA_BYTES = WQA_N * WQA_K + 8 * 32 * 4 + WQA_K * 2 + WQA_N * 4  # config 1: W, f32 tile scales, bf16 x, f32 y
+WQA_COPIES = 96
 
 
 def layer_bytes_k1() -> int:
@@ -71,22 +81,57 @@ def phase1_bytes(pairs: int, tokens: int) -> int:
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=400)
-    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--steps", type=int, default=200, help="timed steps per trial")
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--trials", type=int, default=5, help="trials per leg; each leg reports the median")
     ap.add_argument("--mode", choices=["exact", "fast"], default="exact")
     ap.add_argument("--layers", type=int, default=12, help="layer banks of 257 pages rotated across steps")
     ap.add_argument("--tokens", type=int, default=64, help="distinct tokens rotated across steps")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--profile-steps", type=int, default=64)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline's work per config")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy 10 times (the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     ap.add_argument("--prefill-steps", type=int, default=20)
-    ap.add_argument("--only", choices=["k1", "k8", "prefill", "all"], default="all",
+    ap.add_argument("--only", choices=["k1", "k8", "config0", "config1", "prefill", "all"], default="all",
                     help="restrict the timed work (for profiler runs)")
     return ap.parse_args()
+
+
+def progress(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Timer:
+    """Median-of-trials timing of a step function on torch's current stream
+    (the stream the library launches on)."""
+
+    def __init__(self, torch, trials: int):
+        self.torch = torch
+        self.trials = max(1, trials)
+
+    def run(self, fn, steps: int, warmup: int) -> dict:
+        torch = self.torch
+        steps = max(1, steps)
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        per = []
+        k = warmup
+        for _ in range(self.trials):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record()
+            for i in range(steps):
+                fn(k + i)
+            end.record()
+            torch.cuda.synchronize()
+            k += steps
+            per.append(start.elapsed_time(end) / steps)
+        return {"ms": statistics.median(per), "ms_min": min(per), "ms_max": max(per), "trials": len(per),
+                "steps_per_trial": steps}
 
 
 def main() -> int:
@@ -108,10 +153,12 @@ def main() -> int:
     if args.copy_calibration:
         return copy_calibration(torch)
     ctx = s14.Context(0)
-    mode = s14.EXACT if args.mode == "exact" else s14.FAST
     NL, P = args.layers, args.tokens
+    timer = Timer(torch, args.trials)
+    only = args.only
 
     # ---- resident inputs ----
+    progress(f"filling {NL} x 257 expert pages")
     bank = VramPool(NL * 257, N.EXPERT_PAGE_BYTES, ctx)
     for L in range(NL):
         for e in range(257):
@@ -119,6 +166,7 @@ def main() -> int:
     tables = torch.tensor([[bank.slot_ptr(L * 257 + e) for e in range(256)] for L in range(NL)],
                           dtype=torch.int64, device="cuda")
     shared = [bank.slot_ptr(L * 257 + 256) for L in range(NL)]
+    pages_flat = [bank.slot_ptr(i) for i in range(NL * 257)]
     routers_h = [synth.router(args.seed, L) for L in range(NL)]
     wr = torch.stack([torch.from_numpy(w) for w, _ in routers_h]).cuda()
     bias = torch.stack([torch.from_numpy(b) for _, b in routers_h]).cuda()
@@ -127,84 +175,99 @@ def main() -> int:
     XB = torch.from_numpy(np.stack([synth.block_tokens(args.seed + 1000 + i, 8) for i in range(P)])).cuda()
     Y = torch.empty(4096, dtype=torch.float32, device="cuda")
     YB = torch.empty((8, 4096), dtype=torch.float32, device="cuda")
+    IDS = torch.empty((8, 6), dtype=torch.int16, device="cuda")
     torch.cuda.synchronize()
 
-    def step_k1(i, m=mode):
-        L = i % NL
-        s14.moe_layer_route(ctx, routers[L], tables[L], shared[L], X[i % P], Y, mode=m)
+    def step_k1(m):
+        def f(i):
+            L = i % NL
+            s14.moe_layer_route(ctx, routers[L], tables[L], shared[L], X[i % P], Y, mode=m)
+        return f
 
-    def step_k8(i, m=mode):
-        L = i % NL
-        s14.moe_block_route(ctx, 8, routers[L], tables[L], shared[L], XB[i % P], YB, mode=m)
+    def step_k8(m):
+        def f(i):
+            L = i % NL
+            s14.moe_block_route(ctx, 8, routers[L], tables[L], shared[L], XB[i % P], YB, mode=m)
+        return f
 
-    def timed(fn, steps, warmup, m):
-        for i in range(warmup):
-            fn(i, m)
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for i in range(steps):
-            fn(i, m)
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / steps  # ms per step
+    def step_chain(m):
+        def f(i):
+            # a different page (and layer bank) every step: > 1 GB between reuses
+            page = pages_flat[(i * 37) % len(pages_flat)]
+            s14.expert_chain(ctx, page, X[i % P], 0.17, Y, mode=m)
+        return f
 
-    def stages(fn, steps, m):
+    def stages(fn, steps):
         ctx.enable_stage_timing(True)
         acc = np.zeros(3)
         for i in range(steps):
-            fn(i, m)
+            fn(i)
             acc += np.array(ctx.stage_times())
         ctx.enable_stage_timing(False)
         return (acc / steps).tolist()
 
-    def distinct_pages(m):
-        ds = []
+    def block_routes(m):
+        """Distinct routed pages and the adjacent-token top-6 overlap of the
+        bench's blocks, from the routes the device itself chose."""
+        ds, ov = [], []
         for i in range(min(P, 32)):
-            step_k8(i, m)
+            L = i % NL
+            s14.moe_block_route(ctx, 8, routers[L], tables[L], shared[L], XB[i % P], YB, ids_out=IDS, mode=m)
             ds.append(s14.last_block_distinct(ctx))
-        return float(np.mean(ds))
+            ids = [set(int(v) for v in row) for row in IDS.cpu().numpy().astype(np.int64) & 0xffff]
+            ov += [len(ids[t] & ids[t - 1]) / 6.0 for t in range(1, 8)]
+        return float(np.mean(ds)), float(np.mean(ov))
 
     out = {}
     for name, m in (("exact", s14.EXACT), ("fast", s14.FAST)):
         r = {}
-        if args.only in ("k1", "all"):
-            ms1 = timed(step_k1, args.steps, args.warmup, m)
-            st1 = stages(step_k1, args.profile_steps, m)
-            r["k1"] = {
-                "us_per_token": ms1 * 1e3,
-                "hbm_gbps": layer_bytes_k1() / (ms1 * 1e-3) / 1e9,
-                "stage_ms": {"route": st1[0], "phase1": st1[1], "phase2": st1[2]},
-            }
+        if only in ("k1", "all"):
+            progress(f"config 2 (K=1) {name}")
+            t = timer.run(step_k1(m), args.steps, args.warmup)
+            st = stages(step_k1(m), args.profile_steps)
+            us = t["ms"] * 1e3
+            r["k1"] = {"us_per_token": us, "timing": t, "hbm_gbps": layer_bytes_k1() / (us * 1e-6) / 1e9,
+                       "stage_ms": {"route": st[0], "phase1": st[1], "phase2": st[2]}}
             r["k1"]["hbm_frac"] = r["k1"]["hbm_gbps"] / HBM_PEAK_GBPS
-        if args.only in ("k8", "all"):
-            ms8 = timed(step_k8, max(args.steps // 4, 10), max(args.warmup // 4, 5), m)
-            st8 = stages(step_k8, max(args.profile_steps // 4, 8), m)
-            d = distinct_pages(m)
-            r["k8"] = {
-                "us_per_token": ms8 * 1e3 / 8,
-                "ms_per_block": ms8,
-                "distinct_pages": d,
-                "hbm_gbps": block_bytes(round(d), 8) / (ms8 * 1e-3) / 1e9,
-                "stage_ms": {"route": st8[0], "phase1": st8[1], "phase2": st8[2]},
-            }
+        if only in ("k8", "all"):
+            progress(f"config 3 (K=8) {name}")
+            t = timer.run(step_k8(m), max(args.steps // 4, 10), max(args.warmup // 4, 5))
+            st = stages(step_k8(m), max(args.profile_steps // 4, 8))
+            d, ov = block_routes(m)
+            ms = t["ms"]
+            r["k8"] = {"us_per_token": ms * 1e3 / 8, "ms_per_block": ms, "timing": t, "distinct_pages": d,
+                       "adjacent_overlap": ov, "hbm_gbps": block_bytes(round(d), 8) / (ms * 1e-3) / 1e9,
+                       "stage_ms": {"route": st[0], "phase1": st[1], "phase2": st[2]}}
             r["k8"]["hbm_frac"] = r["k8"]["hbm_gbps"] / HBM_PEAK_GBPS
+        if only in ("config0", "all"):
+            progress(f"config 0 (chain) {name}")
+            t = timer.run(step_chain(m), args.steps, args.warmup)
+            st = stages(step_chain(m), args.profile_steps)
+            us = t["ms"] * 1e3
+            r["config0"] = {"us_per_chain": us, "timing": t, "hbm_gbps": CHAIN_BYTES / (us * 1e-6) / 1e9,
+                            "stage_ms": {"phase1": st[1], "phase2": st[2]}, "algorithmic_bytes": CHAIN_BYTES}
+            r["config0"]["hbm_frac"] = r["config0"]["hbm_gbps"] / HBM_PEAK_GBPS
         out[name] = r
 
+    if only in ("config1", "all"):
+        progress("config 1 (wq_a fp8)")
+        c1 = bench_config1(args, ctx, timer, torch, np, s14, synth)
+        for name in ("exact", "fast"):
+            out[name]["config1"] = c1[name]
+
     prefill = None
-    if args.only in ("prefill", "all"):
+    if only in ("prefill", "all"):
+        progress("config 4 (prefill)")
         prefill = bench_prefill(args, ctx, tables, shared, NL, torch, np, s14, synth)
-    if args.only == "prefill":
-        print(json.dumps({"prefill": prefill}), flush=True)
+    if only != "all" and only not in ("k1",):
+        print(json.dumps({"only": only, "legs": out, "prefill": prefill}), flush=True)
         return 0
 
     main_r = out[args.mode]
-    key = "k1" if "k1" in main_r else "k8"
-    headline = main_r[key]
+    headline = main_r["k1"]
     # dominant kernel of the timed path: phase 1 (w1, w3 of all pairs)
-    pairs, tokens = (7, 1) if key == "k1" else (56, 8)
     p1_ms = headline["stage_ms"]["phase1"]
-    p1_bytes = phase1_bytes(pairs, tokens)
+    p1_bytes = phase1_bytes(7, 1)
     achieved = p1_bytes / (p1_ms * 1e-3) / 1e9
     roofline = {
         "bound": "hbm",
@@ -220,7 +283,8 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(args, bank, routers_h, X, ctx)
+        progress("CPU baseline")
+        cpu = cpu_baseline(args, bank, routers_h, X, ctx, np, torch, synth)
 
     line = {
         "metric": METRIC,
@@ -229,7 +293,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": headline["us_per_token"] * 1e-3 * (1 if key == "k1" else 8),
+        "ms_per_step": headline["us_per_token"] * 1e-3,
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -237,9 +301,11 @@ def main() -> int:
         "data": "synthetic (seeded; MXFP4 codes uniform, UE8M0 exponents in [-10,-4], x ~ N(0,1))",
         "config": {
             "workload": "config2: router + top-6 routed + shared MXFP4 MoE layer, batch 1 (hidden 4096, "
-                        "inter 2048, 256 experts); K=8 verify block reported beside it",
+                        "inter 2048, 256 experts); K=8 verify block, config 0 chain, config 1 wq_a and "
+                        "config 4 prefill reported beside it",
             "mode": args.mode,
             "parity": "bit-identical to the CPU oracle" if args.mode == "exact" else "order-changed f32",
+            "timing": f"median of {args.trials} trials of {args.steps} steps",
             "layer_banks": NL,
             "tokens_rotated": P,
             "layer_bytes_k1": layer_bytes_k1(),
@@ -248,6 +314,8 @@ def main() -> int:
         "hbm_frac": headline["hbm_frac"],
         "k1": main_r.get("k1"),
         "k8": main_r.get("k8"),
+        "config0": main_r.get("config0"),
+        "config1": main_r.get("config1"),
         "other_mode": {k: v for k, v in out.items() if k != args.mode},
         "prefill": prefill,
         "roofline": roofline,
@@ -256,6 +324,33 @@ def main() -> int:
     print(json.dumps(line), flush=True)
     ctx.synchronize()
     return 0
+
+
+def bench_config1(args, ctx, timer, torch, np, s14, synth):
+    """Config 1: the FP8 wq_a matvec (W e4m3 [1024, 4096], f32 128x128 tile
+    scales, bf16 x), rotated over WQA_COPIES copies of W (403 MB, past the
+    MALL)."""
+    cfg = synth.config1(seed=args.seed)
+    w1 = torch.from_numpy(cfg["w"].reshape(-1)).cuda()
+    W = w1.unsqueeze(0).repeat(WQA_COPIES, 1)
+    S = torch.from_numpy(cfg["scale"].reshape(-1)).cuda()
+    xb = torch.from_numpy(cfg["x_bf16"]).cuda().view(torch.bfloat16)
+    y = torch.empty(WQA_N, dtype=torch.float32, device="cuda")
+    pipes = s14.S14NumericPipelines(ctx)
+    shape = s14.S14MatvecShape.new(WQA_N, WQA_K).validate_fp8()
+    res = {}
+    for name, m in (("exact", s14.EXACT), ("fast", s14.FAST)):
+        ds = [pipes.bind_fp8(shape, xb, W[c], S, y, mode=m) for c in range(WQA_COPIES)]
+
+        def f(i, ds=ds):
+            pipes.cmd_fp8_matvec(ds[(i * 7) % WQA_COPIES])
+
+        t = timer.run(f, args.steps, args.warmup)
+        us = t["ms"] * 1e3
+        res[name] = {"us_per_matvec": us, "timing": t, "algorithmic_bytes": WQA_BYTES,
+                     "hbm_gbps": WQA_BYTES / (us * 1e-6) / 1e9, "hbm_frac": WQA_BYTES / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+                     "note": "back-to-back launches from Python: includes the launch gap"}
+    return res
 
 
 def bench_prefill(args, ctx, tables, shared, NL, torch, np, s14, synth):
@@ -284,15 +379,8 @@ def bench_prefill(args, ctx, tables, shared, NL, torch, np, s14, synth):
     for L in range(NL):
         step(L)
         stats.append(s14.last_prefill_stats(ctx))
-    steps = max(args.prefill_steps, 1)
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        step(i)
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    t = Timer(torch, args.trials).run(step, max(args.prefill_steps, 1), 2)
+    ms = t["ms"]
     d = float(np.mean([s["distinct"] for s in stats]))
     nbytes = prefill_bytes(round(d), T)
     flops = prefill_flops(T)
@@ -300,6 +388,7 @@ def bench_prefill(args, ctx, tables, shared, NL, torch, np, s14, synth):
         "tokens": T,
         "ms_per_prefill": ms,
         "us_per_token": ms * 1e3 / T,
+        "timing": t,
         "distinct_experts": d,
         "max_tokens_per_expert": max(s["max_tokens_per_expert"] for s in stats),
         "algorithmic_bytes": nbytes,
@@ -307,7 +396,6 @@ def bench_prefill(args, ctx, tables, shared, NL, torch, np, s14, synth):
         "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
         "tflops": flops / (ms * 1e-3) / 1e12,
         "mfma_frac_fp8": flops / (ms * 1e-3) / 1e12 / FP8_MFMA_PEAK_TFLOPS,
-        "steps": steps,
     }
 
 
@@ -341,50 +429,81 @@ def measured_traffic(kernel: str):
     return None
 
 
-def cpu_baseline(args, bank, routers_h, X, ctx):
-    """The CPU oracle (router + layer) on the host cores, on a bounded sample
-    of config-2 tokens."""
-    import numpy as np
-    import torch
+def cpu_model() -> str:
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
 
+
+def _median_runs(fn, seconds: float, min_runs: int = 5, max_runs: int = 15):
+    """Wall times of fn() after one warm-up run: at least min_runs, more while
+    under `seconds` of total work."""
+    fn()
+    times = []
+    spent = 0.0
+    while len(times) < max_runs and (len(times) < min_runs or spent < seconds):
+        t0 = time.perf_counter()
+        fn()
+        dt = time.perf_counter() - t0
+        times.append(dt)
+        spent += dt
+        if len(times) >= min_runs and spent >= seconds:
+            break
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(args, bank, routers_h, X, ctx, np, torch, synth):
+    """The CPU oracle (the C restatement of the reference's CPU F32 path) on
+    the host cores: config 2 (route + layer), config 0 (chain) and config 1
+    (wq_a), each on all host cores and on one core, median of >= 5 runs
+    after a warm-up run, each config's work bounded by --cpu-seconds."""
     import oracle
 
-    NL = args.layers
     xs = X.cpu().numpy()
-    samples = []
-    for i in range(64):
-        L = i % NL
-        wr, b = routers_h[L]
-        _, ids, w = oracle.route(wr, b, xs[i % len(xs)])
-        samples.append((L, i % len(xs), [int(e) for e in ids], w))
-    pages = {}
+    wr, b = routers_h[0]
+    _, ids, w = oracle.route(wr, b, xs[0])
+    torch.cuda.synchronize()
+    routed = [bank.slot_tensor(int(e))[:PAGE].cpu().numpy() for e in ids]
+    sh = bank.slot_tensor(256)[:PAGE].cpu().numpy()
+    c1 = synth.config1(seed=args.seed)
 
-    def page(L, e):
-        if (L, e) not in pages:
-            torch.cuda.synchronize()
-            pages[(L, e)] = bank.slot_tensor(L * 257 + e)[:PAGE].cpu().numpy()
-        return pages[(L, e)]
+    def layer():
+        oracle.route(wr, b, xs[0])
+        oracle.moe_layer(xs[0], routed, w, sh)
 
-    n_done, t_total = 0, 0.0
-    for L, xi, ids, w in samples:
-        routed = [page(L, e) for e in ids]
-        sh = page(L, 256)
-        wr, b = routers_h[L]
-        t0 = time.perf_counter()
-        oracle.route(wr, b, xs[xi])
-        oracle.moe_layer(xs[xi], routed, w, sh)
-        t_total += time.perf_counter() - t0
-        n_done += 1
-        if t_total >= args.cpu_seconds:
-            break
-        if len(pages) > 120:
-            pages.clear()
+    def chain():
+        oracle.expert_chain(xs[0], routed[0], 0.17)
+
+    def wqa():
+        oracle.fp8_matvec_f32scale_bf16x(c1["x_bf16"], c1["w"], c1["scale"])
+
+    all_cores = oracle.num_threads()
+    res = {}
+    for label, n in (("all_cores", all_cores), ("one_core", 1)):
+        oracle.set_num_threads(n)
+        share = args.cpu_seconds / 2
+        t_layer, n_layer = _median_runs(layer, share * 0.7)
+        t_chain, n_chain = _median_runs(chain, share * 0.2)
+        t_wqa, n_wqa = _median_runs(wqa, share * 0.1)
+        res[label] = {"cores": n, "config2_us_per_token": t_layer * 1e6, "config2_runs": n_layer,
+                      "config0_us_per_chain": t_chain * 1e6, "config0_runs": n_chain,
+                      "config1_us_per_matvec": t_wqa * 1e6, "config1_runs": n_wqa}
+    oracle.set_num_threads(all_cores)
     return {
-        "value": t_total / n_done * 1e6,
+        "value": res["all_cores"]["config2_us_per_token"],
         "unit": "us/token",
-        "cores": oracle.num_threads(),
+        "cores": all_cores,
         "kind": "port",
-        "sample": f"{n_done} config-2 tokens (router + 6 routed + shared, f32 oracle order), OpenMP rows",
+        "cpu_model": cpu_model(),
+        "host_cpus": os.cpu_count(),
+        "sample": "config 2: one token (router + 6 routed + shared MXFP4 pages, f32 oracle order, OpenMP over "
+                  "rows), median of >= 5 runs after a warm-up; configs 0 and 1 likewise",
+        "all_cores": res["all_cores"],
+        "one_core": res["one_core"],
     }
 
 

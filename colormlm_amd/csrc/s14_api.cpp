@@ -84,6 +84,17 @@ int check_ctx(s14_ctx *ctx) {
   return S14_OK;
 }
 
+// The standalone matvec kernels address weights and scales through 32-bit
+// buffer descriptors and 32-bit row offsets (row * row_bytes < weight
+// bytes): shapes whose weight or scale bytes reach 2^32 are rejected here
+// rather than wrapping on the device.
+int check_u32_extent(uint64_t weight_bytes, uint64_t scale_bytes, const char *label) {
+  if (weight_bytes > UINT32_MAX || scale_bytes > UINT32_MAX)
+    return fail(S14_ERR_SHAPE, "%s needs %llu weight / %llu scale bytes; at most %u each are addressable", label,
+                (unsigned long long)weight_bytes, (unsigned long long)scale_bytes, UINT32_MAX);
+  return S14_OK;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -175,15 +186,16 @@ extern "C" int s14_ctx_synchronize(s14_ctx *ctx) {
 }
 
 namespace s14 {
-int pool_alloc_arena(s14_ctx *ctx, uint64_t bytes, uint8_t **out) {
+int pool_alloc_arena(s14_ctx *ctx, uint64_t bytes, uint8_t **out, int *device) {
   S14_HIP(hipSetDevice(ctx->device), "hipSetDevice");
   void *p = nullptr;
   S14_HIP(hipMalloc(&p, bytes), "hipMalloc(pool arena)");
   *out = static_cast<uint8_t *>(p);
+  *device = ctx->device;
   return S14_OK;
 }
-void pool_free_arena(s14_ctx *ctx, uint8_t *base) {
-  if (ctx) (void)hipSetDevice(ctx->device);
+void pool_free_arena(int device, uint8_t *base) {
+  if (device >= 0) (void)hipSetDevice(device);
   (void)hipFree(base);
 }
 }  // namespace s14
@@ -198,6 +210,7 @@ extern "C" int s14_bind_mxfp4(s14_shape shape, s14_buffer x, s14_buffer w, s14_b
   s14_shape_bytes b;
   if (int rc = s14_shape_validate_mxfp4(shape, &b)) return rc;
   if (mode != S14_MODE_EXACT && mode != S14_MODE_FAST) return fail(S14_ERR_INVALID, "unknown mode %d", mode);
+  if (int rc = check_u32_extent(b.weight_bytes, b.scale_bytes, "S14 MXFP4 matvec")) return rc;
   if (int rc = require_capacity(x, b.input_bytes, "S14 MXFP4 input")) return rc;
   if (int rc = require_capacity(w, storage_bytes(b.weight_bytes), "S14 MXFP4 weight")) return rc;
   if (int rc = require_capacity(sc, storage_bytes(b.scale_bytes), "S14 MXFP4 scale")) return rc;
@@ -221,6 +234,7 @@ extern "C" int s14_bind_fp8(s14_shape shape, s14_buffer x, int x_dtype, s14_buff
     return fail(S14_ERR_INVALID, "unknown scale dtype %d", scale_dtype);
   const uint64_t x_bytes = x_dtype == S14_X_BF16 ? uint64_t(shape.k) * 2 : b.input_bytes;
   const uint64_t s_bytes = scale_dtype == S14_SCALE_F32 ? b.scale_bytes * 4 : storage_bytes(b.scale_bytes);
+  if (int rc = check_u32_extent(b.weight_bytes, s_bytes, "S14 FP8 matvec")) return rc;
   if (int rc = require_capacity(x, x_bytes, "S14 FP8 input")) return rc;
   if (int rc = require_capacity(w, storage_bytes(b.weight_bytes), "S14 FP8 weight")) return rc;
   if (int rc = require_capacity(sc, s_bytes, "S14 FP8 scale")) return rc;

@@ -38,7 +38,7 @@ inline bool key_eq(const s14_expert_key &a, const s14_expert_key &b) { return Ke
 enum class SlotState : uint8_t { Empty, Loading, Ready };
 
 struct s14_pool {
-  s14_ctx *ctx = nullptr;   // NULL for a host-only bookkeeping pool
+  int device = -1;          // device of the arena; -1 for a host-only bookkeeping pool
   uint8_t *base = nullptr;  // device arena (one allocation), NULL if host-only
   uint64_t slot_bytes = 0;
   uint32_t n_slots = 0;
@@ -53,7 +53,9 @@ struct s14_pool {
 };
 
 namespace s14 {
-// Device workspace allocation owned by a context (implemented in s14_api.cpp).
-int pool_alloc_arena(s14_ctx *ctx, uint64_t bytes, uint8_t **out);
-void pool_free_arena(s14_ctx *ctx, uint8_t *base);
+// The pool's device arena, allocated on ctx's device (implemented in
+// s14_api.cpp).  The pool keeps the device id, not the context: it may
+// outlive the context that created it.
+int pool_alloc_arena(s14_ctx *ctx, uint64_t bytes, uint8_t **out, int *device);
+void pool_free_arena(int device, uint8_t *base);
 }  // namespace s14

@@ -155,7 +155,7 @@ extern "C" int s14_pool_create(s14_ctx *ctx, uint32_t n_slots, uint64_t slot_byt
   if (slot_bytes > std::numeric_limits<uint64_t>::max() / n_slots)
     return fail(S14_ERR_INVALID, "VRAM pool size overflow");
   std::unique_ptr<s14_pool> p(new s14_pool());
-  p->ctx = ctx;
+  p->device = -1;
   p->slot_bytes = slot_bytes;
   p->n_slots = n_slots;
   p->states.assign(n_slots, SlotState::Empty);
@@ -165,7 +165,7 @@ extern "C" int s14_pool_create(s14_ctx *ctx, uint32_t n_slots, uint64_t slot_byt
   p->generations.assign(n_slots, 0);
   p->index.reserve(n_slots);
   if (ctx) {
-    int rc = s14::pool_alloc_arena(ctx, uint64_t(n_slots) * slot_bytes, &p->base);
+    int rc = s14::pool_alloc_arena(ctx, uint64_t(n_slots) * slot_bytes, &p->base, &p->device);
     if (rc != S14_OK) return rc;
   }
   *out = p.release();
@@ -174,7 +174,7 @@ extern "C" int s14_pool_create(s14_ctx *ctx, uint32_t n_slots, uint64_t slot_byt
 
 extern "C" void s14_pool_destroy(s14_pool *pool) {
   if (!pool) return;
-  if (pool->base) s14::pool_free_arena(pool->ctx, pool->base);
+  if (pool->base) s14::pool_free_arena(pool->device, pool->base);
   delete pool;
 }
 

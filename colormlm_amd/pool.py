@@ -78,6 +78,8 @@ class VramPool:
 
     def __init__(self, n_slots: int, slot_bytes: int, ctx=None):
         self._h = C.c_void_p()
+        # the pool's fences and uploads go through ctx: keep it alive as long as the pool
+        self._ctx = ctx
         check(lib().s14_pool_create(ctx.handle if ctx is not None else None, n_slots, slot_bytes, C.byref(self._h)))
 
     @classmethod

@@ -50,17 +50,24 @@ def buffer(t, nbytes: Optional[int] = None) -> N.Buffer:
     return N.Buffer(_ptr(t), _nbytes(t) if nbytes is None else nbytes)
 
 
+_TORCH_CUDA = []  # [torch] once torch with a visible GPU is found, [None] if not
+
+
 def _stream(stream):
+    """The stream to launch on: the caller's, else torch's current stream
+    (so that torch events and work order against the library's), else the
+    null stream."""
     if stream is not None:
         return stream
-    try:
-        import torch
+    if not _TORCH_CUDA:
+        try:
+            import torch
 
-        if torch.cuda.is_available():
-            return torch.cuda.current_stream().cuda_stream
-    except Exception:  # pragma: no cover - torch is optional for the ABI
-        pass
-    return None
+            _TORCH_CUDA.append(torch if torch.cuda.is_available() else None)
+        except Exception:  # pragma: no cover - torch is optional for the ABI
+            _TORCH_CUDA.append(None)
+    torch = _TORCH_CUDA[0]
+    return torch.cuda.current_stream().cuda_stream if torch is not None else None
 
 
 class Context:

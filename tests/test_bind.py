@@ -79,3 +79,23 @@ def test_cmd_requires_context(native):
     assert N.lib().s14_cmd_mxfp4_matvec(None, None, C.byref(rec)) == N.S14_ERR_INVALID
     with pytest.raises(S14Error):
         N.check(N.lib().s14_expert_chain(None, None, None, None, 0.17, None, 0))
+
+
+def test_bind_rejects_shapes_past_32bit_addressing(native):
+    """The standalone matvecs address weights through 32-bit buffer
+    descriptors: a shape whose weight (or scale) bytes reach 2^32 is a shape
+    error at bind time, not a silent wrap on the device."""
+    A = 0x40000
+    big = 1 << 40
+    # MXFP4: N * K / 2 = 2^32 bytes exactly -> rejected; one row fewer -> accepted
+    n, k = 1 << 20, 1 << 13
+    assert bind_mx(n, k, buf(A, 4 * k), buf(A, big), buf(A, big), buf(A, 4 * n))[0] == N.S14_ERR_SHAPE
+    assert "addressable" in N.last_error()
+    assert bind_mx(n - 1, k, buf(A, 4 * k), buf(A, big), buf(A, big), buf(A, 4 * n))[0] == 0
+    # FP8: N * K = 2^32 bytes -> rejected; f32 tile scales count 4 bytes each
+    rec = N.Fp8Dispatch()
+    L = N.lib()
+    assert L.s14_bind_fp8(N.Shape(1 << 16, 1 << 16), buf(A, 1 << 18), N.S14_X_F32, buf(A, big), buf(A, big),
+                          N.S14_SCALE_UE8M0, buf(A, 1 << 18), N.S14_MODE_EXACT, C.byref(rec)) == N.S14_ERR_SHAPE
+    assert L.s14_bind_fp8(N.Shape((1 << 16) - 128, 1 << 16), buf(A, 1 << 18), N.S14_X_F32, buf(A, big),
+                          buf(A, big), N.S14_SCALE_F32, buf(A, 1 << 18), N.S14_MODE_EXACT, C.byref(rec)) == 0
