@@ -9,7 +9,7 @@ into colormlm_amd/lib/libs14hip.so:
   multiply-then-add must stay unfused) and with packed FP32 instructions
   disabled (-Xclang -target-feature -Xclang -packed-fp32-ops).  Clang has no
   driver spelling that forwards an -Xclang pair to the device pass alone, so
-  the host pass of these two files prints a one-line notice that it does not
+  the host pass of these files prints a one-line notice that it does not
   know the feature; the device code objects are what the flag is for;
 - the host-only translation units (*.cpp: the C ABI, the pool and loader
   contracts) without that flag.
@@ -29,7 +29,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "lib" / "libs14hip.so"
 OBJ = PKG / "lib" / "obj"
-DEVICE_SOURCES = ["s14_device.hip", "s14_prefill.hip"]
+DEVICE_SOURCES = ["s14_device.hip", "s14_prefill.hip", "s14_static.hip"]
 HOST_SOURCES = ["s14_api.cpp", "s14_pool.cpp"]
 SOURCES = DEVICE_SOURCES + HOST_SOURCES
 ARCH = os.environ.get("S14_OFFLOAD_ARCH", "gfx950")

@@ -117,33 +117,14 @@ extern "C" int s14_ctx_create(int device, s14_ctx **out) {
     s14_ctx_destroy(ctx);
     return hip_fail(e, "hipStreamCreate");
   }
-  // workspace: table | h | scores | biased | route counter | h windows
-  size_t off = 0;
-  const size_t o_table = off;
-  off = align_up(off + sizeof(s14::PairTable), 256);
-  const size_t o_h = off;
-  off = align_up(off + sizeof(float) * s14::kMaxPairs * s14::kInter, 256);
-  const size_t o_scores = off;
-  off = align_up(off + sizeof(float) * s14::kMaxTokens * s14::kMaxExperts, 256);
-  const size_t o_biased = off;
-  off = align_up(off + sizeof(float) * s14::kMaxTokens * s14::kMaxExperts, 256);
-  const size_t o_count = off;
-  off = align_up(off + sizeof(uint32_t) * s14::kRouteCounters, 256);
-  const size_t o_hwin = off;
-  off = align_up(off + sizeof(uint32_t) * s14::kMaxPairs * (s14::kInter / s14::kP1ExactRows), 256);
+  // workspace: table | h | scores | biased | route counters | h windows
+  const size_t off = s14::kWorkspaceBytes;
   e = hipMalloc(&ctx->ws_base, off);
   if (e != hipSuccess) {
     s14_ctx_destroy(ctx);
     return hip_fail(e, "hipMalloc(workspace)");
   }
-  uint8_t *b = static_cast<uint8_t *>(ctx->ws_base);
-  ctx->ws.table = reinterpret_cast<s14::PairTable *>(b + o_table);
-  ctx->ws.h = reinterpret_cast<float *>(b + o_h);
-  ctx->ws.scores = reinterpret_cast<float *>(b + o_scores);
-  ctx->ws.biased = reinterpret_cast<float *>(b + o_biased);
-  ctx->ws.route_count = reinterpret_cast<uint32_t *>(b + o_count);  // zeroed below; each route launch leaves it 0
-  ctx->ws.hwin = reinterpret_cast<uint32_t *>(b + o_hwin);
-  ctx->ws.bytes = off;
+  ctx->ws = s14::workspace_carve(ctx->ws_base);  // route counters zeroed below; each route launch leaves them 0
   // one clear at creation, outside any launch sequence
   e = hipMemset(ctx->ws_base, 0, off);
   if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -453,27 +434,57 @@ extern "C" int s14_moe_layer(s14_ctx *ctx, void *stream, uint32_t topk, const ui
   return run_layer(ctx, st, &t, n, 1, x, y, mode);
 }
 
+namespace s14 {
+
+int block_route_validate(uint32_t tokens, const s14_router *router, const uint64_t *expert_pages_dev,
+                         const uint8_t *shared_page, int shared_format, const float *x, float *y, int mode) {
+  if (int rc = check_mode(mode)) return rc;
+  if (int rc = check_router(router)) return rc;
+  if (router->topk != uint32_t(kTopK)) return fail(S14_ERR_SHAPE, "routed layer requires topk=%d", kTopK);
+  if (tokens == 0 || tokens > uint32_t(kMaxTokens))
+    return fail(S14_ERR_SHAPE, "block size %u outside 1..%d", tokens, kMaxTokens);
+  if (!expert_pages_dev || !shared_page || !x || !y) return fail(S14_ERR_INVALID, "NULL layer buffer");
+  if (shared_format != S14_PAGE_MXFP4 && shared_format != S14_PAGE_FP8)
+    return fail(S14_ERR_INVALID, "unknown shared page format %d", shared_format);
+  return S14_OK;
+}
+
+int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, const s14_router *router,
+                       const uint64_t *expert_pages_dev, const uint8_t *shared_page, int shared_format,
+                       const float *x, float *y, uint16_t *ids_out, float *weights_out, int mode,
+                       const KernelEvents *ev) {
+  s14_page_layout l;
+  s14_page_layout_get(S14_PAGE_MXFP4, S14_HIDDEN, S14_INTER, &l);
+  const PageOffsets mx = offsets_of(l);
+  s14_page_layout_get(S14_PAGE_FP8, S14_HIDDEN, S14_INTER, &l);
+  const PageOffsets f8 = offsets_of(l);
+  const RouteSpec rs{router_args(router), tokens, shared_format, expert_pages_dev, shared_page, ids_out, weights_out};
+  hipError_t e = launch_route(st, ws, rs, x, ev ? ev[kStageRoute] : KernelEvents{});
+  if (e != hipSuccess) return hip_fail(e, "router launch");
+  e = launch_phase1(st, ws, nullptr, tokens * (kTopK + 1), tokens, mx, f8, x, mode,
+                    ev ? ev[kStagePhase1] : KernelEvents{});
+  if (e != hipSuccess) return hip_fail(e, "phase 1 launch");
+  e = launch_phase2(st, ws, tokens, mx, f8, y, mode, ev ? ev[kStagePhase2] : KernelEvents{});
+  if (e != hipSuccess) return hip_fail(e, "phase 2 launch");
+  return S14_OK;
+}
+
+}  // namespace s14
+
 extern "C" int s14_moe_block_route(s14_ctx *ctx, void *stream, uint32_t tokens, const s14_router *router,
                                    const uint64_t *expert_pages_dev, const uint8_t *shared_page,
                                    int shared_format, const float *x, float *y, uint16_t *ids_out,
                                    float *weights_out, int mode) {
   if (int rc = check_ctx(ctx)) return rc;
-  if (int rc = check_mode(mode)) return rc;
-  if (int rc = check_router(router)) return rc;
-  if (router->topk != uint32_t(s14::kTopK))
-    return fail(S14_ERR_SHAPE, "routed layer requires topk=%d", s14::kTopK);
-  if (tokens == 0 || tokens > uint32_t(s14::kMaxTokens))
-    return fail(S14_ERR_SHAPE, "block size %u outside 1..%d", tokens, s14::kMaxTokens);
-  if (!expert_pages_dev || !shared_page || !x || !y) return fail(S14_ERR_INVALID, "NULL layer buffer");
-  if (shared_format != S14_PAGE_MXFP4 && shared_format != S14_PAGE_FP8)
-    return fail(S14_ERR_INVALID, "unknown shared page format %d", shared_format);
-  hipStream_t st = pick(ctx, stream);
-  const s14::RouteSpec rs{router_args(router), tokens, shared_format, expert_pages_dev, shared_page, ids_out,
-                          weights_out};
+  if (int rc = s14::block_route_validate(tokens, router, expert_pages_dev, shared_page, shared_format, x, y, mode))
+    return rc;
   stage_begin(ctx);
-  hipError_t e = s14::launch_route(st, ctx->ws, rs, x, stage_events(ctx, kStageRoute));
-  if (e != hipSuccess) return hip_fail(e, "router launch");
-  return run_layer(ctx, st, nullptr, tokens * (s14::kTopK + 1), tokens, x, y, mode);
+  s14::KernelEvents ev[kStages];
+  for (int i = 0; i < kStages; ++i) ev[i] = stage_events(ctx, i);
+  const int rc = s14::block_route_launch(pick(ctx, stream), ctx->ws, tokens, router, expert_pages_dev, shared_page,
+                                         shared_format, x, y, ids_out, weights_out, mode, ev);
+  if (rc == S14_OK) ctx->stage_valid = ctx->stage_timing;
+  return rc;
 }
 
 extern "C" int s14_moe_layer_route(s14_ctx *ctx, void *stream, const s14_router *router,

@@ -1632,6 +1632,17 @@ hipError_t launch_fill_mxfp4_page(hipStream_t s, uint8_t *page, uint64_t seed, u
   return hipGetLastError();
 }
 
+namespace {
+__global__ void k_clear_u32(uint32_t *p, uint32_t n) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+}  // namespace
+
+hipError_t launch_clear_route_counters(hipStream_t s, const Workspace &ws) {
+  k_clear_u32<<<1, 256, 0, s>>>(ws.route_count, kRouteCounters);
+  return hipGetLastError();
+}
+
 hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const RouterArgs &r, uint32_t tokens,
                                 const float *x, KernelEvents ev) {
   hipExtLaunchKernelGGL(k_router_scores, dim3((r.n_experts + 4 * kRtE - 1) / (4 * kRtE), (tokens + kRtT - 1) / kRtT),

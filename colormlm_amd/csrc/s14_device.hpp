@@ -89,6 +89,48 @@ struct Workspace {
   size_t bytes;
 };
 
+// Layout of the workspace in one device allocation (each region 256-byte
+// aligned): table | h | scores | biased | route counters | h windows.
+struct WorkspaceLayout {
+  size_t table, h, scores, biased, count, hwin, bytes;
+};
+constexpr size_t ws_align(size_t v) { return (v + 255) / 256 * 256; }
+constexpr WorkspaceLayout workspace_layout() {
+  WorkspaceLayout l{};
+  size_t off = 0;
+  l.table = off;
+  off = ws_align(off + sizeof(PairTable));
+  l.h = off;
+  off = ws_align(off + sizeof(float) * kMaxPairs * kInter);
+  l.scores = off;
+  off = ws_align(off + sizeof(float) * kMaxTokens * kMaxExperts);
+  l.biased = off;
+  off = ws_align(off + sizeof(float) * kMaxTokens * kMaxExperts);
+  l.count = off;
+  off = ws_align(off + sizeof(uint32_t) * kRouteCounters);
+  l.hwin = off;
+  off = ws_align(off + sizeof(uint32_t) * kMaxPairs * (kInter / kP1ExactRows));
+  l.bytes = off;
+  return l;
+}
+constexpr size_t kWorkspaceBytes = workspace_layout().bytes;
+
+// The workspace views of the allocation at `base` (kWorkspaceBytes bytes,
+// 256-byte aligned).
+inline Workspace workspace_carve(void *base) {
+  constexpr WorkspaceLayout l = workspace_layout();
+  uint8_t *b = static_cast<uint8_t *>(base);
+  Workspace ws{};
+  ws.table = reinterpret_cast<PairTable *>(b + l.table);
+  ws.h = reinterpret_cast<float *>(b + l.h);
+  ws.scores = reinterpret_cast<float *>(b + l.scores);
+  ws.biased = reinterpret_cast<float *>(b + l.biased);
+  ws.route_count = reinterpret_cast<uint32_t *>(b + l.count);
+  ws.hwin = reinterpret_cast<uint32_t *>(b + l.hwin);
+  ws.bytes = l.bytes;
+  return ws;
+}
+
 struct PageOffsets {
   uint64_t w1, s1, w3, s3, w2, s2;
 };
@@ -133,6 +175,10 @@ hipError_t launch_dequant_fp8(hipStream_t s, s14_shape shape, const uint8_t *w, 
 hipError_t launch_fill_mxfp4_page(hipStream_t s, uint8_t *page, uint64_t seed, uint32_t layer,
                                   uint32_t expert, uint32_t hidden, uint32_t inter, int lo, int hi,
                                   const PageOffsets &off);
+
+// Zeroes the route completion counters of a workspace (they start at 0 and
+// every route launch leaves them at 0).
+hipError_t launch_clear_route_counters(hipStream_t s, const Workspace &ws);
 
 // --- fused layer / block path: route (router + plan) -> phase 1 -> phase 2 ---
 // Scores and biased scores of every (token, expert) into ws.scores/biased

@@ -8,9 +8,20 @@
 #include <unordered_map>
 #include <vector>
 
+#include "s14_device.hpp"
 #include "s14_hip.h"
 
 namespace s14 {
+
+// Argument checks of the routed layer/block entry points (s14_api.cpp).
+int block_route_validate(uint32_t tokens, const s14_router *router, const uint64_t *expert_pages_dev,
+                         const uint8_t *shared_page, int shared_format, const float *x, float *y, int mode);
+// Route -> phase 1 -> phase 2 of a routed layer/block on `st` with workspace
+// `ws` (arguments already validated); ev: per-stage timing events or NULL.
+int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, const s14_router *router,
+                       const uint64_t *expert_pages_dev, const uint8_t *shared_page, int shared_format,
+                       const float *x, float *y, uint16_t *ids_out, float *weights_out, int mode,
+                       const KernelEvents *ev);
 
 // Records `msg` as this thread's last error and returns `code`.
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));

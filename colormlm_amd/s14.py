@@ -391,6 +391,39 @@ def moe_block_route(
     )
 
 
+def moe_block_route_noalloc(
+    tokens: int,
+    router: Router,
+    expert_pages,
+    shared_page,
+    x,
+    y,
+    ids_out=None,
+    weights_out=None,
+    shared_format: int = N.S14_PAGE_MXFP4,
+    mode: int = EXACT,
+    stream=None,
+) -> None:
+    """moe_block_route without a context: the workspace is the library's
+    static per-GPU scratch array (no device allocation in the call)."""
+    r = router.c()
+    check(
+        lib().s14_moe_block_route_noalloc(
+            _stream(stream),
+            tokens,
+            C.byref(r),
+            _ptr(expert_pages),
+            _ptr(shared_page),
+            shared_format,
+            _ptr(x),
+            _ptr(y),
+            _ptr(ids_out),
+            _ptr(weights_out),
+            mode,
+        )
+    )
+
+
 def last_block_distinct(ctx: Context) -> int:
     n = C.c_uint32()
     check(lib().s14_last_block_distinct(ctx.handle, C.byref(n)))

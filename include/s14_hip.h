@@ -255,6 +255,24 @@ int s14_moe_block_route(s14_ctx *ctx, void *stream, uint32_t tokens, const s14_r
  * (synchronises the device). */
 int s14_last_block_distinct(s14_ctx *ctx, uint32_t *n_distinct);
 
+/* No counterpart in the reference: the routed layer/block of
+ * s14_moe_block_route (same arguments without a context, same kernels,
+ * bit-identical results) for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It calls no hipMalloc/hipFree: its workspace is a static
+ * device array of s14_noalloc_scratch_bytes() bytes (about 0.5 MB) per GPU,
+ * held until the process ends, whose device address the first call on each
+ * GPU looks up (hipGetSymbolAddress) with that GPU current.  The limit is
+ * the block size: tokens > S14_MAX_BLOCK_TOKENS is S14_ERR_SHAPE.  Launches
+ * go to `stream` on the current device.  Every call on a GPU shares that
+ * GPU's array, so calls that overlap on one GPU (other streams or threads)
+ * race on it. */
+int s14_moe_block_route_noalloc(void *stream, uint32_t tokens, const s14_router *router,
+                                const uint64_t *expert_pages_dev, const uint8_t *shared_page,
+                                int shared_format, const float *x, float *y, uint16_t *ids_out,
+                                float *weights_out, int mode);
+uint64_t s14_noalloc_scratch_bytes(void);
+
 /* Router only (scores f32 [n_experts], ids u16 [topk], weights f32 [topk]). */
 int s14_route(s14_ctx *ctx, void *stream, const s14_router *router, uint32_t tokens,
               const float *x, float *scores_out, uint16_t *ids_out, float *weights_out);

@@ -1,0 +1,78 @@
+"""The no-allocation entry point (s14_moe_block_route_noalloc) against the
+context entry point it varies (s14_moe_block_route): same inputs, outputs,
+routes and weights bit for bit, on two calls in a row, the second with a
+smaller block, in both modes."""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+from colormlm_amd import _native as N  # noqa: E402
+from colormlm_amd import s14, synth  # noqa: E402
+
+HIDDEN = N.HIDDEN
+
+
+def say(msg: str) -> None:
+    print(f"[gpu-test] {msg}", file=sys.stderr, flush=True)
+
+
+def bits(t) -> np.ndarray:
+    torch.cuda.synchronize()
+    return np.ascontiguousarray(t.cpu().numpy()).view(np.uint8)
+
+
+@pytest.fixture(scope="module")
+def setup():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    say("no-alloc: context and 257-page bank")
+    ctx = s14.Context(0)
+    pages = torch.empty((257, N.EXPERT_PAGE_BYTES), dtype=torch.uint8, device="cuda")
+    for e in range(256):
+        s14.fill_mxfp4_page(ctx, pages[e], 5, 1, e)
+    s14.fill_mxfp4_page(ctx, pages[256], 5, 1, synth.SHARED_EXPERT)
+    table = torch.tensor([pages[e].data_ptr() for e in range(256)], dtype=torch.int64, device="cuda")
+    wr, bias = synth.router(seed=5, layer=1)
+    router = s14.Router(torch.from_numpy(wr).cuda(), torch.from_numpy(bias).cuda())
+    torch.cuda.synchronize()
+    yield ctx, pages, table, router
+    torch.cuda.synchronize()
+    ctx.destroy()
+
+
+@pytest.mark.parametrize("mode", [s14.EXACT, s14.FAST])
+def test_noalloc_matches_context_entry(setup, mode):
+    ctx, pages, table, router = setup
+    assert N.lib().s14_noalloc_scratch_bytes() > 0
+    for call, tokens in enumerate((8, 3)):  # the second call smaller than the first
+        say(f"no-alloc call {call}: T={tokens} mode={mode}")
+        x = torch.from_numpy(synth.block_tokens(seed=40 + call, tokens=tokens)).cuda()
+        y_ref = torch.full((tokens, HIDDEN), np.nan, dtype=torch.float32, device="cuda")
+        y_new = torch.full((tokens, HIDDEN), np.nan, dtype=torch.float32, device="cuda")
+        ids_ref = torch.zeros((tokens, 6), dtype=torch.int16, device="cuda")
+        ids_new = torch.zeros((tokens, 6), dtype=torch.int16, device="cuda")
+        w_ref = torch.zeros((tokens, 6), dtype=torch.float32, device="cuda")
+        w_new = torch.zeros((tokens, 6), dtype=torch.float32, device="cuda")
+        s14.moe_block_route(ctx, tokens, router, table, pages[256], x, y_ref, ids_ref, w_ref, mode=mode)
+        s14.moe_block_route_noalloc(tokens, router, table, pages[256], x, y_new, ids_new, w_new, mode=mode)
+        assert np.array_equal(bits(ids_new), bits(ids_ref))
+        assert np.array_equal(bits(w_new), bits(w_ref))
+        assert np.array_equal(bits(y_new), bits(y_ref)), f"call {call}: outputs differ"
+        assert not np.isnan(y_new.cpu().numpy()).any()
+
+
+def test_noalloc_rejects_oversized_block(setup):
+    ctx, pages, table, router = setup
+    x = torch.zeros((9, HIDDEN), dtype=torch.float32, device="cuda")
+    y = torch.zeros((9, HIDDEN), dtype=torch.float32, device="cuda")
+    with pytest.raises(s14.S14Error) as err:
+        s14.moe_block_route_noalloc(9, router, table, pages[256], x, y)
+    assert err.value.code == N.S14_ERR_SHAPE
