@@ -266,19 +266,19 @@ def main() -> int:
     main_r = out[args.mode]
     headline = main_r["k1"]
     # dominant kernel of the timed path: phase 1 (w1, w3 of all pairs)
-    p1_ms = headline["stage_ms"]["phase1"]
-    p1_bytes = phase1_bytes(7, 1)
-    achieved = p1_bytes / (p1_ms * 1e-3) / 1e9
+    st = headline["stage_ms"]
+    kernel, k_ms, k_bytes = f"k_phase1_{args.mode}", st["phase1"], phase1_bytes(7, 1)
+    achieved = k_bytes / (k_ms * 1e-3) / 1e9
     roofline = {
         "bound": "hbm",
-        "kernel": f"k_phase1_{args.mode}",
+        "kernel": kernel,
         "achieved": achieved,
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
         "frac": achieved / HBM_PEAK_GBPS,
-        "traffic": measured_traffic(f"k_phase1_{args.mode}"),
-        "algorithmic_bytes": p1_bytes,
-        "avg_ms": p1_ms,
+        "traffic": measured_traffic(kernel),
+        "algorithmic_bytes": k_bytes,
+        "avg_ms": k_ms,
     }
 
     cpu = None

@@ -228,6 +228,7 @@ SIGNATURES = {
     "s14_moe_layer_route": (I, [P, P, C.POINTER(Router), P, P, I, P, P, P, P, I]),
     "s14_moe_block_route": (I, [P, P, U32, C.POINTER(Router), P, P, I, P, P, P, P, I]),
     "s14_last_block_distinct": (I, [P, C.POINTER(U32)]),
+    "s14_launch_status": (I, [P]),
     "s14_moe_block_route_noalloc": (I, [P, U32, C.POINTER(Router), P, P, I, P, P, P, P, I]),
     "s14_noalloc_scratch_bytes": (C.c_uint64, []),
     "s14_route": (I, [P, P, C.POINTER(Router), U32, P, P, P, P]),

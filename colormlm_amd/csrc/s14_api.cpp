@@ -458,7 +458,8 @@ int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, con
   const PageOffsets mx = offsets_of(l);
   s14_page_layout_get(S14_PAGE_FP8, S14_HIDDEN, S14_INTER, &l);
   const PageOffsets f8 = offsets_of(l);
-  const RouteSpec rs{router_args(router), tokens, shared_format, expert_pages_dev, shared_page, ids_out, weights_out};
+  const RouteSpec rs{router_args(router), tokens,      shared_format,  expert_pages_dev, shared_page,
+                     ids_out,              weights_out, status_word(ws)};
   hipError_t e = launch_route(st, ws, rs, x, ev ? ev[kStageRoute] : KernelEvents{});
   if (e != hipSuccess) return hip_fail(e, "router launch");
   e = launch_phase1(st, ws, nullptr, tokens * (kTopK + 1), tokens, mx, f8, x, mode,
@@ -480,10 +481,15 @@ extern "C" int s14_moe_block_route(s14_ctx *ctx, void *stream, uint32_t tokens, 
     return rc;
   stage_begin(ctx);
   s14::KernelEvents ev[kStages];
-  for (int i = 0; i < kStages; ++i) ev[i] = stage_events(ctx, i);
+  if (ctx->stage_timing)
+    for (int i = 0; i < kStages; ++i) ev[i] = {ctx->stage_ev[2 * i], ctx->stage_ev[2 * i + 1]};
   const int rc = s14::block_route_launch(pick(ctx, stream), ctx->ws, tokens, router, expert_pages_dev, shared_page,
-                                         shared_format, x, y, ids_out, weights_out, mode, ev);
-  if (rc == S14_OK) ctx->stage_valid = ctx->stage_timing;
+                                         shared_format, x, y, ids_out, weights_out, mode,
+                                         ctx->stage_timing ? ev : nullptr);
+  if (rc == S14_OK && ctx->stage_timing) {
+    ctx->stage_mask = (1u << kStageRoute) | (1u << kStagePhase1) | (1u << kStagePhase2);
+    ctx->stage_valid = true;
+  }
   return rc;
 }
 
@@ -506,6 +512,27 @@ extern "C" int s14_last_block_distinct(s14_ctx *ctx, uint32_t *n_distinct) {
   return S14_OK;
 }
 
+namespace s14 {
+int read_launch_status(const Workspace &ws, int device) {
+  S14_HIP(hipSetDevice(device), "hipSetDevice");
+  S14_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  uint32_t *word = ws.sync + kSyncStatusLine * kRouteCounterStride;
+  uint32_t bits = 0;
+  S14_HIP(hipMemcpy(&bits, word, sizeof(bits), hipMemcpyDeviceToHost), "hipMemcpy(status)");
+  if (!bits) return S14_OK;
+  const uint32_t zero = 0;
+  S14_HIP(hipMemcpy(word, &zero, sizeof(zero), hipMemcpyHostToDevice), "hipMemcpy(status clear)");
+  if (bits & kStatusNullPage)
+    return fail(S14_ERR_INVALID, "a routed expert's page address was 0 (page not resident); outputs are NaN");
+  return fail(S14_ERR_HIP, "an in-kernel wait timed out (status 0x%x); outputs are NaN", bits);
+}
+}  // namespace s14
+
+extern "C" int s14_launch_status(s14_ctx *ctx) {
+  if (int rc = check_ctx(ctx)) return rc;
+  return s14::read_launch_status(ctx->ws, ctx->device);
+}
+
 extern "C" int s14_route(s14_ctx *ctx, void *stream, const s14_router *router, uint32_t tokens,
                          const float *x, float *scores_out, uint16_t *ids_out, float *weights_out) {
   if (int rc = check_ctx(ctx)) return rc;
@@ -514,7 +541,8 @@ extern "C" int s14_route(s14_ctx *ctx, void *stream, const s14_router *router, u
     return fail(S14_ERR_SHAPE, "token count %u outside 1..%d", tokens, s14::kMaxTokens);
   if (!x) return fail(S14_ERR_INVALID, "NULL router input");
   hipStream_t st = pick(ctx, stream);
-  const s14::RouteSpec rs{router_args(router), tokens, S14_PAGE_MXFP4, nullptr, nullptr, ids_out, weights_out};
+  const s14::RouteSpec rs{router_args(router), tokens,      S14_PAGE_MXFP4,              nullptr, nullptr,
+                          ids_out,              weights_out, s14::status_word(ctx->ws)};
   hipError_t e = s14::launch_route(st, ctx->ws, rs, x);
   if (e != hipSuccess) return hip_fail(e, "router launch");
   if (scores_out) {
@@ -606,7 +634,7 @@ extern "C" int s14_moe_prefill(s14_ctx *ctx, void *stream, uint32_t tokens, cons
   if (int rc = prefill_workspace(ctx)) return rc;
   hipStream_t st = pick(ctx, stream);
   const s14::PrefillArgs a{router_args(router), tokens, expert_pages_dev, shared_page, ctx->mx, x, y,
-                           ids_out, weights_out};
+                           ids_out, weights_out, s14::status_word(ctx->ws)};
   const hipError_t e = s14::launch_prefill(st, a, ctx->pws);
   if (e != hipSuccess) return hip_fail(e, "prefill launch");
   ctx->prefill_tokens = tokens;

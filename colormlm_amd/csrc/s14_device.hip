@@ -24,515 +24,10 @@
 
 #include "s14_device.hpp"
 #include "s14_device_util.hpp"
+#include "s14_exact.hpp"
 
 namespace s14 {
 namespace {
-
-// Biased-exponent range of the nonzero finite values seen by this lane.
-__device__ __forceinline__ void exp_range_acc(float v, int &lo, int &hi) {
-  const uint32_t u = __float_as_uint(v);
-  const int e = int((u >> 23) & 255u);
-  if ((u & 0x7fffffffu) != 0u && e != 255) {
-    lo = min(lo, e);
-    hi = max(hi, e);
-  }
-}
-
-// Scale codes for which x * (e2m1 * 2^(c-127)) rounds exactly like the
-// oracle's (x * e2m1) * 2^(c-127): both products stay normal and the scaled
-// decode is exact.  With every nonzero finite x in [2^(emin-127),
-// 2^(emax-126)): requires emin >= 2 (x*0.5 normal), emax <= 251 (x*6
-// finite); then c in [max(2, 129 - emin), 252].  (Infinite or NaN x give
-// the same inf/NaN either way.)  Batches holding other codes take the
-// literal two-multiply path.
-struct CodeWindow {
-  int cmin, cmax;
-};
-__device__ __forceinline__ CodeWindow mx_window(int emin, int emax) {
-  if (emin < 2 || emax > 251) return {256, 0};
-  return {max(2, 129 - emin), 252};
-}
-
-// The copy alone, for vectors whose window is known (phase 2's h), in two
-// steps so that other loads can go out while the copy's are in flight:
-// stage_load_wave issues the calling wavefront's loads (lane-strided
-// float4), stage_store_wave writes them to LDS.
-template <int N, int S>
-struct StageRegs {
-  float4 v[S][N / 256];
-};
-template <int N, int S>
-__device__ __forceinline__ void stage_load_wave(StageRegs<N, S> &r, const float *const (&src)[S]) {
-  static_assert(N % 256 == 0, "whole float4 sweeps");
-  const int lane = int(threadIdx.x & 63);
-#pragma unroll
-  for (int s = 0; s < S; ++s)
-#pragma unroll
-    for (int it = 0; it < N / 256; ++it) r.v[s][it] = *reinterpret_cast<const float4 *>(src[s] + it * 256 + lane * 4);
-}
-template <int N, int S>
-__device__ __forceinline__ void stage_store_wave(float *const (&dst)[S], const StageRegs<N, S> &r) {
-  const int lane = int(threadIdx.x & 63);
-#pragma unroll
-  for (int s = 0; s < S; ++s)
-#pragma unroll
-    for (int it = 0; it < N / 256; ++it) *reinterpret_cast<float4 *>(dst[s] + it * 256 + lane * 4) = r.v[s][it];
-}
-
-// Stage one vector of N f32 into LDS with the whole workgroup of NT threads
-// (thread-strided float4) and return its exponent window to every thread;
-// red: LDS scratch of 2 NT / 64 ints.  Ends with a barrier, after which the
-// copy is visible to the workgroup.
-template <int N, int NT>
-__device__ __forceinline__ CodeWindow stage_x_block(float *dst, const float *__restrict__ src, int *red) {
-  static_assert(N % (4 * NT) == 0 && NT % 64 == 0, "whole float4 sweeps");
-  constexpr int IT = N / (4 * NT);
-  constexpr int W = NT / 64;
-  const int t = int(threadIdx.x);
-  float4 v[IT];
-#pragma unroll
-  for (int it = 0; it < IT; ++it) v[it] = *reinterpret_cast<const float4 *>(src + (it * NT + t) * 4);
-  int lo = 255, hi = 0;
-#pragma unroll
-  for (int it = 0; it < IT; ++it) {
-    *reinterpret_cast<float4 *>(dst + (it * NT + t) * 4) = v[it];
-    exp_range_acc(v[it].x, lo, hi);
-    exp_range_acc(v[it].y, lo, hi);
-    exp_range_acc(v[it].z, lo, hi);
-    exp_range_acc(v[it].w, lo, hi);
-  }
-  lo = wave_min_i(lo);
-  hi = wave_max_i(hi);
-  if ((t & 63) == 0) {
-    red[2 * (t >> 6)] = lo;
-    red[2 * (t >> 6) + 1] = hi;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int w = 0; w < W; ++w) {
-    lo = min(lo, red[2 * w]);
-    hi = max(hi, red[2 * w + 1]);
-  }
-  return mx_window(lo, hi);
-}
-
-// Window of one pair's h from the exponent ranges its exact phase-1 tiles
-// recorded (lo | hi << 16 per tile): the same range stage_x_block would find
-// by scanning h.
-constexpr int kP1Tiles = kInter / kP1ExactRows;
-__device__ __forceinline__ CodeWindow h_window(const uint32_t *__restrict__ tiles) {
-  static_assert(kP1Tiles == 128, "two tile words per lane");
-  const uint32_t lane = threadIdx.x & 63;
-  const uint32_t a = tiles[lane], b = tiles[lane + 64];
-  const int lo = min(int(a & 0xffffu), int(b & 0xffffu)), hi = max(int(a >> 16), int(b >> 16));
-  return mx_window(wave_min_i(lo), wave_max_i(hi));
-}
-
-// Copy n f32 (n % 4 == 0) into LDS with the calling wavefront, eight float4
-// loads in flight per lane.
-__device__ __forceinline__ void stage_chunk_wave(float *dst, const float *__restrict__ src, uint32_t n) {
-  const uint32_t lane = threadIdx.x & 63;
-  uint32_t i = lane * 4;
-  for (; i + 7 * 256 < n; i += 8 * 256) {
-    float4 v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4 *>(src + i + j * 256);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) *reinterpret_cast<float4 *>(dst + i + j * 256) = v[j];
-  }
-  for (; i < n; i += 256) *reinterpret_cast<float4 *>(dst + i) = *reinterpret_cast<const float4 *>(src + i);
-}
-
-// ---------------------------------------------------------------------------
-// EXACT row engine (lane pairs)
-// ---------------------------------------------------------------------------
-
-// The 16 x values of a lane's half-group, from LDS (two distinct addresses
-// per wavefront: even and odd lanes).
-struct X16 {
-  float v[16];
-};
-__device__ __forceinline__ void load_x16(X16 &x, const float *__restrict__ xs) {
-  const float4 *p = reinterpret_cast<const float4 *>(xs);
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const float4 q = p[d];
-    x.v[4 * d + 0] = q.x;
-    x.v[4 * d + 1] = q.y;
-    x.v[4 * d + 2] = q.z;
-    x.v[4 * d + 3] = q.w;
-  }
-}
-
-// One group of a lane pair's row chain, in k order: the running sum, held by
-// the odd lane between groups, passes to the even lane, which adds its 16
-// products; it passes back to the odd lane, which adds its own 16.  Each
-// hand-over is a DPP operand of the add that follows it (the other lane's
-// adds in each half are discarded), so a group costs 32 adds of which only
-// the two hand-overs read a just-written register across lanes and need
-// wait states.  A row starts from 0 in both lanes and ends with from_odd.
-__device__ __forceinline__ float pair_chain16(float acc, const float (&p)[16]) {
-  acc = __fadd_rn(from_odd(acc), p[0]);
-#pragma unroll
-  for (int j = 1; j < 16; ++j) acc = __fadd_rn(acc, p[j]);
-  acc = __fadd_rn(from_even(acc), p[0]);
-#pragma unroll
-  for (int j = 1; j < 16; ++j) acc = __fadd_rn(acc, p[j]);
-  return acc;
-}
-
-// MXFP4 products of the lane's 8 code bytes (16 k, low nibble first).
-// Scaled: p = x * (e2m1 * 2^(c-127)) via the gfx950 scaled converter — equal
-// to the oracle's (x * e2m1) * 2^(c-127) for codes inside the window.
-__device__ __forceinline__ void mx_products_scaled(float (&p)[16], uint2 w, uint32_t c, const X16 &x) {
-  const float sc = __uint_as_float(c << 23);
-  const uint32_t words[2] = {w.x, w.y};
-#pragma unroll
-  for (int d = 0; d < 2; ++d) {
-    const v2f q[4] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[d], sc, 0),
-                      __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[d], sc, 1),
-                      __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[d], sc, 2),
-                      __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[d], sc, 3)};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      p[8 * d + 2 * s] = __fmul_rn(x.v[8 * d + 2 * s], q[s].x);
-      p[8 * d + 2 * s + 1] = __fmul_rn(x.v[8 * d + 2 * s + 1], q[s].y);
-    }
-  }
-}
-// Literal: p = (x * e2m1) * ue8m0(c), any code.
-__device__ __forceinline__ void mx_products_literal(float (&p)[16], uint2 w, uint32_t c, const X16 &x) {
-  const float s = ue8m0_f32(c);
-  const uint32_t words[2] = {w.x, w.y};
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const float e = e2m1_f32((words[j >> 3] >> (4 * (j & 7))) & 15u);
-    p[j] = __fmul_rn(__fmul_rn(x.v[j], e), s);
-  }
-}
-
-template <int PF>
-struct MxBatch {
-  uint2 w[PF];
-  uint32_t c[PF / 4];
-};
-
-// Codes of groups [g0, g0+PF): the lane's 8 bytes at woff + 16 g (woff
-// includes the lane's half-group offset), scale codes at soff + g.  Loads
-// past a row's end read neighbouring bytes or, past num_records, zeros;
-// such values are never consumed.
-template <int PF>
-__device__ __forceinline__ void mx_load(MxBatch<PF> &b, const Src1 &src, uint32_t woff, uint32_t soff, int g0) {
-#pragma unroll
-  for (int i = 0; i < PF; ++i) b.w[i] = ld8(src.w, woff + 16u * uint32_t(g0 + i));
-#pragma unroll
-  for (int j = 0; j < PF / 4; ++j) b.c[j] = ld4(src.s, soff + uint32_t(g0) + 4u * j);
-}
-template <int PF>
-__device__ __forceinline__ void mx_load(MxBatch<PF> &b, const Src2 &src, uint32_t woff, uint32_t soff, int g0) {
-  if (src.hi)
-    mx_load<PF>(b, Src1{src.b, src.b}, woff, soff, g0);
-  else
-    mx_load<PF>(b, Src1{src.a, src.a}, woff, soff, g0);
-}
-
-template <int PF>
-__device__ __forceinline__ void mx_load(MxBatch<PF> &b, const SrcP &src, uint32_t woff, uint32_t soff, int g0) {
-#pragma unroll
-  for (int i = 0; i < PF; ++i) b.w[i] = gld8(src.p + woff + 16u * uint32_t(g0 + i));
-#pragma unroll
-  for (int j = 0; j < PF / 4; ++j) b.c[j] = gld4(src.p + soff + uint32_t(g0) + 4u * j);
-}
-
-__device__ __forceinline__ bool codes_in(uint32_t word, CodeWindow win) {
-  bool ok = true;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = int((word >> (8 * i)) & 255u);
-    ok = ok && c >= win.cmin && c <= win.cmax;
-  }
-  return ok;
-}
-
-template <int PF>
-__device__ __forceinline__ uint32_t batch_code(const MxBatch<PF> &b, int i) {
-  return (b.c[i >> 2] >> (8 * (i & 3))) & 255u;
-}
-
-// Single loads through either source form (the literal path re-reads its
-// codes rather than index the register batch dynamically).
-__device__ __forceinline__ uint2 src_ld8(const Src1 &s, uint32_t off) { return ld8(s.w, off); }
-__device__ __forceinline__ uint32_t src_ld1(const Src1 &s, uint32_t off) { return ld1(s.s, off); }
-__device__ __forceinline__ uint2 src_ld8(const Src2 &s, uint32_t off) {
-  uint2 v;
-  if (s.hi)
-    v = ld8(s.b, off);
-  else
-    v = ld8(s.a, off);
-  return v;
-}
-__device__ __forceinline__ uint2 src_ld8(const SrcP &s, uint32_t off) { return gld8(s.p + off); }
-__device__ __forceinline__ uint32_t src_ld1(const SrcP &s, uint32_t off) { return s.p[off]; }
-__device__ __forceinline__ uint32_t src_ld1(const Src2 &s, uint32_t off) {
-  uint32_t v;
-  if (s.hi)
-    v = ld1(s.b, off);
-  else
-    v = ld1(s.a, off);
-  return v;
-}
-
-// The scale codes of a lane pair's row, split between its lanes (the even
-// lane holds groups [0, G/2), the odd lane [G/2, G)), loaded ahead of the
-// row so that one check decides the decode of the whole row.
-template <int G>
-struct RowCodes {
-  uint4 v[G / 32];
-};
-template <int G>
-__device__ __forceinline__ void load_row_codes(RowCodes<G> &rc, const Src1 &src, uint32_t soff) {
-  const uint32_t base = soff + (threadIdx.x & 1u) * uint32_t(G / 2);
-#pragma unroll
-  for (int i = 0; i < G / 32; ++i) rc.v[i] = ld16(src.s, base + 16u * i);
-}
-template <int G>
-__device__ __forceinline__ void load_row_codes(RowCodes<G> &rc, const SrcP &src, uint32_t soff) {
-  const uint32_t base = soff + (threadIdx.x & 1u) * uint32_t(G / 2);
-#pragma unroll
-  for (int i = 0; i < G / 32; ++i) {
-    const v4u v = *(const __attribute__((address_space(1))) v4u *)(src.p + base + 16u * i);
-    rc.v[i] = make_uint4(v.x, v.y, v.z, v.w);
-  }
-}
-
-// True (in every lane) when every scale code of every row of the wavefront
-// lies in its lane's window: byte minimum and maximum through packed 16-bit
-// min/max of the even and odd bytes.
-template <int G>
-__device__ __forceinline__ bool row_codes_in(const RowCodes<G> &rc, CodeWindow win) {
-  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-  u16x2 mn = {255, 255}, mx = {0, 0};
-#pragma unroll
-  for (int i = 0; i < G / 32; ++i) {
-    const uint32_t w[4] = {rc.v[i].x, rc.v[i].y, rc.v[i].z, rc.v[i].w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const u16x2 lo = __builtin_bit_cast(u16x2, w[j] & 0x00ff00ffu);
-      const u16x2 hi = __builtin_bit_cast(u16x2, (w[j] >> 8) & 0x00ff00ffu);
-      mn = __builtin_elementwise_min(mn, __builtin_elementwise_min(lo, hi));
-      mx = __builtin_elementwise_max(mx, __builtin_elementwise_max(lo, hi));
-    }
-  }
-  const int cmin = min(int(mn.x), int(mn.y)), cmax = max(int(mx.x), int(mx.y));
-  const bool ok = cmin >= win.cmin && cmax <= win.cmax;
-  return __builtin_amdgcn_ballot_w64(!ok) == 0;
-}
-
-// One batch: if every lane's codes are inside its window the batch runs the
-// scaled decode as straight-line code, software-pipelined: group i+1's x
-// reads and products are issued ahead of group i's add chain, so LDS latency
-// and the chain's DPP read-after-write waits overlap independent work.
-// Otherwise the batch takes the literal decode, group by group, re-reading
-// its codes (compact code for a path real scale codes do not take).
-template <int PF, bool kCheck = true, class Src>
-__device__ __forceinline__ float mx_consume(float acc, const MxBatch<PF> &b, const Src &src, uint32_t woff,
-                                            uint32_t soff, const float *__restrict__ xh, int g0, CodeWindow win) {
-  bool ok = true;
-  if constexpr (kCheck) {
-#pragma unroll
-    for (int j = 0; j < PF / 4; ++j) ok = ok && codes_in(b.c[j], win);
-  }
-  if (!kCheck || __builtin_amdgcn_ballot_w64(!ok) == 0) {
-    X16 xa, xb;
-    float p[16], q[16];
-    load_x16(xa, xh + g0 * 32);
-    load_x16(xb, xh + (g0 + 1) * 32);
-    mx_products_scaled(p, b.w[0], batch_code(b, 0), xa);
-#pragma unroll
-    for (int i = 0; i < PF; i += 2) {
-      // p holds group i's products; xb holds group i+1's x
-      if (i + 2 < PF) load_x16(xa, xh + (g0 + i + 2) * 32);
-      mx_products_scaled(q, b.w[i + 1], batch_code(b, i + 1), xb);
-      acc = pair_chain16(acc, p);
-      if (i + 3 < PF) load_x16(xb, xh + (g0 + i + 3) * 32);
-      if (i + 2 < PF) mx_products_scaled(p, b.w[i + 2], batch_code(b, i + 2), xa);
-      acc = pair_chain16(acc, q);
-    }
-  } else {
-#pragma unroll 1
-    for (int g = g0; g < g0 + PF; ++g) {
-      float p[16];
-      X16 x;
-      load_x16(x, xh + g * 32);
-      mx_products_literal(p, src_ld8(src, woff + 16u * uint32_t(g)), src_ld1(src, soff + uint32_t(g)), x);
-      acc = pair_chain16(acc, p);
-    }
-  }
-  return acc;
-}
-
-// Dot of one MXFP4 row of G groups (G % PF == 0) with x in LDS (xh = x +
-// 16 * (lane & 1)); result in both lanes.  `ba` arrives holding groups
-// [0, PF) (loaded by the caller with mx_load, ahead of its own set-up work);
-// two register batches of PF groups then ping-pong so that batch b+1 is in
-// flight while batch b is consumed.  (The loop prefetches one batch past
-// the row's end: neighbouring bytes or zeros, never consumed.)
-template <int PF, class Src>
-__device__ __forceinline__ float mx_row_pair(float acc, MxBatch<PF> &ba, const Src &src, uint32_t woff,
-                                             uint32_t soff, int G, const float *__restrict__ xh, CodeWindow win) {
-  static_assert(PF % 4 == 0, "scale words hold 4 codes");
-  MxBatch<PF> bb;
-  int g0 = 0;
-  for (; g0 + 2 * PF <= G; g0 += 2 * PF) {
-    mx_load<PF>(bb, src, woff, soff, g0 + PF);
-    acc = mx_consume<PF>(acc, ba, src, woff, soff, xh, g0, win);
-    mx_load<PF>(ba, src, woff, soff, g0 + 2 * PF);
-    acc = mx_consume<PF>(acc, bb, src, woff, soff, xh, g0 + PF, win);
-  }
-  if (g0 < G) acc = mx_consume<PF>(acc, ba, src, woff, soff, xh, g0, win);  // one batch left
-  return from_odd(acc);
-}
-
-// The same for a compile-time group count G (G % (2 PF) == 0), with the
-// last two batches peeled so that no load reaches past the row (decode
-// chosen batch by batch).
-template <int PF, int G, class Src>
-__device__ __forceinline__ float mx_row_pair_fixed(float acc, MxBatch<PF> &ba, const Src &src, uint32_t woff,
-                                                   uint32_t soff, const float *__restrict__ xh, CodeWindow win) {
-  static_assert(PF % 4 == 0 && G % (2 * PF) == 0, "whole batch pairs");
-  MxBatch<PF> bb;
-#pragma unroll 1
-  for (int g0 = 0; g0 < G - 2 * PF; g0 += 2 * PF) {
-    mx_load<PF>(bb, src, woff, soff, g0 + PF);
-    acc = mx_consume<PF>(acc, ba, src, woff, soff, xh, g0, win);
-    mx_load<PF>(ba, src, woff, soff, g0 + 2 * PF);
-    acc = mx_consume<PF>(acc, bb, src, woff, soff, xh, g0 + PF, win);
-  }
-  mx_load<PF>(bb, src, woff, soff, G - PF);
-  acc = mx_consume<PF>(acc, ba, src, woff, soff, xh, G - 2 * PF, win);
-  acc = mx_consume<PF>(acc, bb, src, woff, soff, xh, G - PF, win);
-  return from_odd(acc);
-}
-
-// The same with the decode chosen once for the whole row from its codes (rc,
-// loaded by the caller with load_row_codes): the scaled batches with no
-// per-batch check, or the literal decode group by group.
-template <int PF, int G, class Src>
-__device__ __forceinline__ float mx_row_pair_fixed(float acc, MxBatch<PF> &ba, const Src &src, uint32_t woff,
-                                                   uint32_t soff, const float *__restrict__ xh, CodeWindow win,
-                                                   const RowCodes<G> &rc) {
-  static_assert(PF % 4 == 0 && G % (2 * PF) == 0, "whole batch pairs");
-  if (row_codes_in<G>(rc, win)) {
-    MxBatch<PF> bb;
-#pragma unroll 1
-    for (int g0 = 0; g0 < G - 2 * PF; g0 += 2 * PF) {
-      mx_load<PF>(bb, src, woff, soff, g0 + PF);
-      acc = mx_consume<PF, false>(acc, ba, src, woff, soff, xh, g0, win);
-      mx_load<PF>(ba, src, woff, soff, g0 + 2 * PF);
-      acc = mx_consume<PF, false>(acc, bb, src, woff, soff, xh, g0 + PF, win);
-    }
-    mx_load<PF>(bb, src, woff, soff, G - PF);
-    acc = mx_consume<PF, false>(acc, ba, src, woff, soff, xh, G - 2 * PF, win);
-    acc = mx_consume<PF, false>(acc, bb, src, woff, soff, xh, G - PF, win);
-  } else {
-#pragma unroll 1
-    for (int g = 0; g < G; ++g) {
-      float p[16];
-      X16 x;
-      load_x16(x, xh + g * 32);
-      mx_products_literal(p, src_ld8(src, woff + 16u * uint32_t(g)), src_ld1(src, soff + uint32_t(g)), x);
-      acc = pair_chain16(acc, p);
-    }
-  }
-  return from_odd(acc);
-}
-
-// FP8 products of the lane's 16 code bytes: p = (x * e4m3) * s
-// (s14_vulkan_numeric.rs:1698-1714).
-__device__ __forceinline__ void fp8_products(float (&p)[16], uint4 w, float s, const X16 &x) {
-  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const v2f lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, false);
-    const v2f hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, true);
-    p[4 * d + 0] = __fmul_rn(__fmul_rn(x.v[4 * d + 0], lo.x), s);
-    p[4 * d + 1] = __fmul_rn(__fmul_rn(x.v[4 * d + 1], lo.y), s);
-    p[4 * d + 2] = __fmul_rn(__fmul_rn(x.v[4 * d + 2], hi.x), s);
-    p[4 * d + 3] = __fmul_rn(__fmul_rn(x.v[4 * d + 3], hi.y), s);
-  }
-}
-
-// FP8 batch: 4 groups of 32 k (one 128-wide scale tile when g0 % 4 == 0).
-struct Fp8Batch {
-  uint4 w[4];
-  float s;
-};
-__device__ __forceinline__ float fp8_scale(Rsrc r, uint32_t soff, uint32_t tile, int scale_f32) {
-  return scale_f32 ? ldf(r, soff + 4u * tile) : ue8m0_f32(ld1(r, soff + tile));
-}
-__device__ __forceinline__ void fp8_load(Fp8Batch &b, const Src1 &src, uint32_t woff, uint32_t soff, int scale_f32,
-                                         int g0) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) b.w[i] = ld16(src.w, woff + 32u * uint32_t(g0 + i));
-  b.s = fp8_scale(src.s, soff, uint32_t(g0) / 4u, scale_f32);
-}
-__device__ __forceinline__ void fp8_load(Fp8Batch &b, const Src2 &src, uint32_t woff, uint32_t soff, int scale_f32,
-                                         int g0) {
-  if (src.hi)
-    fp8_load(b, Src1{src.b, src.b}, woff, soff, scale_f32, g0);
-  else
-    fp8_load(b, Src1{src.a, src.a}, woff, soff, scale_f32, g0);
-}
-// Four groups, pipelined like mx_consume.
-__device__ __forceinline__ float fp8_consume(float acc, const Fp8Batch &b, const float *__restrict__ xh, int g0) {
-  X16 xa, xb;
-  float p[16], q[16];
-  load_x16(xa, xh + g0 * 32);
-  load_x16(xb, xh + (g0 + 1) * 32);
-  fp8_products(p, b.w[0], b.s, xa);
-#pragma unroll
-  for (int i = 0; i < 4; i += 2) {
-    if (i + 2 < 4) load_x16(xa, xh + (g0 + i + 2) * 32);
-    fp8_products(q, b.w[i + 1], b.s, xb);
-    acc = pair_chain16(acc, p);
-    if (i + 3 < 4) load_x16(xb, xh + (g0 + i + 3) * 32);
-    if (i + 2 < 4) fp8_products(p, b.w[i + 2], b.s, xa);
-    acc = pair_chain16(acc, q);
-  }
-  return acc;
-}
-
-// Dot of one FP8 row of G groups of 32 k with x in LDS (woff includes the
-// lane's 16-byte half-group offset; soff is the byte offset of the row's
-// first tile scale); result in both lanes.
-template <class Src>
-__device__ __forceinline__ float fp8_row_pair(float acc, const Src &src, uint32_t woff, uint32_t soff,
-                                              int scale_f32, int G, const float *__restrict__ xh) {
-  const int G4 = G & ~3;
-  Fp8Batch ba, bb;
-  fp8_load(ba, src, woff, soff, scale_f32, 0);
-  int g0 = 0;
-  for (; g0 + 8 <= G4; g0 += 8) {
-    fp8_load(bb, src, woff, soff, scale_f32, g0 + 4);
-    acc = fp8_consume(acc, ba, xh, g0);
-    fp8_load(ba, src, woff, soff, scale_f32, g0 + 8);
-    acc = fp8_consume(acc, bb, xh, g0 + 4);
-  }
-  if (g0 < G4) {
-    acc = fp8_consume(acc, ba, xh, g0);
-    g0 += 4;
-  }
-  for (; g0 < G; ++g0) {  // groups of a last partial tile
-    Fp8Batch t;
-    fp8_load(t, src, woff, soff, scale_f32, g0);  // loads 4 groups, uses one
-    float p[16];
-    X16 x;
-    load_x16(x, xh + g0 * 32);
-    fp8_products(p, t.w[0], t.s, x);
-    acc = pair_chain16(acc, p);
-  }
-  return from_odd(acc);
-}
 
 // ---------------------------------------------------------------------------
 // standalone EXACT matvecs: 32 rows per wavefront (one row per lane pair),
@@ -540,10 +35,6 @@ __device__ __forceinline__ float fp8_row_pair(float acc, const Src &src, uint32_
 // ---------------------------------------------------------------------------
 
 constexpr int kExactChunk = 4096;
-// Groups per register batch in the fused exact kernels.  Larger batches hide
-// more load latency but inline a longer straight-line body; on the box 8
-// beat 16 by 10 % per layer (instruction supply) and 4 (batch overhead).
-constexpr int kPF = 8;
 
 __global__ __launch_bounds__(64) void k_mxfp4_matvec_exact(uint32_t N, uint32_t K,
                                                            const float *__restrict__ x,
@@ -954,50 +445,6 @@ __global__ void k_fill_page(uint8_t *__restrict__ page, uint64_t seed, uint32_t 
 //            last, in LDS (s14_vulkan_numeric.rs:929-946)
 // ---------------------------------------------------------------------------
 
-// Router: one wavefront per (expert, token).  Logit order (fixed here; the
-// reference uses torch F.linear, executor.py:641, whose order is the
-// BLAS's): lane l sums k = 256c + 4l + j (c ascending, j = 0..3), then the
-// xor butterfly over lanes.  Score: sigmoid (north-star config) or
-// sqrt(softplus) with torch's threshold 20 (executor.py:642).
-// Score and biased score of expert e from its logit.
-__device__ __forceinline__ float2 router_finish(const RouterArgs &r, float logit, uint32_t e) {
-  float sc;
-  if (r.score_fn == S14_SCORE_SIGMOID) {
-    sc = __fdiv_rn(1.0f, __fadd_rn(1.0f, s14x::expf_glibc(-logit)));
-  } else {
-    const float sp = logit > 20.0f ? logit : log1pf(s14x::expf_glibc(logit));
-    sc = __fsqrt_rn(sp);
-  }
-  return make_float2(sc, __fadd_rn(sc, r.bias[e]));
-}
-
-// Score of expert e for token t, computed by one whole wavefront; valid in
-// lane 0 (the biased score in .y).
-__device__ __forceinline__ float2 router_score(const RouterArgs &r, const float *__restrict__ X, uint32_t t,
-                                               uint32_t e) {
-  const uint32_t lane = threadIdx.x & 63;
-  const uint32_t K = kHidden;
-  const float *x = X + size_t(t) * K;
-  const float *row = r.weight + size_t(e) * K;
-  float4 wv[K / 256], xv[K / 256];
-#pragma unroll
-  for (uint32_t c = 0; c < K / 256; ++c) {
-    wv[c] = *reinterpret_cast<const float4 *>(row + c * 256 + lane * 4);
-    xv[c] = *reinterpret_cast<const float4 *>(x + c * 256 + lane * 4);
-  }
-  float acc = 0.0f;
-#pragma unroll
-  for (uint32_t c = 0; c < K / 256; ++c) {
-    acc = __fadd_rn(acc, __fmul_rn(wv[c].x, xv[c].x));
-    acc = __fadd_rn(acc, __fmul_rn(wv[c].y, xv[c].y));
-    acc = __fadd_rn(acc, __fmul_rn(wv[c].z, xv[c].z));
-    acc = __fadd_rn(acc, __fmul_rn(wv[c].w, xv[c].w));
-  }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, m));
-  return router_finish(r, acc, e);
-}
-
 // Router scores of many tokens (the prefill's first step): one wavefront per
 // tile of kRtE experts x kRtT tokens, every logit summed in router_score's
 // order (bit-identical), each weight and x chunk loaded once per tile
@@ -1072,10 +519,19 @@ __device__ __forceinline__ void plan_token(const RouteSpec &rs, uint32_t t, cons
   const uint32_t k = rs.r.topk;
   const TopK c = select_topk_lds(biased, scores, pages, rs.r.n_experts, k);
   if (lane < k) {
-    const float wgt = route_weight(c, rs.r.route_scale);
+    float wgt = route_weight(c, rs.r.route_scale);
+    uint64_t pg = c.page;
+    if (pages && pg == 0ull) {
+      // a chosen expert without a resident page: its pair reads the shared
+      // page instead (mapped memory; the result is discarded) and its NaN
+      // weight makes the token's output NaN; the status word says why
+      __hip_atomic_fetch_or(rs.status, kStatusNullPage, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pg = reinterpret_cast<uint64_t>(rs.shared_page);
+      wgt = __builtin_nanf("");
+    }
     pl.ids[t][lane] = c.id;
     pl.wts[t][lane] = wgt;
-    pl.pgs[t][lane] = c.page;
+    pl.pgs[t][lane] = pg;
     if (rs.ids_out) rs.ids_out[t * k + lane] = uint16_t(c.id);
     if (rs.weights_out) rs.weights_out[t * k + lane] = wgt;
   }
@@ -1640,6 +1096,7 @@ __global__ void k_clear_u32(uint32_t *p, uint32_t n) {
 
 hipError_t launch_clear_route_counters(hipStream_t s, const Workspace &ws) {
   k_clear_u32<<<1, 256, 0, s>>>(ws.route_count, kRouteCounters);
+  k_clear_u32<<<1, 256, 0, s>>>(ws.sync, kSyncLines * kRouteCounterStride);
   return hipGetLastError();
 }
 

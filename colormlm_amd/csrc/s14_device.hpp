@@ -86,13 +86,22 @@ struct Workspace {
   float *biased;  // [kMaxTokens][kMaxExperts]
   uint32_t *route_count;  // [kRouteCounters]: groups, then per-group workgroups, of the running route launch that are done (one per 128-byte line)
   uint32_t *hwin;         // [kMaxPairs][kInter / kP1ExactRows]: exponent range (lo | hi << 16) of each exact phase-1 tile's h
+  // kSyncLines lines of kRouteCounterStride words: the status word (kStatus*
+  // bits) that launches leave for s14_launch_status.
+  uint32_t *sync;
   size_t bytes;
 };
+constexpr uint32_t kSyncLines = 1;
+constexpr uint32_t kSyncStatusLine = kSyncLines - 1;  // the status word's line
+inline uint32_t *status_word(const Workspace &ws) { return ws.sync + kSyncStatusLine * kRouteCounterStride; }
+// Status bits a launch leaves in the status line of ws.sync (sticky until
+// read by s14_launch_status).
+enum : uint32_t { kStatusNullPage = 1u, kStatusWaitTimeout = 2u };
 
 // Layout of the workspace in one device allocation (each region 256-byte
 // aligned): table | h | scores | biased | route counters | h windows.
 struct WorkspaceLayout {
-  size_t table, h, scores, biased, count, hwin, bytes;
+  size_t table, h, scores, biased, count, hwin, sync, bytes;
 };
 constexpr size_t ws_align(size_t v) { return (v + 255) / 256 * 256; }
 constexpr WorkspaceLayout workspace_layout() {
@@ -110,6 +119,8 @@ constexpr WorkspaceLayout workspace_layout() {
   off = ws_align(off + sizeof(uint32_t) * kRouteCounters);
   l.hwin = off;
   off = ws_align(off + sizeof(uint32_t) * kMaxPairs * (kInter / kP1ExactRows));
+  l.sync = off;
+  off = ws_align(off + sizeof(uint32_t) * kSyncLines * kRouteCounterStride);
   l.bytes = off;
   return l;
 }
@@ -127,6 +138,7 @@ inline Workspace workspace_carve(void *base) {
   ws.biased = reinterpret_cast<float *>(b + l.biased);
   ws.route_count = reinterpret_cast<uint32_t *>(b + l.count);
   ws.hwin = reinterpret_cast<uint32_t *>(b + l.hwin);
+  ws.sync = reinterpret_cast<uint32_t *>(b + l.sync);
   ws.bytes = l.bytes;
   return ws;
 }
@@ -153,6 +165,7 @@ struct RouteSpec {
   const uint8_t *shared_page;
   uint16_t *ids_out;
   float *weights_out;
+  uint32_t *status;  // the workspace's status word (kStatus* bits)
 };
 
 // Optional start/stop events a fused launcher attaches to its kernel launch
@@ -176,8 +189,9 @@ hipError_t launch_fill_mxfp4_page(hipStream_t s, uint8_t *page, uint64_t seed, u
                                   uint32_t expert, uint32_t hidden, uint32_t inter, int lo, int hi,
                                   const PageOffsets &off);
 
-// Zeroes the route completion counters of a workspace (they start at 0 and
-// every route launch leaves them at 0).
+// Zeroes the route kernel's completion counters and the status word of a
+// workspace (the counters start at 0 and every route launch leaves them at
+// 0).
 hipError_t launch_clear_route_counters(hipStream_t s, const Workspace &ws);
 
 // --- fused layer / block path: route (router + plan) -> phase 1 -> phase 2 ---

@@ -210,8 +210,28 @@ struct TopK {
   uint64_t page;
   float sum;
 };
+// Plain loads of scores, biased scores and pages (written before the kernel).
+struct PlainScoreLoad {
+  const float *biased, *scores;
+  const uint64_t *pages;
+  __device__ float b(uint32_t e) const { return biased[e]; }
+  __device__ float s(uint32_t e) const { return scores[e]; }
+  __device__ uint64_t p(uint32_t e) const { return pages ? pages[e] : 0ull; }
+};
+
+template <class Load>
+__device__ __forceinline__ TopK select_topk_from(const Load &ld, uint32_t n_experts, uint32_t k);
+
 __device__ __forceinline__ TopK select_topk(const float *__restrict__ biased, const float *__restrict__ scores,
                                             const uint64_t *__restrict__ pages, uint32_t n_experts, uint32_t k) {
+  return select_topk_from(PlainScoreLoad{biased, scores, pages}, n_experts, k);
+}
+
+// The selection with the scores and pages read through `ld` (b(e), s(e),
+// p(e)): e.g. device-scope loads of scores other workgroups of the same
+// launch wrote.
+template <class Load>
+__device__ __forceinline__ TopK select_topk_from(const Load &ld, uint32_t n_experts, uint32_t k) {
   const uint32_t lane = threadIdx.x & 63;
   // lane l holds experts 4l .. 4l+3, so a lower lane holds only lower
   // indices: the lowest lane with the maximum key, then its lowest slot, is
@@ -224,9 +244,9 @@ __device__ __forceinline__ TopK select_topk(const float *__restrict__ biased, co
   for (int j = 0; j < 4; ++j) {
     const uint32_t ee = 4u * lane + uint32_t(j);
     const bool absent = ee >= n_experts;
-    kv[j] = absent ? 0u : max(score_key(biased[ee]), 1u);
-    sv[j] = absent ? 0.0f : scores[ee];
-    pv[j] = (absent || !pages) ? 0ull : pages[ee];
+    kv[j] = absent ? 0u : max(score_key(ld.b(ee)), 1u);
+    sv[j] = absent ? 0.0f : ld.s(ee);
+    pv[j] = absent ? 0ull : ld.p(ee);
   }
   TopK mine{0u, 0.0f, 0ull, 0.0f};
   float sum = 0.0f;

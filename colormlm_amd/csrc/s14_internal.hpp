@@ -22,6 +22,9 @@ int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, con
                        const uint64_t *expert_pages_dev, const uint8_t *shared_page, int shared_format,
                        const float *x, float *y, uint16_t *ids_out, float *weights_out, int mode,
                        const KernelEvents *ev);
+// Status bits the last launches left in ws (synchronises the device and
+// clears them): S14_OK, or the error they stand for.
+int read_launch_status(const Workspace &ws, int device);
 
 // Records `msg` as this thread's last error and returns `code`.
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));

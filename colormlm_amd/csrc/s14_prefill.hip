@@ -130,8 +130,12 @@ __global__ __launch_bounds__(256) void k_prefill_topk(PrefillArgs a, PrefillWork
                              a.r.n_experts, k);
   if (lane < k) {
     const float w = route_weight(c, a.r.route_scale);
+    // the pairs of an expert without a resident page combine with a NaN
+    // weight (their GEMM tiles read the shared page instead)
+    const bool resident = a.expert_pages[c.id] != 0ull;
+    if (!resident) __hip_atomic_fetch_or(a.status, kStatusNullPage, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     ws.ids[t * kTopK + lane] = c.id;
-    ws.weights[t * kTopK + lane] = w;
+    ws.weights[t * kTopK + lane] = resident ? w : __builtin_nanf("");
     if (a.ids_out) a.ids_out[t * k + lane] = uint16_t(c.id);
     if (a.weights_out) a.weights_out[t * k + lane] = w;
     atomicOr(&ws.token_bits[c.id * kPrefillBitWords + (t >> 5)], 1u << (t & 31));
@@ -282,8 +286,12 @@ __global__ __launch_bounds__(256) void k_tile_x(PrefillWorkspace ws) {
   }
 }
 
+// A page of 0 (an expert that is not resident) reads the shared page instead
+// (mapped memory); the top-k step gave its pairs a NaN weight and set the
+// status word.
 __device__ __forceinline__ Rsrc page_rsrc(const PrefillArgs &a, uint32_t e) {
   const uint8_t *page = e < kMaxExperts ? reinterpret_cast<const uint8_t *>(a.expert_pages[e]) : a.shared_page;
+  if (!page) page = a.shared_page;
   return make_rsrc(page, uint32_t(S14_EXPERT_PAGE_BYTES));
 }
 

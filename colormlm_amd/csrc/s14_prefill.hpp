@@ -49,6 +49,7 @@ struct PrefillArgs {
   float *y;        // [tokens][4096]
   uint16_t *ids_out;
   float *weights_out;
+  uint32_t *status;  // the context workspace's status word (kStatus* bits)
 };
 
 // Device workspace for up to kMaxPrefillTokens tokens (one allocation per

@@ -105,6 +105,11 @@ class Context:
         check(lib().s14_ctx_stage_times(self._h, ms, 4, C.byref(n)))
         return [float(ms[i]) for i in range(n.value)]
 
+    def launch_status(self) -> None:
+        """Raises S14Error if a routed launch since the last call found a
+        page address of 0 (synchronises)."""
+        check(lib().s14_launch_status(self._h))
+
     def destroy(self) -> None:
         if self._h:
             lib().s14_ctx_destroy(self._h)

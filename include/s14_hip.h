@@ -273,6 +273,16 @@ int s14_moe_block_route_noalloc(void *stream, uint32_t tokens, const s14_router 
                                 float *weights_out, int mode);
 uint64_t s14_noalloc_scratch_bytes(void);
 
+/* Device-side status of the routed launches on this context since the last
+ * call (synchronises the device, then clears it).  The routed entry points
+ * read each chosen expert's page address from expert_pages_dev on the
+ * device; every entry of that table must be the address of a resident,
+ * pinned page of the layer (lease it through s14_moe_pages_* and release it
+ * only after the launch's compute fence).  A launch that finds a 0 entry
+ * reads no memory through it, writes NaN for the affected outputs and leaves
+ * a status that this call reports as S14_ERR_INVALID. */
+int s14_launch_status(s14_ctx *ctx);
+
 /* Router only (scores f32 [n_experts], ids u16 [topk], weights f32 [topk]). */
 int s14_route(s14_ctx *ctx, void *stream, const s14_router *router, uint32_t tokens,
               const float *x, float *scores_out, uint16_t *ids_out, float *weights_out);

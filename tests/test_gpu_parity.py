@@ -765,3 +765,50 @@ def test_prefill_ragged_and_max_tokens(ctx, oracle, bank, prefill_router, tokens
     with pytest.raises(N.S14Error):
         s14.moe_prefill(ctx, 1025, prefill_router["router"], bank["table"], bank["pages"][256], dev(xs[:1]),
                         torch.empty(1, device="cuda"))
+
+
+def test_nonresident_page_is_reported_not_read(ctx, oracle, bank, prefill_router):
+    """A routed expert whose page-table entry is 0 (not resident): the one-token
+    single-launch kernel, a block launch and a prefill each read the shared
+    page in its place (mapped memory), write NaN for the tokens that chose it,
+    and leave a status that s14_launch_status reports as S14_ERR_INVALID; a
+    clean launch afterwards reports S14_OK.  The entry zeroed is one the
+    oracle's router picks for token 0."""
+    ctx.launch_status()  # clear anything earlier tests left
+    router = s14.Router(bank["wr_d"], bank["bias_d"])
+    shared = bank["pages"][256]
+    xs = synth.block_tokens(seed=21, tokens=4)
+    _, i0, _ = oracle.route(bank["wr"], bank["bias"], xs[0])
+    gone = int(i0[2])
+    table = bank["table"].clone()
+    table[gone] = 0
+    chose = [gone in oracle.route(bank["wr"], bank["bias"], xs[t])[1].tolist() for t in range(4)]
+    say(f"non-resident expert {gone}: K=1 exact, K=1 fast, block T=4, prefill T=4")
+    for mode in (s14.EXACT, s14.FAST):
+        y = torch.zeros(HIDDEN, dtype=torch.float32, device="cuda")
+        s14.moe_layer_route(ctx, router, table, shared, dev(xs[0]), y, mode=mode)
+        assert np.isnan(host(y)).all()
+        with pytest.raises(s14.S14Error) as err:
+            ctx.launch_status()
+        assert err.value.code == N.S14_ERR_INVALID
+    yb = torch.zeros((4, HIDDEN), dtype=torch.float32, device="cuda")
+    s14.moe_block_route(ctx, 4, router, table, shared, dev(xs), yb, mode=s14.EXACT)
+    got = host(yb)
+    for t in range(4):
+        assert np.isnan(got[t]).all() == chose[t] and (chose[t] or not np.isnan(got[t]).any())
+    with pytest.raises(s14.S14Error):
+        ctx.launch_status()
+    yp = torch.zeros((4, HIDDEN), dtype=torch.float32, device="cuda")
+    s14.moe_prefill(ctx, 4, prefill_router["router"], table, shared, dev(xs), yp)
+    got = host(yp)
+    p_chose = [gone in oracle.route(prefill_router["wr"], prefill_router["bias"], xs[t])[1].tolist() for t in range(4)]
+    for t in range(4):
+        assert np.isnan(got[t]).all() == p_chose[t]
+    if any(p_chose):
+        with pytest.raises(s14.S14Error):
+            ctx.launch_status()
+    # a clean launch leaves no status
+    y = torch.zeros(HIDDEN, dtype=torch.float32, device="cuda")
+    s14.moe_layer_route(ctx, router, bank["table"], shared, dev(xs[0]), y, mode=s14.EXACT)
+    ctx.launch_status()
+    assert not np.isnan(host(y)).any()

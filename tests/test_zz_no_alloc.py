@@ -52,7 +52,8 @@ def setup():
 def test_noalloc_matches_context_entry(setup, mode):
     ctx, pages, table, router = setup
     assert N.lib().s14_noalloc_scratch_bytes() > 0
-    for call, tokens in enumerate((8, 3)):  # the second call smaller than the first
+    # each call smaller than the one before; one token runs the single-launch layer kernel
+    for call, tokens in enumerate((8, 3, 1)):
         say(f"no-alloc call {call}: T={tokens} mode={mode}")
         x = torch.from_numpy(synth.block_tokens(seed=40 + call, tokens=tokens)).cuda()
         y_ref = torch.full((tokens, HIDDEN), np.nan, dtype=torch.float32, device="cuda")
