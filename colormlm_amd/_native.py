@@ -142,6 +142,9 @@ class Router(C.Structure):
         ("topk", C.c_uint32),
         ("score_fn", C.c_int),
         ("route_scale", C.c_float),
+        ("tid2eid", C.c_void_p),
+        ("vocab", C.c_uint32),
+        ("token_ids", C.c_void_p),
     ]
 
 

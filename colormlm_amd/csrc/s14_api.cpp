@@ -351,11 +351,14 @@ int check_router(const s14_router *r) {
     return fail(S14_ERR_INVALID, "unknown score function %d", r->score_fn);
   if (!std::isfinite(r->route_scale) || r->route_scale <= 0.0f)
     return fail(S14_ERR_INVALID, "route_scale must be finite and positive");
+  if (r->tid2eid && (!r->token_ids || r->vocab == 0))
+    return fail(S14_ERR_INVALID, "hash routing needs token ids and a non-empty tid2eid table");
   return S14_OK;
 }
 
 s14::RouterArgs router_args(const s14_router *r) {
-  return s14::RouterArgs{r->weight, r->bias, r->n_experts, r->topk, r->score_fn, r->route_scale};
+  return s14::RouterArgs{r->weight, r->bias,    r->n_experts, r->topk,     r->score_fn,
+                         r->route_scale, r->tid2eid, r->vocab, r->token_ids};
 }
 
 // Stage-timing events for stage i of a fused launch (none when off).
@@ -524,7 +527,9 @@ int read_launch_status(const Workspace &ws, int device) {
   S14_HIP(hipMemcpy(word, &zero, sizeof(zero), hipMemcpyHostToDevice), "hipMemcpy(status clear)");
   if (bits & kStatusNullPage)
     return fail(S14_ERR_INVALID, "a routed expert's page address was 0 (page not resident); outputs are NaN");
-  return fail(S14_ERR_HIP, "an in-kernel wait timed out (status 0x%x); outputs are NaN", bits);
+  return fail(S14_ERR_ROUTE,
+              "a token's route failed RouteDecision::validate_for (expert id out of range or repeated, weight "
+              "not finite or negative, or weight sum off route_scale by more than 1e-4); its outputs are NaN");
 }
 }  // namespace s14
 

@@ -517,11 +517,22 @@ __device__ __forceinline__ void plan_token(const RouteSpec &rs, uint32_t t, cons
                                            const uint64_t *pages, PlanLds &pl) {
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t k = rs.r.topk;
-  const TopK c = select_topk_lds(biased, scores, pages, rs.r.n_experts, k);
+  bool bad = false;
+  const TopK c = rs.r.tid2eid ? select_hash_from(LdsScoreLoad{scores, pages}, rs.r, t, bad)
+                              : select_topk_lds(biased, scores, pages, rs.r.n_experts, k);
+  float wgt = lane < k ? route_weight(c, rs.r.route_scale) : 0.0f;
+  bad = bad || !route_weights_valid(wgt, k, rs.r.route_scale);
+  if (bad && lane == 0) __hip_atomic_fetch_or(rs.status, kStatusBadRoute, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (lane < k) {
-    float wgt = route_weight(c, rs.r.route_scale);
+    uint32_t id = c.id;
     uint64_t pg = c.page;
-    if (pages && pg == 0ull) {
+    if (bad) {
+      // a route that fails validate_for: distinct placeholder experts (so the
+      // pair table stays well formed) on the shared page, NaN weights
+      id = lane;
+      pg = reinterpret_cast<uint64_t>(rs.shared_page);
+      wgt = __builtin_nanf("");
+    } else if (pages && pg == 0ull) {
       // a chosen expert without a resident page: its pair reads the shared
       // page instead (mapped memory; the result is discarded) and its NaN
       // weight makes the token's output NaN; the status word says why
@@ -529,10 +540,10 @@ __device__ __forceinline__ void plan_token(const RouteSpec &rs, uint32_t t, cons
       pg = reinterpret_cast<uint64_t>(rs.shared_page);
       wgt = __builtin_nanf("");
     }
-    pl.ids[t][lane] = c.id;
+    pl.ids[t][lane] = id;
     pl.wts[t][lane] = wgt;
     pl.pgs[t][lane] = pg;
-    if (rs.ids_out) rs.ids_out[t * k + lane] = uint16_t(c.id);
+    if (rs.ids_out) rs.ids_out[t * k + lane] = uint16_t(id);
     if (rs.weights_out) rs.weights_out[t * k + lane] = wgt;
   }
 }

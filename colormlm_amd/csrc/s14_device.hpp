@@ -96,7 +96,7 @@ constexpr uint32_t kSyncStatusLine = kSyncLines - 1;  // the status word's line
 inline uint32_t *status_word(const Workspace &ws) { return ws.sync + kSyncStatusLine * kRouteCounterStride; }
 // Status bits a launch leaves in the status line of ws.sync (sticky until
 // read by s14_launch_status).
-enum : uint32_t { kStatusNullPage = 1u, kStatusWaitTimeout = 2u };
+enum : uint32_t { kStatusNullPage = 1u, kStatusBadRoute = 2u };
 
 // Layout of the workspace in one device allocation (each region 256-byte
 // aligned): table | h | scores | biased | route counters | h windows.
@@ -154,6 +154,9 @@ struct RouterArgs {
   uint32_t topk;
   int score_fn;
   float route_scale;
+  const int64_t *tid2eid;  // hash routing: [vocab][topk] expert rows; NULL: biased top-k
+  uint32_t vocab;
+  const int32_t *token_ids;  // [tokens] (hash routing)
 };
 
 // Where a device-routed launch finds its pages and reports its routes.

@@ -329,5 +329,68 @@ __device__ __forceinline__ float route_weight(const TopK &c, float route_scale) 
   return w;
 }
 
+// Scores and pages held in LDS.
+struct LdsScoreLoad {
+  const float *scores;
+  const uint64_t *pages;
+  __device__ float s(uint32_t e) const { return scores[e]; }
+  __device__ uint64_t p(uint32_t e) const { return pages ? pages[e] : 0ull; }
+};
+
+// Hash route of token t (the reference's layers 0-2, executor.py:643-667),
+// computed by one whole wavefront: lane j < k takes expert
+// tid2eid[token_ids[t]][j] (row order is route order), its unbiased score
+// and page through `ld`; the sum of the k scores is sequential in row order,
+// as for the top-k.  `bad` (uniform): the token id is outside [0, vocab), or
+// an entry is outside [0, n_experts) or repeats an earlier one (the
+// executor's ContractError cases); such lanes then hold expert 0.
+template <class Load>
+__device__ __forceinline__ TopK select_hash_from(const Load &ld, const RouterArgs &r, uint32_t t, bool &bad) {
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t k = r.topk;
+  const int32_t tok = r.token_ids[t];
+  const bool tok_ok = tok >= 0 && uint32_t(tok) < r.vocab;
+  int64_t e = -1;
+  if (lane < k && tok_ok) e = r.tid2eid[size_t(tok) * k + lane];
+  const bool in_range = e >= 0 && e < int64_t(r.n_experts);
+  const uint32_t id = in_range ? uint32_t(e) : 0u;
+  bool dup = false;
+#pragma unroll
+  for (uint32_t j = 0; j < uint32_t(kTopK); ++j) {
+    const uint32_t other = uint32_t(__builtin_amdgcn_readlane(int(id), int(j)));
+    dup = dup || (j < lane && j < k && other == id);
+  }
+  bad = __ballot(lane < k && (!tok_ok || !in_range || dup)) != 0ull;
+  TopK mine{id, 0.0f, 0ull, 0.0f};
+  if (lane < k) {
+    mine.s = ld.s(id);
+    mine.page = ld.p(id);
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (uint32_t i = 0; i < uint32_t(kTopK); ++i) {
+    if (i >= k) break;
+    sum = __fadd_rn(sum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine.s), int(i))));
+  }
+  mine.sum = sum;
+  return mine;
+}
+
+// The weight checks of RouteDecision::validate_for (runner.rs:128-180) on a
+// device route, lane j < k holding weight j: every weight finite and >= 0,
+// and their f32 sum, sequential in route order from 0, within 1e-4 of
+// route_scale (the reference's 1.5).  Uniform result.
+__device__ __forceinline__ bool route_weights_valid(float w, uint32_t k, float route_scale) {
+  const uint32_t lane = threadIdx.x & 63;
+  const bool lane_ok = lane >= k || (__builtin_isfinite(w) && w >= 0.0f);
+  float sum = 0.0f;
+#pragma unroll
+  for (uint32_t i = 0; i < uint32_t(kTopK); ++i) {
+    if (i >= k) break;
+    sum = __fadd_rn(sum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), int(i))));
+  }
+  return __ballot(!lane_ok) == 0ull && fabsf(__fsub_rn(sum, route_scale)) <= 1e-4f;
+}
+
 }  // namespace
 }  // namespace s14

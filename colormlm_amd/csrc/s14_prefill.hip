@@ -126,19 +126,27 @@ __global__ __launch_bounds__(256) void k_prefill_topk(PrefillArgs a, PrefillWork
   const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
   if (t >= a.tokens) return;
   const uint32_t k = a.r.topk;
-  const TopK c = select_topk(ws.biased + size_t(t) * kMaxExperts, ws.scores + size_t(t) * kMaxExperts, nullptr,
-                             a.r.n_experts, k);
+  const float *bt = ws.biased + size_t(t) * kMaxExperts, *st = ws.scores + size_t(t) * kMaxExperts;
+  bool bad = false;
+  const TopK c = a.r.tid2eid ? select_hash_from(PlainScoreLoad{bt, st, nullptr}, a.r, t, bad)
+                             : select_topk(bt, st, nullptr, a.r.n_experts, k);
+  float w = lane < k ? route_weight(c, a.r.route_scale) : 0.0f;
+  bad = bad || !route_weights_valid(w, k, a.r.route_scale);
+  if (bad && lane == 0) __hip_atomic_fetch_or(a.status, kStatusBadRoute, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (lane < k) {
-    const float w = route_weight(c, a.r.route_scale);
+    // a route that fails validate_for takes distinct placeholder experts
+    // with NaN weights
+    const uint32_t id = bad ? lane : c.id;
+    if (bad) w = __builtin_nanf("");
     // the pairs of an expert without a resident page combine with a NaN
     // weight (their GEMM tiles read the shared page instead)
-    const bool resident = a.expert_pages[c.id] != 0ull;
+    const bool resident = a.expert_pages[id] != 0ull;
     if (!resident) __hip_atomic_fetch_or(a.status, kStatusNullPage, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    ws.ids[t * kTopK + lane] = c.id;
+    ws.ids[t * kTopK + lane] = id;
     ws.weights[t * kTopK + lane] = resident ? w : __builtin_nanf("");
-    if (a.ids_out) a.ids_out[t * k + lane] = uint16_t(c.id);
+    if (a.ids_out) a.ids_out[t * k + lane] = uint16_t(id);
     if (a.weights_out) a.weights_out[t * k + lane] = w;
-    atomicOr(&ws.token_bits[c.id * kPrefillBitWords + (t >> 5)], 1u << (t & 31));
+    atomicOr(&ws.token_bits[id * kPrefillBitWords + (t >> 5)], 1u << (t & 31));
   }
 }
 

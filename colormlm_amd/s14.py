@@ -294,9 +294,13 @@ class Router:
     topk: int = N.TOP_K
     score_fn: int = N.S14_SCORE_SIGMOID
     route_scale: float = 1.0
+    tid2eid: object = None  # hash routing: device int64 [vocab, topk]
+    token_ids: object = None  # hash routing: device int32 [tokens]
 
     def c(self) -> N.Router:
-        return N.Router(_ptr(self.weight), _ptr(self.bias), self.n_experts, self.topk, self.score_fn, self.route_scale)
+        vocab = int(self.tid2eid.shape[0]) if self.tid2eid is not None else 0
+        return N.Router(_ptr(self.weight), _ptr(self.bias), self.n_experts, self.topk, self.score_fn, self.route_scale,
+                        _ptr(self.tid2eid), vocab, _ptr(self.token_ids))
 
 
 def expert_chain(ctx: Context, page, x, route_w: float, y, mode: int = EXACT, stream=None) -> None:

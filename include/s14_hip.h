@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define S14_ABI_VERSION 1
+#define S14_ABI_VERSION 2
 
 /* ---- status codes: one per anyhow::bail! category of the reference ---- */
 enum {
@@ -233,6 +233,16 @@ typedef struct {
   uint32_t topk;         /* 6 */
   int score_fn;          /* S14_SCORE_* */
   float route_scale;     /* 1.0 (BASELINE) or 1.5 (reference route_scale) */
+  /* Hash routing, the reference's layers 0-2 (executor.py:643-656,
+   * contract.rs:81-90): when tid2eid is not NULL, token t's experts are the
+   * row tid2eid[token_ids[t]] (device int64 [vocab][topk]) in row order
+   * instead of the biased top-k; the weights are still the chosen experts'
+   * scores renormalised (times route_scale).  A token id outside [0, vocab),
+   * an entry outside [0, n_experts) or a repeated entry fails that token's
+   * route (see s14_launch_status).  NULL tid2eid: score routing. */
+  const int64_t *tid2eid;
+  uint32_t vocab;
+  const int32_t *token_ids; /* device int32 [tokens] of the launch */
 } s14_router;
 
 /* Router + routed + shared for one token.  expert_pages: device array of
@@ -280,7 +290,12 @@ uint64_t s14_noalloc_scratch_bytes(void);
  * pinned page of the layer (lease it through s14_moe_pages_* and release it
  * only after the launch's compute fence).  A launch that finds a 0 entry
  * reads no memory through it, writes NaN for the affected outputs and leaves
- * a status that this call reports as S14_ERR_INVALID. */
+ * a status that this call reports as S14_ERR_INVALID.  Every routed
+ * launch also runs RouteDecision::validate_for's checks (runner.rs:128-180)
+ * on each token's device-chosen route: expert ids inside [0, n_experts) and
+ * distinct, weights finite and >= 0, their f32 sum within 1e-4 of
+ * route_scale.  A token whose route fails them gets NaN outputs and this
+ * call reports S14_ERR_ROUTE. */
 int s14_launch_status(s14_ctx *ctx);
 
 /* Router only (scores f32 [n_experts], ids u16 [topk], weights f32 [topk]). */

@@ -88,6 +88,8 @@ def _declare(L):
         "s14o_moe_layer": (None, [U32, U32, P, U32, P, P, P, P, P]),
         "s14o_router_logits": (None, [U32, U32, P, P, P]),
         "s14o_route": (None, [U32, U32, P, P, P, I, U32, F, P, P, P]),
+        "s14o_route_hash": (I, [U32, U32, P, P, P, P, I, U32, F, P, P, P]),
+        "s14o_route_valid": (I, [P, P, U32, U32, F]),
         "s14o_error_stats_compute": (None, [C.c_size_t, P, P, C.POINTER(ErrorStats)]),
         "s14o_requant_e4m3": (None, [U32, U32, U32, P, P, P]),
         "s14o_dequant_requant": (None, [U32, U32, U32, P, P, P]),
@@ -263,6 +265,28 @@ def route(wr, bias, x, score_fn=SCORE_SIGMOID, topk=6, route_scale=1.0):
     w = np.empty(topk, dtype=np.float32)
     lib().s14o_route(n, wr.shape[1], _p(wr), _p(bias), _p(x), score_fn, topk, float(route_scale), _p(scores), _p(ids), _p(w))
     return scores, ids, w
+
+
+def route_hash(wr, bias, x, row, score_fn=SCORE_SIGMOID, topk=6, route_scale=1.0):
+    """Hash route of one token from its tid2eid row (executor.py:643-667):
+    (scores, ids, weights), or (scores, None, None) when the row has an entry
+    outside [0, n_experts) or a repeated one."""
+    wr, bias, x = _f32(wr), _f32(bias), _f32(x)
+    row = np.ascontiguousarray(row, dtype=np.int64)
+    n = wr.shape[0]
+    scores = np.empty(n, dtype=np.float32)
+    ids = np.empty(topk, dtype=np.uint16)
+    w = np.empty(topk, dtype=np.float32)
+    bad = lib().s14o_route_hash(n, wr.shape[1], _p(wr), _p(bias), _p(x), _p(row), score_fn, topk,
+                                float(route_scale), _p(scores), _p(ids), _p(w))
+    return (scores, None, None) if bad else (scores, ids, w)
+
+
+def route_valid(ids, w, n_experts=256, route_scale=1.0) -> bool:
+    """RouteDecision::validate_for's id and weight checks (runner.rs:128-180)."""
+    ids = np.ascontiguousarray(ids, dtype=np.uint16)
+    w = _f32(w)
+    return bool(lib().s14o_route_valid(_p(ids), _p(w), ids.size, n_experts, float(route_scale)))
 
 
 def error_stats(actual, expected) -> dict:

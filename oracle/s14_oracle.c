@@ -289,11 +289,10 @@ void s14o_router_logits(uint32_t n_experts, uint32_t k, const float *wr,
 /* Score, biased top-k and weights.  BASELINE: sigmoid, weights renormalised
  * to 1.  Reference (executor.py:641-667): sqrt(softplus) with torch's
  * threshold-20 softplus, weights renormalised then scaled by 1.5. */
-void s14o_route(uint32_t n_experts, uint32_t k, const float *wr, const float *bias,
-                const float *x, int score_fn, uint32_t topk, float route_scale,
-                float *scores_out, uint16_t *ids_out, float *weights_out) {
-  float *z = (float *)malloc(sizeof(float) * n_experts * 2);
-  float *b = z + n_experts;
+/* Scores of every expert and, in b, the biased scores (executor.py:641-645). */
+static void router_scores(uint32_t n_experts, uint32_t k, const float *wr, const float *bias,
+                          const float *x, int score_fn, float *scores_out, float *b) {
+  float *z = (float *)malloc(sizeof(float) * n_experts);
   s14o_router_logits(n_experts, k, wr, x, z);
   for (uint32_t e = 0; e < n_experts; ++e) {
     float s;
@@ -306,6 +305,57 @@ void s14o_route(uint32_t n_experts, uint32_t k, const float *wr, const float *bi
     scores_out[e] = s;
     b[e] = s + bias[e];
   }
+  free(z);
+}
+
+/* Weights of a chosen route: s[id] / sum with the sum sequential in route
+ * order from 0, times route_scale if != 1 (executor.py:664-667). */
+static void route_weights(const float *scores, const uint16_t *ids, uint32_t topk, float route_scale,
+                          float *weights_out) {
+  float sum = 0.0f;
+  for (uint32_t i = 0; i < topk; ++i) sum += scores[ids[i]];
+  for (uint32_t i = 0; i < topk; ++i) {
+    float w = scores[ids[i]] / sum;
+    if (route_scale != 1.0f) w = w * route_scale;
+    weights_out[i] = w;
+  }
+}
+
+int s14o_route_hash(uint32_t n_experts, uint32_t k, const float *wr, const float *bias, const float *x,
+                    const int64_t *row, int score_fn, uint32_t topk, float route_scale, float *scores_out,
+                    uint16_t *ids_out, float *weights_out) {
+  float *b = (float *)malloc(sizeof(float) * n_experts);
+  router_scores(n_experts, k, wr, bias, x, score_fn, scores_out, b);
+  free(b);
+  int bad = 0;
+  for (uint32_t i = 0; i < topk; ++i) {
+    if (row[i] < 0 || row[i] >= (int64_t)n_experts) bad = 1;
+    for (uint32_t j = 0; j < i; ++j)
+      if (row[j] == row[i]) bad = 1;
+  }
+  if (bad) return 1;
+  for (uint32_t i = 0; i < topk; ++i) ids_out[i] = (uint16_t)row[i];
+  route_weights(scores_out, ids_out, topk, route_scale, weights_out);
+  return 0;
+}
+
+int s14o_route_valid(const uint16_t *ids, const float *w, uint32_t topk, uint32_t n_experts, float route_scale) {
+  float sum = 0.0f;
+  for (uint32_t i = 0; i < topk; ++i) {
+    if (ids[i] >= n_experts) return 0;
+    if (!isfinite(w[i]) || w[i] < 0.0f) return 0;
+    for (uint32_t j = 0; j < i; ++j)
+      if (ids[j] == ids[i]) return 0;
+    sum += w[i];
+  }
+  return fabsf(sum - route_scale) <= 1e-4f;
+}
+
+void s14o_route(uint32_t n_experts, uint32_t k, const float *wr, const float *bias,
+                const float *x, int score_fn, uint32_t topk, float route_scale,
+                float *scores_out, uint16_t *ids_out, float *weights_out) {
+  float *b = (float *)malloc(sizeof(float) * n_experts);
+  router_scores(n_experts, k, wr, bias, x, score_fn, scores_out, b);
   unsigned char taken[1024];
   memset(taken, 0, sizeof(taken));
   for (uint32_t i = 0; i < topk; ++i) {
@@ -317,14 +367,8 @@ void s14o_route(uint32_t n_experts, uint32_t k, const float *wr, const float *bi
     taken[best] = 1;
     ids_out[i] = (uint16_t)best;
   }
-  float sum = 0.0f;
-  for (uint32_t i = 0; i < topk; ++i) sum += scores_out[ids_out[i]];
-  for (uint32_t i = 0; i < topk; ++i) {
-    float w = scores_out[ids_out[i]] / sum;
-    if (route_scale != 1.0f) w = w * route_scale;
-    weights_out[i] = w;
-  }
-  free(z);
+  route_weights(scores_out, ids_out, topk, route_scale, weights_out);
+  free(b);
 }
 
 /* ------------------------------------------------------------------ */

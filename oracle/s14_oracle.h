@@ -113,6 +113,17 @@ void s14o_router_logits(uint32_t n_experts, uint32_t k, const float *wr,
                         const float *x, float *z);
 /* scores, top-k of (score + bias) with ties to the lower index, weights =
  * s[id]/sum (sum sequential in selection order) times route_scale if != 1. */
+/* Hash route (executor.py:643-667, the reference's layers 0-2): ids = the
+ * token's tid2eid row, in row order; weights as for s14o_route.  Returns 0,
+ * or 1 (outputs other than the scores untouched) when an entry is outside
+ * [0, n_experts) or repeats an earlier one (the executor's ContractError). */
+int s14o_route_hash(uint32_t n_experts, uint32_t k, const float *wr, const float *bias, const float *x,
+                    const int64_t *row, int score_fn, uint32_t topk, float route_scale, float *scores_out,
+                    uint16_t *ids_out, float *weights_out);
+/* RouteDecision::validate_for's route checks (runner.rs:128-180): ids in
+ * range and distinct, weights finite and >= 0, f32 sum (sequential) within
+ * 1e-4 of route_scale (the reference's 1.5).  1 = valid. */
+int s14o_route_valid(const uint16_t *ids, const float *w, uint32_t topk, uint32_t n_experts, float route_scale);
 void s14o_route(uint32_t n_experts, uint32_t k, const float *wr, const float *bias,
                 const float *x, int score_fn, uint32_t topk, float route_scale,
                 float *scores_out, uint16_t *ids_out, float *weights_out);

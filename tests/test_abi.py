@@ -30,7 +30,7 @@ def test_binding_covers_the_header():
 
 
 def test_abi_version_and_error_channel(native):
-    assert native.s14_abi_version() == 1
+    assert native.s14_abi_version() == 2
     rc = native.s14_shape_validate_mxfp4(N.Shape(0, 128), None)
     assert rc == N.S14_ERR_SHAPE
     assert "non-zero" in N.last_error()

@@ -812,3 +812,93 @@ def test_nonresident_page_is_reported_not_read(ctx, oracle, bank, prefill_router
     s14.moe_layer_route(ctx, router, bank["table"], shared, dev(xs[0]), y, mode=s14.EXACT)
     ctx.launch_status()
     assert not np.isnan(host(y)).any()
+
+
+def _tid2eid(vocab: int = 1000, seed: int = 5) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    return np.stack([rng.choice(256, 6, replace=False) for _ in range(vocab)]).astype(np.int64)
+
+
+@pytest.mark.parametrize("score_fn,scale", [(N.S14_SCORE_SIGMOID, 1.0), (N.S14_SCORE_SQRT_SOFTPLUS, 1.5)])
+def test_hash_router_layer_block_prefill(ctx, oracle, bank, score_fn, scale):
+    """Hash routing (the reference's layers 0-2: experts from tid2eid[token],
+    weights from the chosen scores, executor.py:643-667) through the one-token
+    layer (exact and fast), a block of 4, the route-only entry point and a
+    prefill of 4, against the oracle's hash route and layer.  With the
+    sqrt-softplus score the device's log1pf is not glibc's (the scores agree
+    to 1e-6 relative), so there the layers are checked bit for bit against
+    the oracle layer evaluated with the device's own route weights."""
+    say(f"hash router score_fn={score_fn} scale={scale}")
+    tab_h = _tid2eid()
+    tab_d = torch.from_numpy(tab_h).cuda()
+    tok = np.array([17, 999, 0, 523], np.int32)
+    xs = synth.block_tokens(seed=31, tokens=4)
+    router = s14.Router(bank["wr_d"], bank["bias_d"], score_fn=score_fn, route_scale=scale, tid2eid=tab_d,
+                        token_ids=dev(tok))
+    shared = page_host(bank, 256)
+    want, routes = [], []
+    for t in range(4):
+        sc, i_o, w_o = oracle.route_hash(bank["wr"], bank["bias"], xs[t], tab_h[tok[t]], score_fn=score_fn,
+                                         route_scale=scale)
+        assert i_o.tolist() == tab_h[tok[t]].tolist()
+        routes.append((i_o, w_o))
+        want.append(oracle.moe_layer(xs[t], [page_host(bank, int(e)) for e in i_o], w_o, shared))
+    exact_scores = score_fn == N.S14_SCORE_SIGMOID
+    # route only
+    ids = torch.empty((4, 6), dtype=torch.int16, device="cuda")
+    wts = torch.empty((4, 6), dtype=torch.float32, device="cuda")
+    s14.route(ctx, router, 4, dev(xs), ids_out=ids, weights_out=wts)
+    ids_h, wts_h = host(ids).astype(np.uint16), host(wts)
+    for t in range(4):
+        assert ids_h[t].tolist() == routes[t][0].tolist()
+        if exact_scores:
+            assert_bit_exact(wts_h[t], routes[t][1], f"hash weights t={t}")
+        else:
+            np.testing.assert_allclose(wts_h[t], routes[t][1], rtol=1e-6)
+            routes[t] = (routes[t][0], wts_h[t])
+            want[t] = oracle.moe_layer(xs[t], [page_host(bank, int(e)) for e in routes[t][0]], wts_h[t], shared)
+    # one token (exact, then fast) and a block of 4 (exact)
+    y = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    s14.moe_layer_route(ctx, router, bank["table"], bank["pages"][256], dev(xs[0]), y, mode=s14.EXACT)
+    assert_bit_exact(host(y), want[0], "hash layer exact")
+    s14.moe_layer_route(ctx, router, bank["table"], bank["pages"][256], dev(xs[0]), y, mode=s14.FAST)
+    st = oracle.error_stats(host(y), want[0])
+    assert st["max_abs"] <= 1e-3 and st["rmse"] <= 1.5e-4, st
+    yb = torch.empty((4, HIDDEN), dtype=torch.float32, device="cuda")
+    s14.moe_block_route(ctx, 4, router, bank["table"], bank["pages"][256], dev(xs), yb, mode=s14.EXACT)
+    got = host(yb)
+    for t in range(4):
+        assert_bit_exact(got[t], want[t], f"hash block t={t}")
+    # prefill of the same 4 tokens: routes bit for bit, outputs within the prefill's relative gate
+    yp = torch.empty((4, HIDDEN), dtype=torch.float32, device="cuda")
+    pids = torch.empty((4, 6), dtype=torch.int16, device="cuda")
+    s14.moe_prefill(ctx, 4, router, bank["table"], bank["pages"][256], dev(xs), yp, ids_out=pids)
+    assert (host(pids).astype(np.uint16) == np.stack([r[0] for r in routes])).all()
+    gp = host(yp)
+    for t in range(4):
+        wp = oracle.moe_prefill_token(xs[t], [page_host(bank, int(e)) for e in routes[t][0]], routes[t][1], shared)
+        assert np.max(np.abs(gp[t] - wp)) <= 0.02 * np.max(np.abs(wp))
+    ctx.launch_status()  # every route passed validate_for
+
+
+def test_hash_router_bad_row_poisons_only_its_token(ctx, oracle, bank):
+    """A tid2eid row with a repeated expert, and a token id past the table:
+    those tokens' outputs are NaN and s14_launch_status reports
+    S14_ERR_ROUTE; the other tokens of the block are exact."""
+    tab_h = _tid2eid()
+    tab_h[999] = [5, 9, 5, 200, 31, 77]  # repeated expert
+    tok = np.array([17, 999, 0, 5000], np.int32)  # 5000 is past the 1000-row table
+    xs = synth.block_tokens(seed=33, tokens=4)
+    router = s14.Router(bank["wr_d"], bank["bias_d"], tid2eid=torch.from_numpy(tab_h).cuda(), token_ids=dev(tok))
+    ctx.launch_status()
+    yb = torch.empty((4, HIDDEN), dtype=torch.float32, device="cuda")
+    s14.moe_block_route(ctx, 4, router, bank["table"], bank["pages"][256], dev(xs), yb, mode=s14.EXACT)
+    got = host(yb)
+    shared = page_host(bank, 256)
+    for t in (0, 2):
+        _, i_o, w_o = oracle.route_hash(bank["wr"], bank["bias"], xs[t], tab_h[tok[t]])
+        assert_bit_exact(got[t], oracle.moe_layer(xs[t], [page_host(bank, int(e)) for e in i_o], w_o, shared), f"t={t}")
+    assert np.isnan(got[1]).all() and np.isnan(got[3]).all()
+    with pytest.raises(s14.S14Error) as err:
+        ctx.launch_status()
+    assert err.value.code == N.S14_ERR_ROUTE
