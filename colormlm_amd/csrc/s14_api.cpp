@@ -465,8 +465,16 @@ int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, con
                      ids_out,              weights_out, status_word(ws)};
   hipError_t e = launch_route(st, ws, rs, x, ev ? ev[kStageRoute] : KernelEvents{});
   if (e != hipSuccess) return hip_fail(e, "router launch");
-  e = launch_phase1(st, ws, nullptr, tokens * (kTopK + 1), tokens, mx, f8, x, mode,
-                    ev ? ev[kStagePhase1] : KernelEvents{});
+  const uint32_t n_pairs = tokens * (kTopK + 1);
+  if (tokens > 1 && mode == S14_MODE_EXACT) {
+    // blocks: one row per lane (enough (token, expert) chains to fill the GPU)
+    e = launch_block_phase1(st, ws, n_pairs, mx, f8, x, ev ? ev[kStagePhase1] : KernelEvents{});
+    if (e != hipSuccess) return hip_fail(e, "phase 1 launch");
+    e = launch_block_phase2(st, ws, tokens, mx, f8, y, ev ? ev[kStagePhase2] : KernelEvents{});
+    if (e != hipSuccess) return hip_fail(e, "phase 2 launch");
+    return S14_OK;
+  }
+  e = launch_phase1(st, ws, nullptr, n_pairs, tokens, mx, f8, x, mode, ev ? ev[kStagePhase1] : KernelEvents{});
   if (e != hipSuccess) return hip_fail(e, "phase 1 launch");
   e = launch_phase2(st, ws, tokens, mx, f8, y, mode, ev ? ev[kStagePhase2] : KernelEvents{});
   if (e != hipSuccess) return hip_fail(e, "phase 2 launch");

@@ -89,6 +89,7 @@ struct Workspace {
   // kSyncLines lines of kRouteCounterStride words: the status word (kStatus*
   // bits) that launches leave for s14_launch_status.
   uint32_t *sync;
+  float *down;  // [kMaxPairs][kHidden]: each pair's w2 output of a block launch (before its route weight)
   size_t bytes;
 };
 constexpr uint32_t kSyncLines = 1;
@@ -101,7 +102,7 @@ enum : uint32_t { kStatusNullPage = 1u, kStatusBadRoute = 2u };
 // Layout of the workspace in one device allocation (each region 256-byte
 // aligned): table | h | scores | biased | route counters | h windows.
 struct WorkspaceLayout {
-  size_t table, h, scores, biased, count, hwin, sync, bytes;
+  size_t table, h, scores, biased, count, hwin, sync, down, bytes;
 };
 constexpr size_t ws_align(size_t v) { return (v + 255) / 256 * 256; }
 constexpr WorkspaceLayout workspace_layout() {
@@ -121,6 +122,8 @@ constexpr WorkspaceLayout workspace_layout() {
   off = ws_align(off + sizeof(uint32_t) * kMaxPairs * (kInter / kP1ExactRows));
   l.sync = off;
   off = ws_align(off + sizeof(uint32_t) * kSyncLines * kRouteCounterStride);
+  l.down = off;
+  off = ws_align(off + sizeof(float) * kMaxPairs * kHidden);
   l.bytes = off;
   return l;
 }
@@ -139,6 +142,7 @@ inline Workspace workspace_carve(void *base) {
   ws.route_count = reinterpret_cast<uint32_t *>(b + l.count);
   ws.hwin = reinterpret_cast<uint32_t *>(b + l.hwin);
   ws.sync = reinterpret_cast<uint32_t *>(b + l.sync);
+  ws.down = reinterpret_cast<float *>(b + l.down);
   ws.bytes = l.bytes;
   return ws;
 }
@@ -213,6 +217,13 @@ hipError_t launch_route(hipStream_t s, const Workspace &ws, const RouteSpec &rs,
 hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *host_plan,
                          uint32_t n_pairs, uint32_t tokens, const PageOffsets &mx,
                          const PageOffsets &fp8, const float *x, int mode, KernelEvents ev = {});
+// Blocks of 2..8 tokens in EXACT order, one row per lane (s14_block.hip):
+// phase 1 of every pair of the table the route kernel wrote, and phase 2 of
+// every token with its route-order accumulation into y [tokens][hidden].
+hipError_t launch_block_phase1(hipStream_t s, const Workspace &ws, uint32_t n_pairs, const PageOffsets &mx,
+                               const PageOffsets &fp8, const float *x, KernelEvents ev = {});
+hipError_t launch_block_phase2(hipStream_t s, const Workspace &ws, uint32_t tokens, const PageOffsets &mx,
+                               const PageOffsets &fp8, float *y, KernelEvents ev = {});
 // w2 of every pair and the per-token accumulation into y [tokens][hidden].
 hipError_t launch_phase2(hipStream_t s, const Workspace &ws, uint32_t tokens,
                          const PageOffsets &mx, const PageOffsets &fp8, float *y, int mode,
