@@ -40,6 +40,7 @@ ERROR_NAMES = {
 
 S14_MODE_EXACT = 0
 S14_MODE_FAST = 1
+S14_MODE_OFFICIAL = 2
 S14_X_F32 = 0
 S14_X_BF16 = 1
 S14_SCALE_UE8M0 = 0

@@ -336,8 +336,10 @@ extern "C" int s14_fill_mxfp4_page(s14_ctx *ctx, void *stream, uint8_t *page, ui
 
 namespace {
 
+// Fused expert entry points also take the official expert semantics.
 int check_mode(int mode) {
-  if (mode != S14_MODE_EXACT && mode != S14_MODE_FAST) return fail(S14_ERR_INVALID, "unknown mode %d", mode);
+  if (mode != S14_MODE_EXACT && mode != S14_MODE_FAST && mode != S14_MODE_OFFICIAL)
+    return fail(S14_ERR_INVALID, "unknown mode %d", mode);
   return S14_OK;
 }
 

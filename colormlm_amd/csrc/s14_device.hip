@@ -569,6 +569,7 @@ __device__ __forceinline__ void plan_publish(const RouteSpec &rs, PairTable *tab
     tab->page[rank] = pg;
     tab->fmt[rank] = S14_PAGE_MXFP4;
     tab->token[rank] = mt;
+    tab->weight[rank] = pl.wts[mt][mr];
     tab->slot_pair[mt][mr] = rank;
     tab->slot_page[mt][mr] = pg;
     tab->slot_fmt[mt][mr] = S14_PAGE_MXFP4;
@@ -582,6 +583,7 @@ __device__ __forceinline__ void plan_publish(const RouteSpec &rs, PairTable *tab
     tab->page[sp] = pg;
     tab->fmt[sp] = uint32_t(rs.shared_fmt);
     tab->token[sp] = lane;
+    tab->weight[sp] = 1.0f;
     tab->slot_pair[lane][k] = sp;
     tab->slot_page[lane][k] = pg;
     tab->slot_fmt[lane][k] = uint32_t(rs.shared_fmt);
@@ -690,6 +692,7 @@ struct PairRef {
   const uint8_t *page;
   uint32_t fmt;
   uint32_t token;
+  float weight;
 };
 
 template <bool kHostPlan>
@@ -700,9 +703,9 @@ __device__ __forceinline__ PairRef phase1_pair(const PairTable &plan, PairTable 
       uint32_t *dst = reinterpret_cast<uint32_t *>(tab);
       for (uint32_t i = threadIdx.x; i < sizeof(PairTable) / 4; i += blockDim.x) dst[i] = src[i];
     }
-    return PairRef{reinterpret_cast<const uint8_t *>(plan.page[p]), plan.fmt[p], plan.token[p]};
+    return PairRef{reinterpret_cast<const uint8_t *>(plan.page[p]), plan.fmt[p], plan.token[p], plan.weight[p]};
   }
-  return PairRef{reinterpret_cast<const uint8_t *>(tab->page[p]), tab->fmt[p], tab->token[p]};
+  return PairRef{reinterpret_cast<const uint8_t *>(tab->page[p]), tab->fmt[p], tab->token[p], tab->weight[p]};
 }
 
 __device__ __forceinline__ uint32_t page_bytes(uint32_t fmt) {
@@ -716,7 +719,7 @@ __device__ __forceinline__ uint32_t page_bytes(uint32_t fmt) {
 // kTier (1: single-token launch, 8: block launch) names the instantiation,
 // so traces and profiles keep the two workloads apart, and picks the code
 // check (per row at batch 1, per batch of groups for blocks).
-template <bool kHostPlan, int kTier>
+template <bool kHostPlan, int kTier, bool kOfficial>
 __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable plan, Workspace ws,
                                                                      const float *__restrict__ X, PageOffsets mx,
                                                                      PageOffsets f8) {
@@ -743,24 +746,34 @@ __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable p
       // batch 1 (one wavefront per SIMD, issue-bound): one code check per row
       RowCodes<kHidden / 32> rc;
       load_row_codes<kHidden / 32>(rc, src, soff);
-      const CodeWindow win = stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
+      CodeWindow win = stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
+      if constexpr (kOfficial) win = requant128_block<64 * kP1ExactWaves>(xs, kHidden, red);
       acc = mx_row_pair_fixed<kPF, kHidden / 32>(0.0f, ba, src, woff, soff, xs + 16 * h, win, rc);
     } else {
       // blocks: per-batch code checks measured faster here
-      const CodeWindow win = stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
+      CodeWindow win = stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
+      if constexpr (kOfficial) win = requant128_block<64 * kP1ExactWaves>(xs, kHidden, red);
       acc = mx_row_pair_fixed<kPF, kHidden / 32>(0.0f, ba, src, woff, soff, xs + 16 * h, win);
     }
   } else {
     const uint32_t woff = uint32_t(upper ? f8.w3 : f8.w1) + row * kHidden + 16u * h;
     const uint32_t soff = uint32_t(upper ? f8.s3 : f8.s1) + (row / 128) * (kHidden / 128);
     stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
+    if constexpr (kOfficial) requant128_block<64 * kP1ExactWaves>(xs, kHidden, red);
     acc = fp8_row_pair(0.0f, src, woff, soff, 0, kHidden / 32, xs + 16 * h);
   }
   const float other = __shfl_xor(acc, 32);
   const bool writer = !upper && h == 0;
   int lo = 255, hi = 0;
   if (writer) {
-    const float hv = swiglu_exact(acc, other, exptab);
+    float hv;
+    if constexpr (kOfficial) {
+      // g and u rounded to bf16; h = bf16(swiglu(g, u) * w), the route weight
+      // before w2 (1 for the shared expert) (executor.py:717-731)
+      hv = bf16_round(__fmul_rn(swiglu_exact(bf16_round(acc), bf16_round(other), exptab), pr.weight));
+    } else {
+      hv = swiglu_exact(acc, other, exptab);
+    }
     ws.h[size_t(p) * kInter + row] = hv;
     exp_range_acc(hv, lo, hi);
   }
@@ -860,13 +873,19 @@ __device__ __forceinline__ SlotInfo load_slot_info(const PairTable *__restrict__
 // acc = 0; acc += w * down (routed, route order); acc += down (shared) — or
 // y = w * down for the single-expert chain (s14_vulkan_numeric.rs:929-946,
 // :1300).  Called by one whole wavefront.
-template <int ROWS>
+template <int ROWS, bool kOfficial = false>
 __device__ __forceinline__ void phase2_accumulate(const SlotInfo &si, const float (*part)[ROWS], uint32_t t,
                                                   uint32_t row0, float *__restrict__ Y) {
   const uint32_t lane = threadIdx.x & 63;
   const bool row_lane = lane < uint32_t(ROWS);
   float acc = 0.0f;
-  if (si.chain) {
+  if constexpr (kOfficial) {
+    // official semantics: each slot's bf16 output already carries its route
+    // weight; acc = 0; acc += out_j in route order, shared last; y =
+    // bf16(acc) (executor.py:712-739)
+    for (uint32_t j = 0; j < si.np; ++j) acc = __fadd_rn(acc, row_lane ? part[j][lane] : 0.0f);
+    acc = bf16_round(acc);
+  } else if (si.chain) {
     const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(si.w), 0));
     acc = __fmul_rn(w, row_lane ? part[0][lane] : 0.0f);
   } else {
@@ -886,7 +905,7 @@ __device__ __forceinline__ void phase2_accumulate(const SlotInfo &si, const floa
 // LDS (row stride padded so the two slots' reads fall in different banks).
 constexpr int kHStride = kInter + 8;
 
-template <int kTier>
+template <int kTier, bool kOfficial>
 __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairTable *__restrict__ tab,
                                                                      const float *__restrict__ H,
                                                                      const uint32_t *__restrict__ hwin,
@@ -931,16 +950,24 @@ __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairT
     const float *const srch[2] = {H + size_t(pa) * kInter, H + size_t(pb) * kInter};
     StageRegs<kInter, 2> hr;
     stage_load_wave<kInter, 2>(hr, srch);
-    win[0] = h_window(hwin + size_t(pa) * kP1Tiles);
-    win[1] = h_window(hwin + size_t(pb) * kP1Tiles);
+    if constexpr (!kOfficial) {
+      win[0] = h_window(hwin + size_t(pa) * kP1Tiles);
+      win[1] = h_window(hwin + size_t(pb) * kP1Tiles);
+    }
     stage_store_wave<kInter, 2>(dst, hr);
+    if constexpr (kOfficial) {
+      // act_quant of each slot's h before w2 (this wavefront's own copies)
+      win[0] = requant128_wave(hs[sa], kInter);
+      win[1] = requant128_wave(hs[sb], kInter);
+    }
   } else if (has_a) {
     float *const dst[1] = {hs[sa]};
     const float *const srch[1] = {H + size_t(pa) * kInter};
     StageRegs<kInter, 1> hr;
     stage_load_wave<kInter, 1>(hr, srch);
-    win[0] = win[1] = h_window(hwin + size_t(pa) * kP1Tiles);
+    if constexpr (!kOfficial) win[0] = win[1] = h_window(hwin + size_t(pa) * kP1Tiles);
     stage_store_wave<kInter, 1>(dst, hr);
+    if constexpr (kOfficial) win[0] = win[1] = requant128_wave(hs[sa], kInter);
   }
   __syncthreads();
   if (has_a) {
@@ -956,10 +983,11 @@ __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairT
       acc = fp8_row_pair(0.0f, src, uint32_t(f8.w2) + row * kInter + 16u * h,
                          uint32_t(f8.s2) + (row / 128) * (kInter / 128), 0, kInter / 32, xh);
     }
+    if constexpr (kOfficial) acc = bf16_round(acc);  // w2's output rounded to bf16
     if (h == 0 && (!hi || has_b)) part[slot][r] = acc;
   }
   __syncthreads();
-  if (wave == 0) phase2_accumulate<kP2ExactRows>(si, part, t, blockIdx.x * kP2ExactRows, Y);
+  if (wave == 0) phase2_accumulate<kP2ExactRows, kOfficial>(si, part, t, blockIdx.x * kP2ExactRows, Y);
 }
 
 // Phase 2 FAST: wavefront j computes kP2FastRows w2 rows of the token's j-th
@@ -1144,12 +1172,21 @@ void phase1_tier(hipStream_t s, const Workspace &ws, const PairTable *host_plan,
                             mx, fp8);
   } else {
     const dim3 grid(kInter / (kP1ExactRows * kP1ExactWaves), n_pairs);
-    if (host_plan)
-      hipExtLaunchKernelGGL(k_phase1_exact<true, kTier>, grid, dim3(64 * kP1ExactWaves), 0, s, ev.start, ev.stop, 0,
-                            plan, ws, x, mx, fp8);
-    else
-      hipExtLaunchKernelGGL(k_phase1_exact<false, kTier>, grid, dim3(64 * kP1ExactWaves), 0, s, ev.start, ev.stop, 0,
-                            plan, ws, x, mx, fp8);
+    const dim3 blk(64 * kP1ExactWaves);
+    if (mode == S14_MODE_OFFICIAL) {
+      if (host_plan)
+        hipExtLaunchKernelGGL(k_phase1_exact<true, kTier, true>, grid, blk, 0, s, ev.start, ev.stop, 0, plan, ws, x, mx,
+                              fp8);
+      else
+        hipExtLaunchKernelGGL(k_phase1_exact<false, kTier, true>, grid, blk, 0, s, ev.start, ev.stop, 0, plan, ws, x,
+                              mx, fp8);
+    } else if (host_plan) {
+      hipExtLaunchKernelGGL(k_phase1_exact<true, kTier, false>, grid, blk, 0, s, ev.start, ev.stop, 0, plan, ws, x, mx,
+                            fp8);
+    } else {
+      hipExtLaunchKernelGGL(k_phase1_exact<false, kTier, false>, grid, blk, 0, s, ev.start, ev.stop, 0, plan, ws, x,
+                            mx, fp8);
+    }
   }
 }
 
@@ -1161,9 +1198,12 @@ void phase2_tier(hipStream_t s, const Workspace &ws, uint32_t tokens, const Page
   if (mode == S14_MODE_FAST)
     hipExtLaunchKernelGGL(k_phase2_fast<kTier>, dim3(kHidden / kP2FastRows, tokens), dim3(64 * kP2FastWaves), 0, s,
                           ev.start, ev.stop, 0, tab, h, y, mx, fp8);
+  else if (mode == S14_MODE_OFFICIAL)
+    hipExtLaunchKernelGGL(k_phase2_exact<kTier, true>, dim3(kHidden / kP2ExactRows, tokens), dim3(64 * kP2ExactWaves),
+                          0, s, ev.start, ev.stop, 0, tab, h, ws.hwin, y, mx, fp8);
   else
-    hipExtLaunchKernelGGL(k_phase2_exact<kTier>, dim3(kHidden / kP2ExactRows, tokens), dim3(64 * kP2ExactWaves), 0,
-                          s, ev.start, ev.stop, 0, tab, h, ws.hwin, y, mx, fp8);
+    hipExtLaunchKernelGGL(k_phase2_exact<kTier, false>, dim3(kHidden / kP2ExactRows, tokens), dim3(64 * kP2ExactWaves),
+                          0, s, ev.start, ev.stop, 0, tab, h, ws.hwin, y, mx, fp8);
 }
 }  // namespace
 

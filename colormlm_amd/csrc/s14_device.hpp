@@ -55,6 +55,7 @@ struct PairTable {
   uint64_t page[kMaxPairs];
   uint32_t fmt[kMaxPairs];
   uint32_t token[kMaxPairs];
+  float weight[kMaxPairs];  // route weight (1 for the shared expert): official mode applies it in phase 1
   // per token and slot (phase 2)
   uint32_t npairs[kMaxTokens];
   uint32_t slot_pair[kMaxTokens][kSlots];  // pair index: row of the h buffer
@@ -71,6 +72,7 @@ inline void plan_pair(PairTable &t, uint32_t p, const void *page, uint32_t fmt, 
   t.page[p] = reinterpret_cast<uint64_t>(page);
   t.fmt[p] = fmt;
   t.token[p] = token;
+  t.weight[p] = shared ? 1.0f : weight;
   t.slot_pair[token][j] = p;
   t.slot_page[token][j] = reinterpret_cast<uint64_t>(page);
   t.slot_fmt[token][j] = fmt;

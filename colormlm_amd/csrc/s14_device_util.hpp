@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include "s14_device.hpp"
+#include "s14_e4m3.h"
 #include "s14_expf.h"
 
 namespace s14 {
@@ -98,6 +99,28 @@ __device__ __forceinline__ float e4m3_f32(uint32_t code) {
 }
 
 __device__ __forceinline__ float bf16_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// v rounded to bf16 (ties to even; a NaN stays a quiet NaN), as an f32: the
+// rounding of torch's .to(bfloat16) that the official expert semantics apply
+// to every linear output (executor.py:717-727).
+__device__ __forceinline__ float bf16_round(float v) {
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return __uint_as_float((u | 0x00400000u) & 0xffff0000u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return __uint_as_float(u & 0xffff0000u);
+}
+
+// E8M0 code of an activation-requant group: 127 + ceil(log2(max(amax, 1e-4)
+// / 448)) (l42_reference.py:390-403), the f32 quotient rounded to nearest,
+// ceil(log2) taken exactly from its bits.
+__device__ __forceinline__ uint32_t requant_code(float amax) {
+  if (amax < 1.0e-4f) amax = 1.0e-4f;
+  const float r = __fdiv_rn(amax, 448.0f);
+  const uint32_t u = __float_as_uint(r);
+  const int e = int((u >> 23) & 255u) - 127;  // r is normal: amax/448 >= 2.2e-7
+  const int c = (u & 0x7fffffu) ? e + 1 : e;  // ceil(log2 r)
+  return uint32_t(c + 127);
+}
 
 // expf's 32 table entries in LDS (see s14x::expf_glibc_with): filled by the
 // first 32 lanes of a wavefront, then a barrier before any use.

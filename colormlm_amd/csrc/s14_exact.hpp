@@ -526,6 +526,63 @@ __device__ __forceinline__ float fp8_row_pair(float acc, const Src &src, uint32_
   return from_odd(acc);
 }
 
+// ---------------------------------------------------------------------------
+// act_quant of the official expert semantics (l42_reference.py:390-403,
+// group 128): a vector in LDS is replaced, in place, by its requantised
+// values e4m3(v / s) * s with s = 2^(code-127) per 128 values, each exactly
+// representable in f32; the decode window of the result is returned.
+// ---------------------------------------------------------------------------
+
+// Groups g = first, first + stride, ... of v (128 values each), by one
+// wavefront, two values per lane; accumulates the exponent range.
+__device__ __forceinline__ void requant128_groups(float *v, int n_groups, int first, int stride, int &lo, int &hi) {
+  const uint32_t lane = threadIdx.x & 63;
+  for (int g = first; g < n_groups; g += stride) {
+    float2 *p = reinterpret_cast<float2 *>(v + 128 * g) + lane;
+    const float2 a = *p;
+    // amax over the group (NaN ignored, as the oracle's strict '>' scan does)
+    const float m = fmaxf(fabsf(a.x), fabsf(a.y));
+    const float amax = __uint_as_float(uint32_t(wave_max_i(int(__float_as_uint(m)))));  // m >= 0: bits order as values
+    const uint32_t code = requant_code(amax);
+    const float inv = __uint_as_float((254u - code) << 23), sc = __uint_as_float(code << 23);
+    const float qa = __fmul_rn(e4m3_f32(s14x::e4m3_rne_sat(__fmul_rn(a.x, inv))), sc);
+    const float qb = __fmul_rn(e4m3_f32(s14x::e4m3_rne_sat(__fmul_rn(a.y, inv))), sc);
+    *p = make_float2(qa, qb);
+    exp_range_acc(qa, lo, hi);
+    exp_range_acc(qb, lo, hi);
+  }
+}
+// A whole vector of n values (n % 128 == 0) by one wavefront.
+__device__ __forceinline__ CodeWindow requant128_wave(float *v, int n) {
+  int lo = 255, hi = 0;
+  requant128_groups(v, n / 128, 0, 1, lo, hi);
+  return mx_window(wave_min_i(lo), wave_max_i(hi));
+}
+// A whole vector by the W = NT / 64 wavefronts of a workgroup (groups
+// strided over the wavefronts), between two barriers; red: LDS scratch of
+// 2 W ints.  Every thread gets the window.
+template <int NT>
+__device__ __forceinline__ CodeWindow requant128_block(float *v, int n, int *red) {
+  constexpr int W = NT / 64;
+  const int wave = int(threadIdx.x >> 6);
+  __syncthreads();  // the staged vector is complete
+  int lo = 255, hi = 0;
+  requant128_groups(v, n / 128, wave, W, lo, hi);
+  lo = wave_min_i(lo);
+  hi = wave_max_i(hi);
+  if ((threadIdx.x & 63) == 0) {
+    red[2 * wave] = lo;
+    red[2 * wave + 1] = hi;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    lo = min(lo, red[2 * w]);
+    hi = max(hi, red[2 * w + 1]);
+  }
+  return mx_window(lo, hi);
+}
+
 // Groups per register batch in the fused exact kernels.  Larger batches hide
 // more load latency but inline a longer straight-line body; on the box 8
 // beat 16 by 10 % per layer (instruction supply) and 4 (batch overhead).

@@ -48,17 +48,6 @@ constexpr uint32_t kQGroup = 32;  // requant group (k values per E8M0 scale)
 // requant (bit-identical to the oracle's s14o_requant_e4m3)
 // ---------------------------------------------------------------------------
 
-// E8M0 code of a group: 127 + ceil(log2(max(amax, 1e-4) / 448)), the f32
-// quotient rounded to nearest, ceil(log2) taken exactly from its bits.
-__device__ __forceinline__ uint32_t requant_code(float amax) {
-  if (amax < 1.0e-4f) amax = 1.0e-4f;
-  const float r = __fdiv_rn(amax, 448.0f);
-  const uint32_t u = __float_as_uint(r);
-  const int e = int((u >> 23) & 255u) - 127;  // r is normal: amax/448 >= 2.2e-7
-  const int c = (u & 0x7fffffu) ? e + 1 : e;  // ceil(log2 r)
-  return uint32_t(c + 127);
-}
-
 using s14x::e4m3_rne_sat;  // s14_e4m3.h: straight-line, checked against the oracle on the CPU
 
 // X [T, 4096] f32 -> Q [T, 4096] e4m3 in MFMA order + S [T, 128] E8M0.

@@ -27,6 +27,7 @@ from ._native import S14Error, check, lib
 
 EXACT = N.S14_MODE_EXACT
 FAST = N.S14_MODE_FAST
+OFFICIAL = N.S14_MODE_OFFICIAL  # fused expert entry points only
 
 
 def _ptr(t) -> int:
@@ -542,6 +543,7 @@ def fill_mxfp4_page(
 
 __all__ = [
     "EXACT",
+    "OFFICIAL",
     "FAST",
     "Context",
     "S14MatvecShape",

@@ -116,8 +116,18 @@ typedef struct {
 /* Reduction order.  S14_MODE_EXACT reproduces the reference CPU oracle's
  * order (one output row per lane, k ascending, multiply then add, no FMA),
  * so results are bit-identical to it.  S14_MODE_FAST splits K across a
- * wavefront and reduces with cross-lane adds: HBM-bound, not bit-identical. */
-enum { S14_MODE_EXACT = 0, S14_MODE_FAST = 1 };
+ * wavefront and reduces with cross-lane adds: HBM-bound, not bit-identical.
+ * S14_MODE_OFFICIAL (fused expert entry points only: expert chain, MoE
+ * layer, routed layer/block, no-alloc block) computes the model's official
+ * expert (executor.py:712-744, l42_reference.py:390-419): each linear's
+ * activation requantised to e4m3 with one power-of-two scale per 128
+ * values, each linear's output rounded to bf16, the route weight applied to
+ * h before w2 (shared expert: none), expert outputs summed in f32 in route
+ * order with the shared expert last, the layer output rounded to bf16; dot
+ * products in the EXACT order, so results are bit-identical to the oracle's
+ * official restatement.  The expert chain in this mode applies its weight
+ * the same way, to h before w2. */
+enum { S14_MODE_EXACT = 0, S14_MODE_FAST = 1, S14_MODE_OFFICIAL = 2 };
 
 /* ---- dispatch records (bind → cmd) ---- */
 typedef struct {

@@ -89,6 +89,8 @@ def _declare(L):
         "s14o_router_logits": (None, [U32, U32, P, P, P]),
         "s14o_route": (None, [U32, U32, P, P, P, I, U32, F, P, P, P]),
         "s14o_route_hash": (I, [U32, U32, P, P, P, P, I, U32, F, P, P, P]),
+        "s14o_expert_official": (None, [U32, U32, P, P, P, F, I, P]),
+        "s14o_moe_layer_official": (None, [U32, U32, P, U32, P, P, P, P, P, P]),
         "s14o_route_valid": (I, [P, P, U32, U32, F]),
         "s14o_error_stats_compute": (None, [C.c_size_t, P, P, C.POINTER(ErrorStats)]),
         "s14o_requant_e4m3": (None, [U32, U32, U32, P, P, P]),
@@ -248,6 +250,36 @@ def moe_layer(x, routed_pages, weights, shared_page, shared_fmt="mxfp4", hidden=
     sh_f8 = C.byref(sh) if shared_fmt != "mxfp4" else None
     lib().s14o_moe_layer(hidden, inter, _p(x), k, C.cast(arr, P), _p(w), sh_mx, sh_f8, _p(y))
     return y
+
+
+def expert_official(x, page, weight=1.0, apply_weight=True, fmt="mxfp4", hidden=HIDDEN, inter=INTER) -> np.ndarray:
+    """One expert under the official semantics (executor.py:712-744): bf16
+    linear outputs, group-128 e4m3 activation requant before every linear,
+    the route weight applied to h before w2 (routed experts only)."""
+    x = _f32(x)
+    e = _expert(page, fmt, hidden, inter)
+    out = np.empty(hidden, dtype=np.float32)
+    mx = C.byref(e) if fmt == "mxfp4" else None
+    f8 = C.byref(e) if fmt != "mxfp4" else None
+    lib().s14o_expert_official(hidden, inter, _p(x), mx, f8, float(weight), int(apply_weight), _p(out))
+    return out
+
+
+def moe_layer_official(x, routed_pages, weights, shared_page, shared_fmt="mxfp4", hidden=HIDDEN, inter=INTER,
+                       with_f32=False):
+    """Official layer: bf16(sum of the routed experts' outputs in route order,
+    then the shared expert's, in f32); shared_page None: routed experts only."""
+    x = _f32(x)
+    k = len(routed_pages)
+    arr = (_Expert * max(1, k))(*[_expert(p, "mxfp4", hidden, inter) for p in routed_pages])
+    w = _f32(weights)
+    y = np.empty(hidden, dtype=np.float32)
+    y32 = np.empty(hidden, dtype=np.float32)
+    sh = _expert(shared_page, shared_fmt, hidden, inter) if shared_page is not None else None
+    sh_mx = C.byref(sh) if sh is not None and shared_fmt == "mxfp4" else None
+    sh_f8 = C.byref(sh) if sh is not None and shared_fmt != "mxfp4" else None
+    lib().s14o_moe_layer_official(hidden, inter, _p(x), k, C.cast(arr, P), _p(w), sh_mx, sh_f8, _p(y), _p(y32))
+    return (y, y32) if with_f32 else y
 
 
 def router_logits(wr, x) -> np.ndarray:

@@ -464,3 +464,69 @@ void s14o_mxfp4_expert_down_requant(uint32_t hidden, uint32_t inter, uint32_t gr
   free(q);
   free(xd);
 }
+
+/* ------------------------------------------------------------------ */
+/* official expert semantics                                           */
+/* ------------------------------------------------------------------ */
+
+/* act_quant of l42_reference.py:390-403 with group 128, dequantised: the
+ * activation every official linear multiplies (exact f32 values). */
+static void act_quant_128(uint32_t n, const float *x, float *xd) {
+  uint8_t *q = (uint8_t *)malloc(n + n / 128);
+  uint8_t *sc = q + n;
+  s14o_requant_e4m3(1, n, 128, x, q, sc);
+  s14o_dequant_requant(1, n, 128, q, sc, xd);
+  free(q);
+}
+
+static float bf16_round(float v) { return s14o_bf16_to_f32(s14o_f32_to_bf16_rne(v)); }
+
+void s14o_expert_official(uint32_t hidden, uint32_t inter, const float *x, const s14o_mxfp4_expert *mx,
+                          const s14o_fp8_expert *f8, float weight, int apply_weight, float *out) {
+  size_t big = hidden > inter ? hidden : inter;
+  float *xd = (float *)malloc(sizeof(float) * (big + 3 * inter));
+  float *g = xd + big, *u = g + inter, *h = u + inter;
+  act_quant_128(hidden, x, xd);
+  if (mx) {
+    s14o_mxfp4_matvec(inter, hidden, xd, mx->w1, mx->s1, g);
+    s14o_mxfp4_matvec(inter, hidden, xd, mx->w3, mx->s3, u);
+  } else {
+    s14o_fp8_matvec_ue8m0(inter, hidden, xd, f8->w1, f8->s1, g);
+    s14o_fp8_matvec_ue8m0(inter, hidden, xd, f8->w3, f8->s3, u);
+  }
+  for (uint32_t i = 0; i < inter; ++i) {
+    g[i] = bf16_round(g[i]);
+    u[i] = bf16_round(u[i]);
+  }
+  s14o_swiglu_limit(inter, g, u, h);
+  for (uint32_t i = 0; i < inter; ++i) h[i] = bf16_round(apply_weight ? h[i] * weight : h[i]);
+  act_quant_128(inter, h, xd);
+  if (mx)
+    s14o_mxfp4_matvec(hidden, inter, xd, mx->w2, mx->s2, out);
+  else
+    s14o_fp8_matvec_ue8m0(hidden, inter, xd, f8->w2, f8->s2, out);
+  for (uint32_t i = 0; i < hidden; ++i) out[i] = bf16_round(out[i]);
+  free(xd);
+}
+
+void s14o_moe_layer_official(uint32_t hidden, uint32_t inter, const float *x, uint32_t topk,
+                             const s14o_mxfp4_expert *routed, const float *weights,
+                             const s14o_mxfp4_expert *shared_mx, const s14o_fp8_expert *shared_fp8, float *y,
+                             float *y_f32) {
+  float *acc = (float *)calloc(hidden, sizeof(float));
+  float *out = (float *)malloc(sizeof(float) * hidden);
+  for (uint32_t e = 0; e < topk; ++e) {
+    s14o_expert_official(hidden, inter, x, &routed[e], NULL, weights[e], 1, out);
+    for (uint32_t i = 0; i < hidden; ++i) acc[i] += out[i];
+  }
+  if (shared_mx || shared_fp8) {
+    s14o_expert_official(hidden, inter, x, shared_mx, shared_fp8, 1.0f, 0, out);
+    for (uint32_t i = 0; i < hidden; ++i) acc[i] += out[i];
+  }
+  for (uint32_t i = 0; i < hidden; ++i) {
+    if (y_f32) y_f32[i] = acc[i];
+    y[i] = bf16_round(acc[i]);
+  }
+  free(out);
+  free(acc);
+}

@@ -102,6 +102,23 @@ void s14o_moe_layer(uint32_t hidden, uint32_t inter, const float *x, uint32_t to
                     const s14o_mxfp4_expert *shared_mx, const s14o_fp8_expert *shared_fp8,
                     float *y);
 
+/* Official expert semantics (executor.py:712-744, l42_reference.py:390-419):
+ * every linear multiplies the activation requantised by act_quant (e4m3, one
+ * E8M0 scale 2^ceil(log2(max(amax,1e-4)/448)) per 128 values, dequantised:
+ * exact f32) in the oracle's row order and rounds its output to bf16 (RNE).
+ * Expert: g = bf16(W1 xq), u = bf16(W3 xq); h = bf16(swiglu(g, u) * weight)
+ * for a routed expert (the route weight before w2, executor.py:720-722),
+ * h = bf16(swiglu(g, u)) for the shared one (apply_weight = 0); out =
+ * bf16(W2 hq).  mx or f8 selects the page format. */
+void s14o_expert_official(uint32_t hidden, uint32_t inter, const float *x, const s14o_mxfp4_expert *mx,
+                          const s14o_fp8_expert *f8, float weight, int apply_weight, float *out);
+/* Official layer: acc = 0; acc += out_e (f32) for the routed experts in route
+ * order, then the shared one; y = bf16(acc) (and y_f32 = acc if not NULL). */
+void s14o_moe_layer_official(uint32_t hidden, uint32_t inter, const float *x, uint32_t topk,
+                             const s14o_mxfp4_expert *routed, const float *weights,
+                             const s14o_mxfp4_expert *shared_mx, const s14o_fp8_expert *shared_fp8, float *y,
+                             float *y_f32);
+
 /* ---- router ---- */
 enum { S14O_SCORE_SIGMOID = 0, S14O_SCORE_SQRT_SOFTPLUS = 1 };
 /* Router logits z[e] = W_r[e,:] . x.  The reference computes this with

@@ -40,6 +40,9 @@ def test_bind_mxfp4_capacities(native):
     assert bind_mx(2048, 4096, buf(None, 16384), *cases[0][1:])[0] == N.S14_ERR_INVALID
     assert bind_mx(2048, 4096, buf(A + 4, 16384), buf(A, 4194304), buf(A, 262144), buf(A, 8192))[0] == N.S14_ERR_INVALID
     assert bind_mx(2048, 4096, buf(A, 16384), buf(A, 4194304), buf(A, 262144), buf(A, 8192), mode=7)[0] == N.S14_ERR_INVALID
+    # official semantics belong to the fused expert entry points, not to a plain matvec
+    ok_bufs = (buf(A, 16384), buf(A, 4194304), buf(A, 262144), buf(A, 8192))
+    assert bind_mx(2048, 4096, *ok_bufs, mode=N.S14_MODE_OFFICIAL)[0] == N.S14_ERR_INVALID
 
 
 def test_bind_fp8_dtypes_and_tiles(native):

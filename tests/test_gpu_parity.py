@@ -902,3 +902,94 @@ def test_hash_router_bad_row_poisons_only_its_token(ctx, oracle, bank):
     with pytest.raises(s14.S14Error) as err:
         ctx.launch_status()
     assert err.value.code == N.S14_ERR_ROUTE
+
+
+# --------------------------------------------------------------------------
+# official expert semantics (executor.py:712-744, l42_reference.py:390-419)
+
+
+def _is_bf16(a) -> bool:
+    b = bits(a)
+    return bool(np.all((b & 0xFFFF) == 0))
+
+
+def test_official_config2_device_router(ctx, oracle, bank):
+    """Config 2 in S14_MODE_OFFICIAL: the device router's route, then each
+    linear's activation requantised in groups of 128, bf16 outputs, the route
+    weight on h before w2, f32 sum in route order with the shared expert
+    last, bf16 layer output; bit for bit against the oracle's official
+    layer."""
+    say("config 2 official, device router, MXFP4 shared")
+    x = synth.token(seed=0)
+    _, i_o, w_o = oracle.route(bank["wr"], bank["bias"], x)
+    want = oracle.moe_layer_official(x, [page_host(bank, int(e)) for e in i_o], w_o, page_host(bank, 256))
+    router = s14.Router(bank["wr_d"], bank["bias_d"])
+    y = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    ids = torch.empty(6, dtype=torch.int16, device="cuda")
+    wts = torch.empty(6, dtype=torch.float32, device="cuda")
+    s14.moe_layer_route(ctx, router, bank["table"], bank["pages"][256], dev(x), y, ids, wts, mode=s14.OFFICIAL)
+    assert host(ids).astype(np.uint16).tolist() == i_o.tolist()
+    assert_bit_exact(host(wts), w_o, "route weights")
+    got = host(y)
+    assert_bit_exact(got, want, "config2 official")
+    assert _is_bf16(got)
+    # not the exact mode's layer (the modes must differ)
+    exact = oracle.moe_layer(x, [page_host(bank, int(e)) for e in i_o], w_o, page_host(bank, 256))
+    assert not np.array_equal(got, exact)
+
+
+def test_official_route_given_fp8_shared(ctx, oracle, bank):
+    """Official layer with a given route and the reference's FP8 shared page
+    (e4m3 weights, 128x128 block scales): the FP8 rows see the requantised
+    activation too."""
+    say("official layer, route given, FP8 shared")
+    ids = [126, 12, 205, 149, 227, 174]
+    w = np.array([0.3, 0.2, 0.15, 0.15, 0.1, 0.1], dtype=np.float32)
+    sh = synth.gen_fp8_page(0, 0)
+    x = synth.token(seed=2)
+    want = oracle.moe_layer_official(x, [page_host(bank, e) for e in ids], w, sh, shared_fmt="fp8")
+    y = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    s14.moe_layer(ctx, [bank["pages"][e] for e in ids], w.tolist(), dev(sh), dev(x), y,
+                  shared_format=N.S14_PAGE_FP8, mode=s14.OFFICIAL)
+    assert_bit_exact(host(y), want, "official fp8 shared")
+
+
+def test_official_chain_weight_before_w2(ctx, oracle, bank):
+    """The expert chain in official mode: one routed expert, its weight on h
+    before w2, no shared expert."""
+    say("official expert chain")
+    cfg = synth.config0(seed=5)
+    w = float(cfg["route_w"])
+    want = oracle.moe_layer_official(cfg["x"], [cfg["page"]], np.array([w], np.float32), None)
+    y = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    s14.expert_chain(ctx, dev(cfg["page"]), dev(cfg["x"]), w, y, mode=s14.OFFICIAL)
+    assert_bit_exact(host(y), want, "official chain")
+
+
+@pytest.mark.parametrize("score_fn,scale,tokens", [(N.S14_SCORE_SIGMOID, 1.0, 8),
+                                                   (N.S14_SCORE_SQRT_SOFTPLUS, 1.5, 3)])
+def test_official_block(ctx, oracle, bank, score_fn, scale, tokens):
+    """Official blocks through the device router, token by token against the
+    oracle's official layer evaluated with the device's route (bit for bit
+    for the sigmoid score; sqrt-softplus weights within 1e-6 relative, the
+    device's log1pf not being glibc's)."""
+    say(f"official block T={tokens} score_fn={score_fn}")
+    xs = synth.block_tokens(seed=9, tokens=tokens)
+    router = s14.Router(bank["wr_d"], bank["bias_d"], score_fn=score_fn, route_scale=scale)
+    y = torch.empty((tokens, HIDDEN), dtype=torch.float32, device="cuda")
+    ids = torch.empty((tokens, 6), dtype=torch.int16, device="cuda")
+    wts = torch.empty((tokens, 6), dtype=torch.float32, device="cuda")
+    s14.moe_block_route(ctx, tokens, router, bank["table"], bank["pages"][256], dev(xs), y, ids, wts,
+                        mode=s14.OFFICIAL)
+    got, ids_h, wts_h = host(y), host(ids).astype(np.uint16), host(wts)
+    shared = page_host(bank, 256)
+    for t in range(tokens):
+        _, i_o, w_o = oracle.route(bank["wr"], bank["bias"], xs[t], score_fn=score_fn, route_scale=scale)
+        assert ids_h[t].tolist() == i_o.tolist()
+        if score_fn == N.S14_SCORE_SIGMOID:
+            assert_bit_exact(wts_h[t], w_o, f"weights t={t}")
+        else:
+            np.testing.assert_allclose(wts_h[t], w_o, rtol=1e-6)
+        want = oracle.moe_layer_official(xs[t], [page_host(bank, int(e)) for e in i_o], wts_h[t], shared)
+        assert_bit_exact(got[t], want, f"official block t={t}")
+
