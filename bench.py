@@ -95,7 +95,7 @@ def parse():
                     help="only run a plain 256 MiB device copy 10 times (the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     ap.add_argument("--prefill-steps", type=int, default=20)
-    ap.add_argument("--only", choices=["k1", "k8", "config0", "config1", "prefill", "all"], default="all",
+    ap.add_argument("--only", choices=["k1", "k8", "config0", "config1", "prefill", "linear", "all"], default="all",
                     help="restrict the timed work (for profiler runs)")
     return ap.parse_args()
 
@@ -132,6 +132,32 @@ class Timer:
             per.append(start.elapsed_time(end) / steps)
         return {"ms": statistics.median(per), "ms_min": min(per), "ms_max": max(per), "trials": len(per),
                 "steps_per_trial": steps}
+
+    def run_graph(self, fn, launches: int, warmup: int) -> dict:
+        """Median per-launch time of `launches` calls captured in one HIP
+        graph and replayed once per trial: device time without the host's
+        launch gap (for kernels of a few microseconds)."""
+        torch = self.torch
+        for i in range(max(1, warmup)):
+            fn(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(launches):
+                fn(i)
+        g.replay()  # first replay uploads the graph
+        torch.cuda.synchronize()
+        per = []
+        for _ in range(self.trials):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            g.replay()
+            end.record()
+            torch.cuda.synchronize()
+            per.append(start.elapsed_time(end) / launches)
+        del g
+        return {"ms": statistics.median(per), "ms_min": min(per), "ms_max": max(per), "trials": len(per),
+                "launches_per_trial": launches, "timing": "hip graph replay"}
 
 
 def main() -> int:
@@ -259,8 +285,12 @@ def main() -> int:
     if only in ("prefill", "all"):
         progress("config 4 (prefill)")
         prefill = bench_prefill(args, ctx, tables, shared, NL, torch, np, s14, synth)
+    linear = None
+    if only in ("linear", "all"):
+        progress("adjacent FP8 projections (fp8_linear)")
+        linear = bench_linear(args, ctx, timer, torch, s14)
     if only != "all" and only not in ("k1",):
-        print(json.dumps({"only": only, "legs": out, "prefill": prefill}), flush=True)
+        print(json.dumps({"only": only, "legs": out, "prefill": prefill, "fp8_linear": linear}), flush=True)
         return 0
 
     main_r = out[args.mode]
@@ -318,6 +348,7 @@ def main() -> int:
         "config1": main_r.get("config1"),
         "other_mode": {k: v for k, v in out.items() if k != args.mode},
         "prefill": prefill,
+        "fp8_linear": linear,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
@@ -350,6 +381,51 @@ def bench_config1(args, ctx, timer, torch, np, s14, synth):
         res[name] = {"us_per_matvec": us, "timing": t, "algorithmic_bytes": WQA_BYTES,
                      "hbm_gbps": WQA_BYTES / (us * 1e-6) / 1e9, "hbm_frac": WQA_BYTES / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
                      "note": "back-to-back launches from Python: includes the launch gap"}
+    return res
+
+
+LINEAR_SHAPES = {"wq_b": (32768, 1024), "wkv": (512, 4096), "wo_a": (8192, 4096), "wo_b": (4096, 8192)}
+
+
+def linear_bytes(m: int, n: int, k: int) -> int:
+    """Algorithmic bytes of one fp8_linear: e4m3 weight, UE8M0 tile scales,
+    e4m3 activations and their scales, f32 output."""
+    g = -(-k // 128)
+    return n * k + -(-n // 128) * g + m * k + m * g + 4 * m * n
+
+
+def bench_linear(args, ctx, timer, torch, s14):
+    """The adjacent FP8 projections (fp8_linear, fp8.py:111-193) at wq_b,
+    wkv, wo_a and wo_b (l42_reference.py:89-102) for 1 and 8 tokens, each
+    mode timed as a HIP graph of launches over weight copies that total at
+    least 512 MB (past the 256 MB MALL)."""
+    res = {}
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed)
+    for name, (n, k) in LINEAR_SHAPES.items():
+        copies = max(2, -(-(512 << 20) // (n * k)))
+        W = torch.randint(0, 256, (copies, n, k), dtype=torch.uint8, device="cuda", generator=gen)
+        W[(W & 0x7F) == 0x7F] = 0x7E
+        WS = torch.randint(114, 122, (copies, -(-n // 128), k // 128), dtype=torch.uint8, device="cuda", generator=gen)
+        for m in (1, 8):
+            X = torch.randint(0, 256, (m, k), dtype=torch.uint8, device="cuda", generator=gen)
+            X[(X & 0x7F) == 0x7F] = 0x7E
+            XS = torch.randint(120, 128, (m, k // 128), dtype=torch.uint8, device="cuda", generator=gen)
+            y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            nbytes = linear_bytes(m, n, k)
+            for mode_name, mode in (("exact", s14.EXACT), ("fast", s14.FAST)):
+                def f(i, mode=mode):
+                    c = i % copies
+                    s14.fp8_linear(ctx, X, XS, W[c], WS[c], y, mode=mode)
+
+                t = timer.run_graph(f, copies, 3)
+                us = t["ms"] * 1e3
+                gbps = nbytes / (us * 1e-6) / 1e9
+                res[f"{name}_m{m}_{mode_name}"] = {"n": n, "k": k, "m": m, "us": us, "algorithmic_bytes": nbytes,
+                                                   "hbm_gbps": gbps, "hbm_frac": gbps / HBM_PEAK_GBPS, "timing": t}
+                progress(f"  {name} m={m} {mode_name}: {us:.2f} us, {gbps:.0f} GB/s")
+        del W, WS
+        torch.cuda.synchronize()
     return res
 
 

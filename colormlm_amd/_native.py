@@ -41,6 +41,7 @@ ERROR_NAMES = {
 S14_MODE_EXACT = 0
 S14_MODE_FAST = 1
 S14_MODE_OFFICIAL = 2
+S14_LINEAR_ROUND_BF16 = 1
 S14_X_F32 = 0
 S14_X_BF16 = 1
 S14_SCALE_UE8M0 = 0
@@ -239,6 +240,8 @@ SIGNATURES = {
     "s14_moe_prefill": (I, [P, P, U32, C.POINTER(Router), P, P, P, P, P, P]),
     "s14_last_prefill_stats": (I, [P, C.POINTER(U32), C.POINTER(U32), C.POINTER(U32)]),
     "s14_requant_e4m3": (I, [P, P, U32, U32, P, P, P]),
+    "s14_act_quant_e4m3": (I, [P, P, U32, U32, U32, P, P, P]),
+    "s14_fp8_linear": (I, [P, P, U32, U32, U32, Buffer, Buffer, I, Buffer, Buffer, I, Buffer, Buffer, I, I]),
     "s14_last_prefill_view": (I, [P, C.POINTER(PrefillView)]),
     "s14_fill_mxfp4_page": (I, [P, P, P, U64, U32, U32, U32, U32, I, I]),
     "s14_pool_create": (I, [P, U32, U64, C.POINTER(P)]),

@@ -29,7 +29,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "lib" / "libs14hip.so"
 OBJ = PKG / "lib" / "obj"
-DEVICE_SOURCES = ["s14_device.hip", "s14_block.hip", "s14_prefill.hip", "s14_static.hip"]
+DEVICE_SOURCES = ["s14_device.hip", "s14_block.hip", "s14_prefill.hip", "s14_static.hip", "s14_linear.hip"]
 HOST_SOURCES = ["s14_api.cpp", "s14_pool.cpp"]
 SOURCES = DEVICE_SOURCES + HOST_SOURCES
 ARCH = os.environ.get("S14_OFFLOAD_ARCH", "gfx950")

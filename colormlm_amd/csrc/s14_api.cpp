@@ -14,6 +14,7 @@
 
 #include "s14_device.hpp"
 #include "s14_internal.hpp"
+#include "s14_linear.hpp"
 #include "s14_prefill.hpp"
 
 using s14::fail;
@@ -29,6 +30,8 @@ struct s14_ctx {
   hipStream_t copy = nullptr;
   void *ws_base = nullptr;
   void *prefill_base = nullptr;  // prefill workspace, made on the first prefill call
+  void *lin_base = nullptr;      // fp8_linear FAST split-K workspace, made on the first FAST call
+  s14::LinearWorkspace lws{};
   uint32_t prefill_tokens = 0;   // token count of the last prefill
   s14::PrefillWorkspace pws{};
   s14::Workspace ws{};
@@ -149,6 +152,7 @@ extern "C" void s14_ctx_destroy(s14_ctx *ctx) {
   if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
   if (ctx->ws_base) (void)hipFree(ctx->ws_base);
   if (ctx->prefill_base) (void)hipFree(ctx->prefill_base);
+  if (ctx->lin_base) (void)hipFree(ctx->lin_base);
   if (ctx->compute) (void)hipStreamDestroy(ctx->compute);
   if (ctx->copy) (void)hipStreamDestroy(ctx->copy);
   for (auto ev : ctx->stage_ev)
@@ -656,15 +660,89 @@ extern "C" int s14_moe_prefill(s14_ctx *ctx, void *stream, uint32_t tokens, cons
   return S14_OK;
 }
 
-extern "C" int s14_requant_e4m3(s14_ctx *ctx, void *stream, uint32_t rows, uint32_t k, const float *x,
-                                uint8_t *q, uint8_t *scales) {
+extern "C" int s14_act_quant_e4m3(s14_ctx *ctx, void *stream, uint32_t rows, uint32_t k, uint32_t group,
+                                  const float *x, uint8_t *q, uint8_t *scales) {
   if (int rc = check_ctx(ctx)) return rc;
-  if (rows == 0 || k == 0 || k % 32 != 0) return fail(S14_ERR_SHAPE, "requant needs rows > 0 and k a multiple of 32");
+  if (group != 32 && group != 64 && group != 128) return fail(S14_ERR_SHAPE, "requant group %u is not 32, 64 or 128", group);
+  if (rows == 0 || k == 0 || k % group != 0)
+    return fail(S14_ERR_SHAPE, "requant needs rows > 0 and k a multiple of the group (%u)", group);
   if (uint64_t(rows) * k >= (uint64_t(1) << 32))
     return fail(S14_ERR_SHAPE, "requant of %u x %u values exceeds 2^32 values", rows, k);
   if (!x || !q || !scales) return fail(S14_ERR_INVALID, "NULL requant buffer");
-  const hipError_t e = s14::launch_requant_e4m3(pick(ctx, stream), rows, k, x, q, scales);
+  const hipError_t e = s14::launch_act_quant(pick(ctx, stream), rows, k, group, x, q, scales);
   if (e != hipSuccess) return hip_fail(e, "requant launch");
+  return S14_OK;
+}
+
+extern "C" int s14_requant_e4m3(s14_ctx *ctx, void *stream, uint32_t rows, uint32_t k, const float *x,
+                                uint8_t *q, uint8_t *scales) {
+  return s14_act_quant_e4m3(ctx, stream, rows, k, 32, x, q, scales);
+}
+
+// ---------------------------------------------------------------------------
+// activation-quantised FP8 linear (fp8.py:111-193)
+// ---------------------------------------------------------------------------
+
+namespace {
+
+// FAST's split-K partials and arrival counters, allocated on the first FAST
+// call (counters zeroed once; every launch leaves them zero).
+int linear_workspace(s14_ctx *ctx) {
+  if (ctx->lin_base) return S14_OK;
+  const size_t cnt_bytes = sizeof(uint32_t) * s14::kLinMaxCounters;
+  S14_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  S14_HIP(hipMalloc(&ctx->lin_base, s14::kLinPartBytes + cnt_bytes), "hipMalloc(linear workspace)");
+  uint8_t *b = static_cast<uint8_t *>(ctx->lin_base);
+  S14_HIP(hipMemset(b + s14::kLinPartBytes, 0, cnt_bytes), "hipMemset(linear counters)");
+  S14_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  ctx->lws.part = reinterpret_cast<float *>(b);
+  ctx->lws.count = reinterpret_cast<uint32_t *>(b + s14::kLinPartBytes);
+  return S14_OK;
+}
+
+}  // namespace
+
+extern "C" int s14_fp8_linear(s14_ctx *ctx, void *stream, uint32_t m, uint32_t n, uint32_t k, s14_buffer x,
+                              s14_buffer x_scale, int x_scale_dtype, s14_buffer weight, s14_buffer weight_scale,
+                              int weight_scale_dtype, s14_buffer bias, s14_buffer y, int flags, int mode) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (mode != S14_MODE_EXACT && mode != S14_MODE_FAST) return fail(S14_ERR_INVALID, "unknown mode %d", mode);
+  if (flags & ~S14_LINEAR_ROUND_BF16) return fail(S14_ERR_INVALID, "unknown linear flags 0x%x", flags);
+  if (m == 0 || n == 0 || k == 0) return fail(S14_ERR_SHAPE, "fp8_linear needs m, n and k > 0 (m=%u n=%u k=%u)", m, n, k);
+  if (k > s14::kLinMaxK) return fail(S14_ERR_SHAPE, "fp8_linear k=%u exceeds %u", k, s14::kLinMaxK);
+  const bool xs_f32 = x_scale_dtype == S14_SCALE_F32, ws_f32 = weight_scale_dtype == S14_SCALE_F32;
+  if ((!xs_f32 && x_scale_dtype != S14_SCALE_UE8M0) || (!ws_f32 && weight_scale_dtype != S14_SCALE_UE8M0))
+    return fail(S14_ERR_INVALID, "unknown scale dtype");
+  const uint64_t G = (k + 127) / 128;
+  // 32-bit buffer offsets: weight rows of the last 32-row tile, and every
+  // activation offset below the out-of-range marker the FAST kernel uses
+  if (uint64_t(n + 31) * k > UINT32_MAX || uint64_t(m) * k >= 0xFFFFFF00ull || uint64_t(m) * n > UINT32_MAX)
+    return fail(S14_ERR_SHAPE, "fp8_linear m=%u n=%u k=%u exceeds 32-bit addressing", m, n, k);
+  if (int rc = require_capacity(x, uint64_t(m) * k, "x")) return rc;
+  if (int rc = require_capacity(x_scale, uint64_t(m) * G * (xs_f32 ? 4 : 1), "activation_scale")) return rc;
+  if (int rc = require_capacity(weight, uint64_t(n) * k, "weight")) return rc;
+  if (int rc = require_capacity(weight_scale, (uint64_t(n) + 127) / 128 * G * (ws_f32 ? 4 : 1), "weight_scale"))
+    return rc;
+  if (bias.ptr)
+    if (int rc = require_capacity(bias, uint64_t(n) * 4, "bias")) return rc;
+  if (int rc = require_capacity(y, uint64_t(m) * n * 4, "y")) return rc;
+  if (mode == S14_MODE_FAST)
+    if (int rc = linear_workspace(ctx)) return rc;
+  const s14::LinearArgs a{m,
+                          n,
+                          k,
+                          uint32_t(G),
+                          static_cast<const uint8_t *>(x.ptr),
+                          x_scale.ptr,
+                          xs_f32,
+                          static_cast<const uint8_t *>(weight.ptr),
+                          weight_scale.ptr,
+                          ws_f32,
+                          static_cast<const float *>(bias.ptr),
+                          static_cast<float *>(y.ptr),
+                          (flags & S14_LINEAR_ROUND_BF16) ? 1 : 0};
+  const hipError_t e = s14::launch_fp8_linear(pick(ctx, stream), a, mode, ctx->lws);
+  if (e != hipSuccess) return hip_fail(e, "fp8_linear launch");
   return S14_OK;
 }
 

@@ -1,0 +1,466 @@
+// Activation-quantised FP8 linear on gfx950: the adjacent FP8 projections of
+// the S14 layer (wq_b [32768, 1024], wkv [512, 4096], wo_a [8192, 4096],
+// wo_b [4096, 8192]; l42_reference.py:89-102) in fp8_linear's semantics
+// (local_s14_primitives/fp8.py:111-193):
+//
+//   x  e4m3 codes [m][k], one scale per (token, 128 k)       (activation)
+//   w  e4m3 codes [n][k], one scale per (128 rows, 128 k)    (weight)
+//   y[t][r] = sum over groups g ascending of
+//               partial_g = sum_k (dec(x) * sa[t][g]) * (dec(w) * sb[r/128][g])
+//             then + bias[r]; f32 throughout (acc = 0; acc += partial_g).
+//
+// Scales are UE8M0 codes or f32 values (fp8.py:37-46).  The reference sums
+// each group's products with torch addmm, whose order is the BLAS's; EXACT
+// fixes it to k ascending, multiply then add, so its results are bit-equal
+// to the CPU oracle's s14o_fp8_linear.  FAST computes each group's dot
+// products on the bf16 MFMA (v_mfma_f32_32x32x16_bf16) from operands decoded
+// exactly (every e4m3 value is a bf16 value), so products are exact and sums
+// f32, and folds the group scales in afterwards: not order-exact.  The fp8
+// MFMA (v_mfma_scale_f32_32x32x64_f8f6f4) is not used here: measured on
+// MI355X, its internal sum keeps about 16 bits below the largest product of
+// a step (256 * 256 + 1 * 1 comes back as 65536), which put FAST 5e-5 of a
+// row's sum of |products| away from the oracle on uniformly drawn codes.
+//
+// The activation requant that produces x (l42_reference.py:390-403: e4m3
+// RNE saturating, scale 2^ceil(log2(max(amax, 1e-4) / 448)) per group) is
+// k_act_quant; group 128 feeds this linear, group 32 the prefill.
+#include <hip/hip_runtime.h>
+
+#include "s14_device.hpp"
+#include "s14_device_util.hpp"
+#include "s14_e4m3.h"
+#include "s14_linear.hpp"
+
+namespace s14 {
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+// Eight e4m3 codes (two little-endian words) as eight bf16, exactly.
+__device__ __forceinline__ v8bf e4m3x8_bf16(uint32_t w0, uint32_t w1) {
+  const v4u v = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
+                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
+                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
+                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+  return __builtin_bit_cast(v8bf, v);
+}
+
+// ---------------------------------------------------------------------------
+// activation requant: one thread per group of `group` values along k
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void k_act_quant(uint32_t n_groups, uint32_t group, const float *__restrict__ X,
+                                                   uint8_t *__restrict__ Q, uint8_t *__restrict__ S) {
+  const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n_groups) return;
+  const float *src = X + size_t(gid) * group;
+  float amax = 0.0f;  // strict '>' scan: a NaN never becomes the maximum
+  for (uint32_t i = 0; i < group; ++i) amax = fabsf(src[i]) > amax ? fabsf(src[i]) : amax;
+  const uint32_t code = requant_code(amax);
+  const float inv = __uint_as_float((254u - code) << 23);
+  uint8_t *dst = Q + size_t(gid) * group;
+  for (uint32_t i = 0; i < group; ++i) dst[i] = uint8_t(s14x::e4m3_rne_sat(__fmul_rn(src[i], inv)));
+  S[gid] = uint8_t(code);
+}
+
+__device__ __forceinline__ float lin_scale(Rsrc r, uint32_t i, int is_f32) {
+  return is_f32 ? ldf(r, 4u * i) : ue8m0_f32(ld1(r, i));
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint4 v, int b) {
+  const uint32_t w = b < 4 ? v.x : b < 8 ? v.y : b < 12 ? v.z : v.w;
+  return (w >> (8 * (b & 3))) & 0xffu;
+}
+
+// ---------------------------------------------------------------------------
+// EXACT: one lane per (row, group) computes partial_g for MT tokens, k
+// ascending; the row's partials meet in LDS and one lane per (token, row)
+// adds them in group order.  A workgroup holds R = max(1, 256 / G) rows.
+// kVec: k % 16 == 0 and 16-byte aligned operands (16-byte loads).
+// ---------------------------------------------------------------------------
+
+template <int MT, bool kVec>
+__global__ __launch_bounds__(256) void k_linear_exact(LinearArgs a) {
+  extern __shared__ float lpart[];  // [MT][R][G]
+  const uint32_t G = a.groups, K = a.k, N = a.n, M = a.m;
+  const uint32_t R = G >= 256u ? 1u : 256u / G;
+  const uint32_t row0 = blockIdx.x * R, m0 = blockIdx.y * uint32_t(MT);
+  const Rsrc rw = make_rsrc(a.w, N * K);
+  const Rsrc rx = make_rsrc(a.x, M * K);
+  const uint32_t n_sw = (N + 127u) / 128u * G, n_sx = M * G;
+  const Rsrc rsw = make_rsrc(a.w_scale, a.w_scale_f32 ? 4u * n_sw : n_sw);
+  const Rsrc rsx = make_rsrc(a.x_scale, a.x_scale_f32 ? 4u * n_sx : n_sx);
+  for (uint32_t task = threadIdx.x; task < R * G; task += 256u) {
+    const uint32_t r = task / G, g = task % G, row = row0 + r;
+    float p[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) p[j] = 0.0f;
+    if (row < N) {
+      const float sb = lin_scale(rsw, (row / 128u) * G + g, a.w_scale_f32);
+      float sa[MT];
+#pragma unroll
+      for (int j = 0; j < MT; ++j) sa[j] = m0 + j < M ? lin_scale(rsx, (m0 + j) * G + g, a.x_scale_f32) : 0.0f;
+      const uint32_t k0 = g * kLinGroup, len = min(kLinGroup, K - k0);
+      const uint32_t wo = row * K + k0;
+      if constexpr (kVec) {
+        for (uint32_t c = 0; c < len; c += 16u) {
+          const uint4 w16 = ld16(rw, wo + c);
+          uint4 x16[MT];
+#pragma unroll
+          for (int j = 0; j < MT; ++j) x16[j] = m0 + j < M ? ld16(rx, (m0 + j) * K + k0 + c) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+          for (int b = 0; b < 16; ++b) {
+            const float wv = __fmul_rn(e4m3_f32(byte_of(w16, b)), sb);
+#pragma unroll
+            for (int j = 0; j < MT; ++j)
+              p[j] = __fadd_rn(p[j], __fmul_rn(__fmul_rn(e4m3_f32(byte_of(x16[j], b)), sa[j]), wv));
+          }
+        }
+      } else {
+        for (uint32_t c = 0; c < len; ++c) {
+          const float wv = __fmul_rn(e4m3_f32(ld1(rw, wo + c)), sb);
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            const uint32_t xc = m0 + j < M ? ld1(rx, (m0 + j) * K + k0 + c) : 0u;
+            p[j] = __fadd_rn(p[j], __fmul_rn(__fmul_rn(e4m3_f32(xc), sa[j]), wv));
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < MT; ++j) lpart[(j * R + r) * G + g] = p[j];
+  }
+  __syncthreads();
+  for (uint32_t t = threadIdx.x; t < uint32_t(MT) * R; t += 256u) {
+    const uint32_t j = t / R, r = t % R, row = row0 + r, m = m0 + j;
+    if (row >= N || m >= M) continue;
+    const float *pp = lpart + (j * R + r) * G;
+    float acc = 0.0f;
+    for (uint32_t g = 0; g < G; ++g) acc = __fadd_rn(acc, pp[g]);
+    if (a.bias) acc = __fadd_rn(acc, a.bias[row]);
+    if (a.round_bf16) acc = bf16_round(acc);
+    a.y[size_t(m) * N + row] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// FAST: one wavefront per (32-row tile, K split, 32-token block).  A chunk is
+// one scale group: 32 rows x 128 k of weight (4 KiB), DMA-loaded into a ring
+// of four LDS slots with four chunks in flight (buffer_load ... lds, 8 lanes
+// per row so each quarter-wave moves two whole 128-byte rows).  Before the
+// ring starts, the wavefront stages its tokens' activations for all of its
+// chunks in LDS, decoded to bf16; with UE8M0 scales the power of two
+// sa[t][g] * sb[g] is folded into them exactly, so the MFMAs accumulate the
+// whole K range into one f32 accumulator; with f32 scales each chunk's sums
+// are scaled after its MFMAs (acc += part * sa[t][g] * sb[g]).  Only the
+// weight DMA is then on the vector-memory counter, so waiting for a chunk
+// never waits for the chunks behind it.
+//
+// Operand layout (32x32x16 bf16, lane l = column l % 32, half h = l / 32;
+// value j of an A lane pairs with value j of the B lane of the same half):
+// for steps 2q and 2q + 1 lane (r, h) reads the 16 bytes k = 16 (2q + h) ..
+// +15 of weight row r (one LDS read) and uses bytes 0-7 in step 2q, bytes
+// 8-15 in step 2q + 1; lane (t, h) reads the same 16 k of token t.  D
+// element i of lane l: row 8 (i / 4) + 4 h + i % 4, column l % 32.  Lanes
+// of tokens past m read token 0's activations: an MFMA column depends on its
+// own B column only, and those columns are never stored.
+//
+// Splits > 1: each wavefront stores its 32 x 32 partial tile; the last to
+// arrive at the tile's counter adds the partials in split order, adds the
+// bias and writes y, and resets the counter for the next launch.
+// ---------------------------------------------------------------------------
+
+constexpr uint32_t kLChunkBytes = kLinTile * kLinGroup;
+__shared__ __attribute__((aligned(16))) uint8_t lin_slot0[kLChunkBytes];
+__shared__ __attribute__((aligned(16))) uint8_t lin_slot1[kLChunkBytes];
+__shared__ __attribute__((aligned(16))) uint8_t lin_slot2[kLChunkBytes];
+__shared__ __attribute__((aligned(16))) uint8_t lin_slot3[kLChunkBytes];
+
+template <int S>
+__device__ __forceinline__ uint8_t *lin_slot() {
+  if constexpr (S == 0) return lin_slot0;
+  else if constexpr (S == 1) return lin_slot1;
+  else if constexpr (S == 2) return lin_slot2;
+  else return lin_slot3;
+}
+template <int S>
+struct LSlot {
+  static constexpr int value = S;
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ __forceinline__ void lin_dma16(Rsrc r, uint8_t *lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(lds), 16, off, 0, 0, 0);
+}
+// Before a DMA load refills a slot, the LDS reads of its previous chunk have
+// returned.
+__device__ __forceinline__ void lin_lds_reads_done() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+// 16-byte piece q of row r sits at piece q ^ lin_swz(r): the 32 rows of a
+// read pass spread over the banks.
+__device__ __forceinline__ uint32_t lin_swz(uint32_t r) { return (r + (r >> 3)) & 7u; }
+
+// Cache policy of the split-K partials' loads: agent scope (sc1), coherent
+// with the write-through stores of the other XCDs.
+constexpr int kCacheAgent = 0x10;
+
+// Staged activations per wavefront: ntok x cw chunks x 128 bf16, plus the
+// f32 scale of every (token, chunk) when the scales are f32 (host bound).
+constexpr uint32_t kLinStageBytes = 40u * 1024u;
+__host__ __device__ constexpr uint32_t lin_stage_bytes(uint32_t ntok, uint32_t cw) {
+  return ntok * cw * (kLinGroup * 2u + 4u);
+}
+
+// Sixteen e4m3 codes times a power of two (or 1) as sixteen bf16, exact.
+__device__ __forceinline__ v4u e4m3x4_bf16s(uint32_t w0, uint32_t w1, float s) {
+  return v4u{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, s, false)),
+             __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, s, true)),
+             __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, s, false)),
+             __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, s, true))};
+}
+
+template <bool kXsF32, bool kWsF32>
+__global__ __launch_bounds__(64) void k_linear_fast(LinearArgs a, LinearWorkspace ws, uint32_t cw, uint32_t splits) {
+  constexpr bool kFold = !kXsF32 && !kWsF32;  // power-of-two scales ride in the bf16 activations
+  extern __shared__ __attribute__((aligned(16))) uint8_t lin_x[];  // [ntok][cw * 128] bf16, then [ntok][cw] f32
+  const uint32_t tile = blockIdx.x, sidx = blockIdx.y, cb = blockIdx.z, ncb = gridDim.z;
+  const uint32_t lane = threadIdx.x & 63u, col = lane & 31u, h = lane >> 5;
+  const uint32_t K = a.k, N = a.n, M = a.m, G = a.groups;
+  const uint32_t g0 = sidx * cw;
+  const uint32_t tok0 = cb * kLinTile, ntok = min(kLinTile, M - tok0);
+  const Rsrc rw = make_rsrc(a.w, N * K);
+  const Rsrc rx = make_rsrc(a.x, M * K);
+  const uint32_t n_sw = (N + 127u) / 128u * G, n_sx = M * G;
+  const Rsrc rsw = make_rsrc(a.w_scale, kWsF32 ? 4u * n_sw : n_sw);
+  const Rsrc rsx = make_rsrc(a.x_scale, kXsF32 ? 4u * n_sx : n_sx);
+  const uint32_t sbrow = (tile * kLinTile / 128u) * G;
+  // DMA lane map: load j of a chunk covers rows 8j..8j+7 of the tile; lane
+  // -> row 8j + lane / 8, LDS piece lane % 8 holding source piece
+  // (lane % 8) ^ lin_swz(row), lin_swz(8j + r) = (j + r) % 8
+  const uint32_t lrow = lane >> 3;
+  uint32_t dma_off[4];
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j)
+    dma_off[j] = (tile * kLinTile + 8u * j + lrow) * K + 16u * ((lane & 7u) ^ ((j + lrow) & 7u));
+  auto issue = [&](auto slot_tag, uint32_t c) {
+    uint8_t *dst = lin_slot<decltype(slot_tag)::value>();
+    lin_lds_reads_done();
+    const uint32_t kb = (g0 + c) * kLinGroup;
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) lin_dma16(rw, dst + 1024u * j, dma_off[j] + kb);
+  };
+  // the first chunks' weights are in flight while the activations are staged
+  issue(LSlot<0>{}, 0);
+  issue(LSlot<1>{}, 1);
+  issue(LSlot<2>{}, 2);
+  issue(LSlot<3>{}, 3);
+  // stage: item = (token, chunk, 16-k piece), one 16-byte load per item
+  const uint32_t row_elems = cw * kLinGroup;  // bf16 per staged token
+  float *stage_scale = reinterpret_cast<float *>(lin_x + size_t(ntok) * row_elems * 2u);
+  for (uint32_t item = lane; item < ntok * cw * 8u; item += 64u) {
+    const uint32_t t = item / (cw * 8u), pc = item % (cw * 8u), c = pc >> 3, piece = pc & 7u;
+    const uint32_t g = g0 + c;
+    const uint4 codes = ld16(rx, (tok0 + t) * K + g * kLinGroup + 16u * piece);
+    float s = 1.0f;
+    if constexpr (kFold) s = ue8m0_f32(ld1(rsx, (tok0 + t) * G + g)) * ue8m0_f32(ld1(rsw, sbrow + g));
+    v4u *dst = reinterpret_cast<v4u *>(lin_x + (size_t(t) * row_elems + c * kLinGroup + 16u * piece) * 2u);
+    dst[0] = e4m3x4_bf16s(codes.x, codes.y, s);
+    dst[1] = e4m3x4_bf16s(codes.z, codes.w, s);
+    if constexpr (!kFold) {
+      if (piece == 0) {
+        const float sa = kXsF32 ? ldf(rsx, 4u * ((tok0 + t) * G + g)) : ue8m0_f32(ld1(rsx, (tok0 + t) * G + g));
+        const float sb = kWsF32 ? ldf(rsw, 4u * (sbrow + g)) : ue8m0_f32(ld1(rsw, sbrow + g));
+        stage_scale[t * cw + c] = sa * sb;
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t my_tok = col < ntok ? col : 0u;
+  const uint8_t *xrow = lin_x + size_t(my_tok) * row_elems * 2u + 32u * h;
+  v16f acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+  const uint32_t sw = lin_swz(col);
+  auto consume = [&](auto slot_tag, uint32_t c) {
+    constexpr int S = decltype(slot_tag)::value;
+    const uint8_t *src = lin_slot<S>() + 128u * col;
+    const uint8_t *xb = xrow + c * (kLinGroup * 2u);
+    v16f part;
+    if constexpr (!kFold) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) part[i] = 0.0f;
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+      const uint4 w = *reinterpret_cast<const uint4 *>(src + 16u * ((2u * q + h) ^ sw));
+      const v8bf b0 = *reinterpret_cast<const v8bf *>(xb + 64u * q);
+      const v8bf b1 = *reinterpret_cast<const v8bf *>(xb + 64u * q + 16u);
+      if constexpr (kFold) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(e4m3x8_bf16(w.x, w.y), b0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(e4m3x8_bf16(w.z, w.w), b1, acc, 0, 0, 0);
+      } else {
+        part = __builtin_amdgcn_mfma_f32_32x32x16_bf16(e4m3x8_bf16(w.x, w.y), b0, part, 0, 0, 0);
+        part = __builtin_amdgcn_mfma_f32_32x32x16_bf16(e4m3x8_bf16(w.z, w.w), b1, part, 0, 0, 0);
+      }
+    }
+    if constexpr (!kFold) {
+      const float s = stage_scale[my_tok * cw + c];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] = fmaf(part[i], s, acc[i]);
+    }
+  };
+  // cw is a multiple of 4 (host): whole rounds of the four-slot ring; a slot
+  // is refilled as soon as it has been read
+#pragma unroll 1
+  for (uint32_t c = 0; c + 4u < cw; c += 4u) {
+    consume(LSlot<0>{}, c);
+    issue(LSlot<0>{}, c + 4u);
+    consume(LSlot<1>{}, c + 1u);
+    issue(LSlot<1>{}, c + 5u);
+    consume(LSlot<2>{}, c + 2u);
+    issue(LSlot<2>{}, c + 6u);
+    consume(LSlot<3>{}, c + 3u);
+    issue(LSlot<3>{}, c + 7u);
+  }
+  consume(LSlot<0>{}, cw - 4u);
+  consume(LSlot<1>{}, cw - 3u);
+  consume(LSlot<2>{}, cw - 2u);
+  consume(LSlot<3>{}, cw - 1u);
+  // pin the accumulators in uniform control flow before the per-lane epilogue
+  asm volatile("" : "+v"(acc));
+  const uint32_t token = tok0 + col;
+  const bool live = col < ntok;
+  const uint32_t rbase = tile * kLinTile + 4u * h;  // + 8 q + v
+  if (splits > 1u) {
+    // The partials are written and read with agent-scope atomics (coherent
+    // across the XCDs' L2s without a whole-L2 write-back, which an
+    // agent-scope release fence per wavefront would cost); the arrival
+    // counts after this wavefront's partial stores have completed.
+    const uint32_t slot = tile * ncb + cb;
+    float *mine = ws.part + (size_t(slot) * splits + sidx) * (kLinTile * kLinTile) + col * kLinTile + 4u * h;
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        __hip_atomic_store(mine + 8 * (i / 4) + (i % 4), acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wavefront's stores are done
+    uint32_t prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(ws.count + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = uint32_t(__shfl(int(prev), 0));
+    if (prev + 1u != splits) return;
+    // last arrival: every other split's partial is complete (and no load of
+    // them may move above this point)
+    asm volatile("" ::: "memory");
+    if (lane == 0) __hip_atomic_store(ws.count + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!live) return;
+    // agent-scope loads, four splits' partials in flight at a time, summed
+    // in split order
+    const Rsrc rp = make_rsrc(ws.part + size_t(slot) * splits * (kLinTile * kLinTile),
+                              splits * (kLinTile * kLinTile) * 4u);
+    const uint32_t lo = 4u * (col * kLinTile + 4u * h);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+    for (uint32_t s0 = 0; s0 < splits; s0 += 4u) {
+      v4u v[4][4];
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j)
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q)  // past the last split: zeros (descriptor range)
+          v[j][q] = __builtin_amdgcn_raw_buffer_load_b128(rp, ((s0 + j) * (kLinTile * kLinTile)) * 4u + lo + 32u * q,
+                                                          0, kCacheAgent);
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j)
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+          acc[4 * q] += __uint_as_float(v[j][q].x);
+          acc[4 * q + 1] += __uint_as_float(v[j][q].y);
+          acc[4 * q + 2] += __uint_as_float(v[j][q].z);
+          acc[4 * q + 3] += __uint_as_float(v[j][q].w);
+        }
+    }
+  }
+  if (!live) return;
+  float *yrow = a.y + size_t(token) * N;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t row = rbase + 8u * uint32_t(i / 4) + uint32_t(i % 4);
+    if (row >= N) continue;
+    float v = acc[i];
+    if (a.bias) v += a.bias[row];
+    if (a.round_bf16) v = bf16_round(v);
+    yrow[row] = v;
+  }
+}
+
+// Chunks per FAST wavefront: the smallest multiple of 4 dividing G that
+// keeps the grid within kFastWaves wavefronts (more K splits fill the GPU for
+// short, wide weights; fewer amortise the ring's prologue), limited by the
+// staged activations, the partial buffer and the counters.
+constexpr uint32_t kFastWaves = 1024;
+
+uint32_t fast_chunks(uint32_t G, uint32_t tiles, uint32_t ncb, uint32_t ntok) {
+  const uint64_t tiles_all = uint64_t(tiles) * ncb;
+  uint32_t best = 4;  // G % 4 == 0 (host): always a divisor, and it fits the stage for 32 tokens
+  for (uint32_t cw = 4; cw <= G; cw += 4) {
+    if (G % cw) continue;
+    if (lin_stage_bytes(ntok, cw) > kLinStageBytes) break;
+    best = cw;
+    const uint64_t splits = G / cw;
+    if (splits > 1 && (tiles_all > kLinMaxCounters ||
+                       tiles_all * splits * kLinTile * kLinTile * sizeof(float) > kLinPartBytes))
+      continue;
+    if (tiles_all * splits <= kFastWaves) return cw;
+  }
+  return best;
+}
+
+}  // namespace
+
+hipError_t launch_act_quant(hipStream_t s, uint32_t rows, uint32_t k, uint32_t group, const float *x, uint8_t *q,
+                            uint8_t *scales) {
+  const uint32_t n = rows * (k / group);
+  k_act_quant<<<(n + 255) / 256, 256, 0, s>>>(n, group, x, q, scales);
+  return hipGetLastError();
+}
+
+template <int MT>
+static hipError_t launch_exact_mt(hipStream_t s, const LinearArgs &a, bool vec) {
+  const uint32_t G = a.groups;
+  const uint32_t R = G >= 256u ? 1u : 256u / G;
+  const dim3 grid((a.n + R - 1) / R, (a.m + MT - 1) / MT);
+  const size_t lds = sizeof(float) * MT * R * G;
+  if (vec)
+    k_linear_exact<MT, true><<<grid, 256, lds, s>>>(a);
+  else
+    k_linear_exact<MT, false><<<grid, 256, lds, s>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_fp8_linear(hipStream_t s, const LinearArgs &a, int mode, const LinearWorkspace &ws) {
+  const bool fast = mode == S14_MODE_FAST && a.k % (4u * kLinGroup) == 0u;
+  if (fast) {
+    const uint32_t tiles = (a.n + kLinTile - 1) / kLinTile, ncb = (a.m + kLinTile - 1) / kLinTile;
+    const uint32_t ntok = min(a.m, kLinTile);
+    const uint32_t cw = fast_chunks(a.groups, tiles, ncb, ntok);
+    const uint32_t splits = a.groups / cw;
+    const dim3 grid(tiles, splits, ncb);
+    const size_t lds = lin_stage_bytes(ntok, cw);
+    if (a.x_scale_f32 && a.w_scale_f32)
+      k_linear_fast<true, true><<<grid, 64, lds, s>>>(a, ws, cw, splits);
+    else if (a.x_scale_f32)
+      k_linear_fast<true, false><<<grid, 64, lds, s>>>(a, ws, cw, splits);
+    else if (a.w_scale_f32)
+      k_linear_fast<false, true><<<grid, 64, lds, s>>>(a, ws, cw, splits);
+    else
+      k_linear_fast<false, false><<<grid, 64, lds, s>>>(a, ws, cw, splits);
+    return hipGetLastError();
+  }
+  const bool vec = a.k % 16u == 0u &&
+                   ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.w)) & 15u) == 0u;
+  if (a.m == 1) return launch_exact_mt<1>(s, a, vec);
+  if (a.m == 2) return launch_exact_mt<2>(s, a, vec);
+  if (a.m <= 4) return launch_exact_mt<4>(s, a, vec);
+  return launch_exact_mt<8>(s, a, vec);
+}
+
+}  // namespace s14

@@ -89,22 +89,6 @@ __global__ __launch_bounds__(256) void k_requant_x(uint32_t tokens, const float 
   S[size_t(t) * groups + g] = uint8_t(code);
 }
 
-// The same requant in natural layout (the standalone dispatch): rows x k,
-// groups of 32 along k.
-__global__ __launch_bounds__(256) void k_requant_rows(uint32_t rows, uint32_t k, const float *__restrict__ X,
-                                                      uint8_t *__restrict__ Q, uint8_t *__restrict__ S) {
-  const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
-  const uint32_t groups = k / kQGroup;
-  if (gid >= rows * groups) return;
-  const float *src = X + size_t(gid) * kQGroup;  // group gid of the row-major matrix
-  float amax = 0.0f;
-  for (int i = 0; i < 32; ++i) amax = fabsf(src[i]) > amax ? fabsf(src[i]) : amax;
-  const uint32_t code = requant_code(amax);
-  const float inv = __uint_as_float((254u - code) << 23);
-  for (int i = 0; i < 32; ++i) Q[size_t(gid) * kQGroup + i] = uint8_t(e4m3_rne_sat(__fmul_rn(src[i], inv)));
-  S[gid] = uint8_t(code);
-}
-
 // ---------------------------------------------------------------------------
 // routing and grouping
 // ---------------------------------------------------------------------------
@@ -647,13 +631,6 @@ __global__ __launch_bounds__(256) void k_prefill_combine(PrefillArgs a, PrefillW
 }
 
 }  // namespace
-
-hipError_t launch_requant_e4m3(hipStream_t s, uint32_t rows, uint32_t k, const float *x, uint8_t *q,
-                               uint8_t *scales) {
-  const uint32_t n = rows * (k / kQGroup);
-  k_requant_rows<<<(n + 255) / 256, 256, 0, s>>>(rows, k, x, q, scales);
-  return hipGetLastError();
-}
 
 hipError_t launch_prefill(hipStream_t s, const PrefillArgs &a, const PrefillWorkspace &ws) {
   const uint32_t T = a.tokens;

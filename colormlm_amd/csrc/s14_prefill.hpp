@@ -75,9 +75,5 @@ struct PrefillWorkspace {
 };
 
 hipError_t launch_prefill(hipStream_t s, const PrefillArgs &a, const PrefillWorkspace &ws);
-// e4m3 requant of a row-major [rows, k] f32 matrix, groups of 32 along k
-// (natural layout): q [rows, k], scales [rows, k/32] E8M0.
-hipError_t launch_requant_e4m3(hipStream_t s, uint32_t rows, uint32_t k, const float *x, uint8_t *q,
-                               uint8_t *scales);
 
 }  // namespace s14

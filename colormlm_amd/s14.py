@@ -521,6 +521,43 @@ def requant_e4m3(ctx: Context, rows: int, k: int, x, q, scales, stream=None) -> 
     check(lib().s14_requant_e4m3(ctx.handle, _stream(stream), rows, k, _ptr(x), _ptr(q), _ptr(scales)))
 
 
+def act_quant_e4m3(ctx: Context, x, q, scales, group: int = 128, stream=None) -> None:
+    """The official activation quant (l42_reference.py:390-403): x f32
+    [rows, k] -> q e4m3 [rows, k] and E8M0 codes [rows, k / group]."""
+    rows, k = (1, x.shape[0]) if x.dim() == 1 else (x.shape[0], x.shape[-1])
+    check(lib().s14_act_quant_e4m3(ctx.handle, _stream(stream), rows, k, group, _ptr(x), _ptr(q), _ptr(scales)))
+
+
+def fp8_linear(
+    ctx: Context,
+    x,
+    x_scale,
+    weight,
+    weight_scale,
+    y,
+    bias=None,
+    round_bf16: bool = False,
+    mode: int = EXACT,
+    stream=None,
+) -> None:
+    """fp8_linear (fp8.py:111-193): x e4m3 codes [m, k] (uint8), weight
+    [n, k]; scales uint8 UE8M0 codes or float32, [m, ceil(k/128)] and
+    [ceil(n/128), ceil(k/128)]; y float32 [m, n]."""
+    m, k = (1, x.shape[0]) if x.dim() == 1 else (x.shape[0], x.shape[-1])
+    n = weight.shape[0]
+
+    def sdt(t):
+        return N.S14_SCALE_F32 if str(t.dtype).endswith("float32") else N.S14_SCALE_UE8M0
+
+    flags = N.S14_LINEAR_ROUND_BF16 if round_bf16 else 0
+    check(
+        lib().s14_fp8_linear(
+            ctx.handle, _stream(stream), m, n, k, buffer(x), buffer(x_scale), sdt(x_scale), buffer(weight),
+            buffer(weight_scale), sdt(weight_scale), buffer(bias), buffer(y), flags, mode
+        )
+    )
+
+
 def fill_mxfp4_page(
     ctx: Context,
     page,
@@ -544,6 +581,8 @@ def fill_mxfp4_page(
 __all__ = [
     "EXACT",
     "OFFICIAL",
+    "act_quant_e4m3",
+    "fp8_linear",
     "FAST",
     "Context",
     "S14MatvecShape",

@@ -361,6 +361,55 @@ int s14_requant_e4m3(s14_ctx *ctx, void *stream, uint32_t rows, uint32_t k, cons
                      uint8_t *q, uint8_t *scales);
 
 /* ======================================================================
+ * Adjacent FP8 projections: activation-quantised FP8 linear
+ * ====================================================================== */
+
+/* The official activation quant (l42_reference.py:390-403,
+ * _activation_quant): x f32 [rows, k] -> q e4m3 [rows, k] (RNE,
+ * saturating at 448) and E8M0 scale codes [rows, k / group], one scale
+ * 2^ceil(log2(max(amax, 1e-4) / 448)) per group of `group` consecutive
+ * values; group is 32, 64 or 128 and divides k (the reference raises
+ * otherwise).  Group 128 feeds s14_fp8_linear; s14_requant_e4m3 is group
+ * 32.  Bit-identical to the CPU oracle's requant. */
+int s14_act_quant_e4m3(s14_ctx *ctx, void *stream, uint32_t rows, uint32_t k, uint32_t group,
+                       const float *x, uint8_t *q, uint8_t *scales);
+
+/* Round each output to bf16 (as an f32 value): the official linear's
+ * output rounding (l42_reference.py:405-411, _linear_fp8). */
+enum { S14_LINEAR_ROUND_BF16 = 1 };
+
+/* fp8_linear (local_s14_primitives/fp8.py:111-193): y [m, n] f32 from
+ *   x            e4m3 codes [m, k]
+ *   x_scale      [m, ceil(k/128)]  UE8M0 codes or f32 (x_scale_dtype)
+ *   weight       e4m3 codes [n, k]
+ *   weight_scale [ceil(n/128), ceil(k/128)]  UE8M0 codes or f32, one per
+ *                128 x 128 weight tile
+ *   bias         f32 [n], or ptr NULL for none
+ * y[t][r] = sum over 128-k groups g, ascending, of
+ *   partial_g = sum_k (dec(x) * x_scale[t][g]) * (dec(w) * w_scale[r/128][g])
+ * (acc = 0; acc += partial_g; then acc += bias[r]), f32 throughout.  A
+ * ragged last group (k % 128 != 0) holds the remaining k.
+ *
+ * S14_MODE_EXACT sums each group's products k ascending (multiply, then
+ * add; the reference's addmm leaves that order to the BLAS): bit-identical
+ * to the CPU oracle's s14o_fp8_linear.  S14_MODE_FAST computes the group
+ * dot products on the MFMA (within the reference's own 2e-5 relative
+ * tolerance of it); it needs k % 512 == 0 and otherwise runs the EXACT
+ * kernel.  FAST keeps split-K partials and arrival counters in a 32 MiB
+ * context workspace allocated on the first FAST call: FAST calls on one
+ * context must not overlap (serialise them on one stream).
+ *
+ * Errors (fp8.py:141-171): S14_ERR_SHAPE for m, n or k zero, k > 131072,
+ * or sizes past 32-bit addressing; S14_ERR_CAPACITY for a buffer smaller
+ * than its shape; S14_ERR_INVALID for NULL buffers, an unknown scale dtype,
+ * flag or mode.  E4M3FN NaN codes (0x7f, 0xff) are the caller's to reject
+ * first (s14_validate_e4m3fn_codes; fp8.py:73-75 raises on them), as are
+ * non-finite f32 scales (fp8.py:43-44). */
+int s14_fp8_linear(s14_ctx *ctx, void *stream, uint32_t m, uint32_t n, uint32_t k, s14_buffer x,
+                   s14_buffer x_scale, int x_scale_dtype, s14_buffer weight, s14_buffer weight_scale,
+                   int weight_scale_dtype, s14_buffer bias, s14_buffer y, int flags, int mode);
+
+/* ======================================================================
  * Synthetic page fill (bench / tests): integer hash, same spec as the
  * oracle's generator, computed on the device.
  * ====================================================================== */

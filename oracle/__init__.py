@@ -91,6 +91,7 @@ def _declare(L):
         "s14o_route_hash": (I, [U32, U32, P, P, P, P, I, U32, F, P, P, P]),
         "s14o_expert_official": (None, [U32, U32, P, P, P, F, I, P]),
         "s14o_moe_layer_official": (None, [U32, U32, P, U32, P, P, P, P, P, P]),
+        "s14o_fp8_linear": (None, [U32, U32, U32, P, P, I, P, P, I, P, I, P]),
         "s14o_route_valid": (I, [P, P, U32, U32, F]),
         "s14o_error_stats_compute": (None, [C.c_size_t, P, P, C.POINTER(ErrorStats)]),
         "s14o_requant_e4m3": (None, [U32, U32, U32, P, P, P]),
@@ -319,6 +320,27 @@ def route_valid(ids, w, n_experts=256, route_scale=1.0) -> bool:
     ids = np.ascontiguousarray(ids, dtype=np.uint16)
     w = _f32(w)
     return bool(lib().s14o_route_valid(_p(ids), _p(w), ids.size, n_experts, float(route_scale)))
+
+
+def fp8_linear(x, x_scale, w, w_scale, bias=None, round_bf16=False) -> np.ndarray:
+    """fp8_linear (fp8.py:111-193) with each group's products summed k
+    ascending: x, w e4m3 codes [m, k] / [n, k]; scales UE8M0 codes (uint8)
+    or float32, [m, ceil(k/128)] and [ceil(n/128), ceil(k/128)]."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.uint8)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    m, k = x.shape
+    n = w.shape[0]
+    assert w.shape[1] == k
+    g = (k + 127) // 128
+    xs = np.ascontiguousarray(np.atleast_2d(x_scale))
+    ws = np.ascontiguousarray(np.atleast_2d(w_scale))
+    assert xs.shape == (m, g) and ws.shape == ((n + 127) // 128, g)
+    assert xs.dtype in (np.uint8, np.float32) and ws.dtype in (np.uint8, np.float32)
+    b = None if bias is None else _f32(bias)
+    y = np.empty((m, n), dtype=np.float32)
+    lib().s14o_fp8_linear(m, n, k, _p(x), _p(xs), int(xs.dtype == np.float32), _p(w), _p(ws),
+                          int(ws.dtype == np.float32), None if b is None else _p(b), int(bool(round_bf16)), _p(y))
+    return y
 
 
 def error_stats(actual, expected) -> dict:

@@ -530,3 +530,34 @@ void s14o_moe_layer_official(uint32_t hidden, uint32_t inter, const float *x, ui
   free(out);
   free(acc);
 }
+
+static float linear_scale(const void *s, size_t i, int is_f32) {
+  return is_f32 ? ((const float *)s)[i] : s14o_ue8m0(((const uint8_t *)s)[i]);
+}
+
+void s14o_fp8_linear(uint32_t m, uint32_t n, uint32_t k, const uint8_t *x, const void *x_scale, int x_scale_f32,
+                     const uint8_t *w, const void *w_scale, int w_scale_f32, const float *bias, int round_bf16,
+                     float *y) {
+  const uint32_t groups = (k + 127) / 128;
+#pragma omp parallel for schedule(static)
+  for (int64_t rr = 0; rr < (int64_t)n; ++rr) {
+    const uint32_t r = (uint32_t)rr;
+    for (uint32_t t = 0; t < m; ++t) {
+      float acc = 0.0f;
+      for (uint32_t g = 0; g < groups; ++g) {
+        const float sa = linear_scale(x_scale, (size_t)t * groups + g, x_scale_f32);
+        const float sb = linear_scale(w_scale, (size_t)(r / 128) * groups + g, w_scale_f32);
+        const uint32_t k0 = 128 * g, k1 = k0 + 128 < k ? k0 + 128 : k;
+        float partial = 0.0f;
+        for (uint32_t kk = k0; kk < k1; ++kk) {
+          const float a = s14o_e4m3fn(x[(size_t)t * k + kk]) * sa;
+          const float b = s14o_e4m3fn(w[(size_t)r * k + kk]) * sb;
+          partial += a * b;
+        }
+        acc += partial;
+      }
+      if (bias) acc += bias[r];
+      y[(size_t)t * n + r] = round_bf16 ? bf16_round(acc) : acc;
+    }
+  }
+}

@@ -31,6 +31,11 @@
  *   swiglu/router libm identities; top-k against numpy argsort; tie rule.
  *   layer/block   composition identities against the pinned parts and f64.
  *   requant       RNE e4m3 encoder against torch's float8_e4m3fn cast.
+ *   fp8_linear    the reference's own known-answer case (torch-seeded codes,
+ *                 tolerance 2e-5 against decoded x @ decoded w.T); f64 brute
+ *                 force; a group-order construction (per-group partials
+ *                 differ from one flat sum) in closed form; power-of-two
+ *                 scale identities.
  */
 #ifndef S14_ORACLE_H
 #define S14_ORACLE_H
@@ -175,6 +180,19 @@ void s14o_dequant_requant(uint32_t rows, uint32_t k, uint32_t group, const uint8
  * order, so parity for this config is a measured tolerance. */
 void s14o_mxfp4_expert_down_requant(uint32_t hidden, uint32_t inter, uint32_t group,
                                     const float *x, const s14o_mxfp4_expert *e, float *down);
+
+/* ---- activation-quantised FP8 linear (local_s14_primitives/fp8.py:111-193) ----
+ * x e4m3 [m, k] with scales [m, G], weight e4m3 [n, k] with scales
+ * [ceil(n/128), G], G = ceil(k/128); a scale is a UE8M0 code (f32 flag 0)
+ * or an f32 (flag 1).  For each output: acc = 0; for each 128-k group g
+ * ascending: partial = sum over the group's k of (e4m3(x) * sa) * (e4m3(w) *
+ * sb), each product and sum rounded to f32; acc += partial (fp8.py:173-191,
+ * one addmm per group); then acc += bias (if not NULL); y = acc, rounded to
+ * bf16 if round_bf16.  The reference's addmm sums a group's products in its
+ * BLAS's order; this oracle fixes k ascending. */
+void s14o_fp8_linear(uint32_t m, uint32_t n, uint32_t k, const uint8_t *x, const void *x_scale, int x_scale_f32,
+                     const uint8_t *w, const void *w_scale, int w_scale_f32, const float *bias, int round_bf16,
+                     float *y);
 
 int s14o_num_threads(void);
 void s14o_set_num_threads(int n);
