@@ -95,7 +95,8 @@ def parse():
                     help="only run a plain 256 MiB device copy 10 times (the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     ap.add_argument("--prefill-steps", type=int, default=20)
-    ap.add_argument("--only", choices=["k1", "k8", "config0", "config1", "prefill", "linear", "all"], default="all",
+    ap.add_argument("--only", choices=["k1", "k8", "config0", "config1", "prefill", "linear", "upload", "all"],
+                    default="all",
                     help="restrict the timed work (for profiler runs)")
     return ap.parse_args()
 
@@ -289,8 +290,13 @@ def main() -> int:
     if only in ("linear", "all"):
         progress("adjacent FP8 projections (fp8_linear)")
         linear = bench_linear(args, ctx, timer, torch, s14)
+    upload = None
+    if only in ("upload", "all"):
+        progress("page upload (ExpertLoader)")
+        upload = bench_upload(args, ctx, torch, np, N, step_k1(s14.EXACT))
     if only != "all" and only not in ("k1",):
-        print(json.dumps({"only": only, "legs": out, "prefill": prefill, "fp8_linear": linear}), flush=True)
+        print(json.dumps({"only": only, "legs": out, "prefill": prefill, "fp8_linear": linear, "upload": upload}),
+              flush=True)
         return 0
 
     main_r = out[args.mode]
@@ -349,6 +355,7 @@ def main() -> int:
         "other_mode": {k: v for k, v in out.items() if k != args.mode},
         "prefill": prefill,
         "fp8_linear": linear,
+        "upload": upload,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
@@ -426,6 +433,93 @@ def bench_linear(args, ctx, timer, torch, s14):
                 progress(f"  {name} m={m} {mode_name}: {us:.2f} us, {gbps:.0f} GB/s")
         del W, WS
         torch.cuda.synchronize()
+    return res
+
+
+UPLOAD_PAGES = 48  # 642 MB per batch
+
+
+def bench_upload(args, ctx, torch, np, N, layer_step):
+    """The page upload path (ExpertLoader, expert_loader.rs:299-360): a batch
+    of UPLOAD_PAGES distinct pages from host memory (the enqueue_from_buf
+    path: bytes already read) through a ring of pinned staging slots into a
+    VramPool on the context's copy stream, until the last transfer fence.
+    Alone, then while the K=1 exact layer replays from a HIP graph on the
+    compute side; overlap = (t_layer + t_upload - t_both) / min(t_layer,
+    t_upload), 1 when the two hide each other completely."""
+    from colormlm_amd.pool import ExpertKey, ExpertLoader, VramPool
+
+    rng = np.random.default_rng(args.seed)
+    sources = [rng.integers(0, 256, PAGE, dtype=np.uint8) for _ in range(8)]  # cycled: 107 MB of distinct bytes
+    pool = VramPool(UPLOAD_PAGES, PAGE, ctx)
+    res = {"pages": UPLOAD_PAGES, "page_bytes": PAGE, "sources": "host memory (numpy), 8 distinct 13.4 MB buffers"}
+    batch = [0]
+
+    def upload(loader):
+        b = batch[0]
+        batch[0] += 1
+        keys = [ExpertKey(b % 60, 0, i) for i in range(UPLOAD_PAGES)]
+        t0 = time.perf_counter()
+        loader.batch_enqueue_from_bufs(pool, keys, [sources[i % 8] for i in range(UPLOAD_PAGES)])
+        loader.wait_all(pool)
+        return time.perf_counter() - t0
+
+    for depth in (2, 4, 8):
+        loader = ExpertLoader(ctx, depth, PAGE)
+        upload(loader)  # warm: pool slots and staging touched once
+        ts = [upload(loader) for _ in range(max(3, args.trials))]
+        t = statistics.median(ts)
+        res[f"depth{depth}"] = {"s_per_batch": t, "h2d_gbps": UPLOAD_PAGES * PAGE / t / 1e9}
+        loader.destroy()
+        progress(f"  upload depth {depth}: {UPLOAD_PAGES * PAGE / t / 1e9:.1f} GB/s")
+    # raw copy-engine rate from pinned memory, for comparison
+    src = torch.empty(UPLOAD_PAGES * PAGE, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(UPLOAD_PAGES * PAGE, dtype=torch.uint8, device="cuda")
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    res["pinned_memcpy_gbps"] = UPLOAD_PAGES * PAGE / (time.perf_counter() - t0) / 1e9
+    del src, dst
+    # overlap with the layer: 100 K=1 exact steps per graph replay
+    loader = ExpertLoader(ctx, 4, PAGE)
+    upload(loader)
+    for i in range(3):
+        layer_step(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(100):
+            layer_step(i)
+    g.replay()
+    torch.cuda.synchronize()
+    t_up = statistics.median([upload(loader) for _ in range(3)])
+    t0 = time.perf_counter()
+    for _ in range(8):
+        g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, round(8 * t_up / (time.perf_counter() - t0)))  # layer time ~ upload time
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    t_layer = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    t_up_both = upload(loader)
+    torch.cuda.synchronize()
+    t_both = time.perf_counter() - t0
+    loader.destroy()
+    del g
+    res["overlap"] = {"layer_steps": 100 * reps, "t_layer_s": t_layer, "t_upload_s": t_up, "t_both_s": t_both,
+                      "upload_during_layer_gbps": UPLOAD_PAGES * PAGE / t_up_both / 1e9,
+                      "layer_us_per_token_during_upload": t_both / (100 * reps) * 1e6,
+                      "overlap": (t_layer + t_up - t_both) / min(t_layer, t_up)}
+    progress(f"  overlap {res['overlap']['overlap']:.2f} (layer {t_layer * 1e3:.1f} ms, upload {t_up * 1e3:.1f} ms, "
+             f"both {t_both * 1e3:.1f} ms)")
+    pool.destroy()
     return res
 
 

@@ -285,7 +285,21 @@ SIGNATURES = {
     "s14_moe_pages_release_after_compute_fence": (I, [P, P]),
     "s14_moe_pages_cancel": (I, [P, P]),
     "s14_route_load_batch_shared_reservation": (I, [P, C.POINTER(LoadingReservationC)]),
+    "s14_loader_create": (I, [P, U32, U64, C.POINTER(P)]),
+    "s14_loader_destroy": (None, [P]),
+    "s14_loader_enqueue": (I, [P, P, ExpertKeyC, U64, P, P, C.POINTER(U32)]),
+    "s14_loader_enqueue_from_buf": (I, [P, P, ExpertKeyC, P, U64, C.POINTER(U32)]),
+    "s14_loader_wait_all": (I, [P, P]),
+    "s14_loader_batch_enqueue": (I, [P, P, C.POINTER(ExpertKeyC), C.POINTER(U64), C.c_size_t, P, P, C.POINTER(U32)]),
+    "s14_loader_batch_enqueue_from_bufs": (
+        I,
+        [P, P, C.POINTER(ExpertKeyC), C.POINTER(P), C.POINTER(U64), C.c_size_t, C.POINTER(U32)],
+    ),
+    "s14_loader_stats": (I, [P, C.POINTER(U64), C.POINTER(U64), C.POINTER(U32)]),
 }
+
+# s14_read_fn: int (*)(void *user, s14_expert_key key, void *dst, uint64_t bytes)
+READ_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, ExpertKeyC, C.c_void_p, C.c_uint64)
 
 _lib = None
 

@@ -30,7 +30,7 @@ CSRC = PKG / "csrc"
 OUT = PKG / "lib" / "libs14hip.so"
 OBJ = PKG / "lib" / "obj"
 DEVICE_SOURCES = ["s14_device.hip", "s14_block.hip", "s14_prefill.hip", "s14_static.hip", "s14_linear.hip"]
-HOST_SOURCES = ["s14_api.cpp", "s14_pool.cpp"]
+HOST_SOURCES = ["s14_api.cpp", "s14_pool.cpp", "s14_loader.cpp"]
 SOURCES = DEVICE_SOURCES + HOST_SOURCES
 ARCH = os.environ.get("S14_OFFLOAD_ARCH", "gfx950")
 NO_PACKED_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

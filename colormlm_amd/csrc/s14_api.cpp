@@ -161,6 +161,7 @@ extern "C" void s14_ctx_destroy(s14_ctx *ctx) {
 }
 
 extern "C" void *s14_ctx_compute_stream(s14_ctx *ctx) { return ctx ? ctx->compute : nullptr; }
+int s14::ctx_device(const s14_ctx *ctx) { return ctx->device; }
 extern "C" void *s14_ctx_copy_stream(s14_ctx *ctx) { return ctx ? ctx->copy : nullptr; }
 
 extern "C" int s14_ctx_synchronize(s14_ctx *ctx) {

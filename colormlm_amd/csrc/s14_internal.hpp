@@ -26,6 +26,9 @@ int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, con
 // clears them): S14_OK, or the error they stand for.
 int read_launch_status(const Workspace &ws, int device);
 
+// The device a context was created on.
+int ctx_device(const s14_ctx *ctx);
+
 // Records `msg` as this thread's last error and returns `code`.
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();

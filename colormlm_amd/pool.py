@@ -3,6 +3,7 @@
 Mirrors, name for name, the reference's Rust interface so callers and tests
 read the same:
   VramPool                 scheduler/ssd_inference/src/vram_pool.rs:62-405
+  ExpertLoader             scheduler/ssd_inference/src/expert_loader.rs:26-474
   S14MoePages              scheduler/ssd_inference/src/s14_vulkan.rs:703-819
   RouteDecision.validate_for  scheduler/s14_runner/src/runner.rs:128-180
 All state lives in the C++ library; this module only marshals arguments and
@@ -187,6 +188,92 @@ class VramPool:
         return Fence(fence, keepalive=buf)
 
 
+class ExpertLoader:
+    """ExpertLoader (expert_loader.rs:26-474): a pinned staging ring of
+    ``pipeline_depth`` slots feeding the VRAM pool over the context's copy
+    stream, one transfer fence per slot.
+
+    ``reader(key, dst_view)`` fills a writable memoryview of the page's size
+    (the role of ExpertReader::read_into) and returns nothing; an exception
+    cancels the reservation and surfaces as S14Error."""
+
+    def __init__(self, ctx, pipeline_depth: int, staging_bytes: int):
+        self._h = C.c_void_p()
+        check(lib().s14_loader_create(ctx.handle, pipeline_depth, staging_bytes, C.byref(self._h)))
+        self.pipeline_depth = pipeline_depth
+        self.staging_bytes = staging_bytes
+
+    def destroy(self) -> None:
+        if self._h:
+            lib().s14_loader_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+    @staticmethod
+    def _reader(reader):
+        def cb(user, key, dst, nbytes):
+            try:
+                reader(ExpertKey.from_c(key), (C.c_ubyte * nbytes).from_address(dst))
+                return 0
+            except Exception:
+                return 1
+
+        return N.READ_FN(cb)
+
+    def enqueue(self, pool: VramPool, key: ExpertKey, nbytes: int, reader) -> int:
+        """enqueue (expert_loader.rs:163-284): the page's VRAM slot."""
+        slot = C.c_uint32()
+        fn = self._reader(reader)
+        check(lib().s14_loader_enqueue(self._h, pool.handle, key.c(), nbytes, fn, None, C.byref(slot)))
+        return int(slot.value)
+
+    def enqueue_from_buf(self, pool: VramPool, key: ExpertKey, data) -> int:
+        """enqueue_from_buf (expert_loader.rs:362-442): bytes already in host memory."""
+        import numpy as np
+
+        buf = np.ascontiguousarray(np.frombuffer(data, dtype=np.uint8))
+        slot = C.c_uint32()
+        check(lib().s14_loader_enqueue_from_buf(self._h, pool.handle, key.c(), buf.ctypes.data, buf.nbytes,
+                                                C.byref(slot)))
+        return int(slot.value)
+
+    def wait_all(self, pool: VramPool) -> None:
+        check(lib().s14_loader_wait_all(self._h, pool.handle))
+
+    def batch_enqueue(self, pool: VramPool, keys: Sequence[ExpertKey], sizes: Sequence[int], reader) -> List[int]:
+        """batch_enqueue (expert_loader.rs:299-360): VRAM slots in input order."""
+        n = len(keys)
+        kc = (N.ExpertKeyC * max(1, n))(*[k.c() for k in keys])
+        sz = (C.c_uint64 * max(1, n))(*sizes)
+        out = (C.c_uint32 * max(1, n))()
+        fn = self._reader(reader)
+        check(lib().s14_loader_batch_enqueue(self._h, pool.handle, kc, sz, n, fn, None, out))
+        return [int(out[i]) for i in range(n)]
+
+    def batch_enqueue_from_bufs(self, pool: VramPool, keys: Sequence[ExpertKey], datas) -> List[int]:
+        """batch_enqueue with every page's bytes in host memory."""
+        import numpy as np
+
+        bufs = [np.ascontiguousarray(np.frombuffer(d, dtype=np.uint8)) for d in datas]
+        n = len(keys)
+        kc = (N.ExpertKeyC * max(1, n))(*[k.c() for k in keys])
+        ptrs = (C.c_void_p * max(1, n))(*[b.ctypes.data for b in bufs])
+        sz = (C.c_uint64 * max(1, n))(*[b.nbytes for b in bufs])
+        out = (C.c_uint32 * max(1, n))()
+        check(lib().s14_loader_batch_enqueue_from_bufs(self._h, pool.handle, kc, ptrs, sz, n, out))
+        return [int(out[i]) for i in range(n)]
+
+    def stats(self) -> dict:
+        loads, nbytes, inflight = C.c_uint64(), C.c_uint64(), C.c_uint32()
+        check(lib().s14_loader_stats(self._h, C.byref(loads), C.byref(nbytes), C.byref(inflight)))
+        return {"stat_loads": int(loads.value), "stat_bytes": int(nbytes.value), "in_flight": int(inflight.value)}
+
+
 class _DeviceBytes:
     """__cuda_array_interface__ of a byte range of device memory."""
 
@@ -369,6 +456,7 @@ __all__ = [
     "SlotLease",
     "LoadingReservation",
     "VramPool",
+    "ExpertLoader",
     "Fence",
     "RouterKind",
     "GraphProfile",

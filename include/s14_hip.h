@@ -502,6 +502,50 @@ int s14_fence_wait(s14_fence *fence);
 void s14_fence_destroy(s14_fence *fence);
 
 /* ======================================================================
+ * Expert page uploader — ExpertLoader, expert_loader.rs:1-474
+ * ====================================================================== */
+
+/* A ring of pipeline_depth pinned host staging slots (hipHostMalloc) of
+ * staging_bytes each, one hipEvent transfer fence per slot, copies on ctx's
+ * copy stream (ExpertLoader::new_with_staging_bytes, expert_loader.rs:51-104).
+ * A loader is used by one thread at a time, like the reference's &mut self. */
+typedef struct s14_loader s14_loader;
+/* Fills dst with the page of `key` (bytes long); returns 0 on success.  The
+ * role of ExpertReader::read_into (expert_loader.rs:209-218). */
+typedef int (*s14_read_fn)(void *user, s14_expert_key key, void *dst, uint64_t bytes);
+int s14_loader_create(s14_ctx *ctx, uint32_t pipeline_depth, uint64_t staging_bytes, s14_loader **out);
+/* Waits only for submitted transfers, then frees the ring (expert_loader.rs:444-458). */
+void s14_loader_destroy(s14_loader *loader);
+/* enqueue (expert_loader.rs:163-284): a Ready key returns its slot; a key
+ * still in the ring has its transfer completed and returns its slot;
+ * otherwise the next ring slot's previous transfer is completed (fence wait,
+ * then mark_ready), a Loading slot is reserved (may evict), the page is read
+ * into the staging slot and its hipMemcpyAsync and fence are submitted.  The
+ * page is visible through s14_pool_lookup only after its fence completes
+ * (a later enqueue reusing the ring slot, s14_loader_wait_all, or a repeat
+ * enqueue of the key).  A failed read cancels the reservation.
+ * S14_ERR_CAPACITY if bytes exceed the staging slot or the pool slot. */
+int s14_loader_enqueue(s14_loader *loader, s14_pool *pool, s14_expert_key key, uint64_t bytes,
+                       s14_read_fn read, void *user, uint32_t *slot_out);
+/* enqueue_from_buf (expert_loader.rs:362-442): the same from bytes already in host memory. */
+int s14_loader_enqueue_from_buf(s14_loader *loader, s14_pool *pool, s14_expert_key key, const void *data,
+                                uint64_t bytes, uint32_t *slot_out);
+/* wait_all (expert_loader.rs:286-291): complete and publish every transfer in the ring. */
+int s14_loader_wait_all(s14_loader *loader, s14_pool *pool);
+/* batch_enqueue (expert_loader.rs:299-360): settle the ring, deduplicate the
+ * keys, reject more distinct keys than the pool has slots (S14_ERR_CAPACITY),
+ * then enqueue in waves no deeper than the ring, draining between waves; the
+ * last wave stays in flight.  slots_out[i] is the VRAM slot of keys[i]. */
+int s14_loader_batch_enqueue(s14_loader *loader, s14_pool *pool, const s14_expert_key *keys,
+                             const uint64_t *bytes, size_t n, s14_read_fn read, void *user, uint32_t *slots_out);
+/* The same with every page's bytes already in host memory (data[i], bytes[i]). */
+int s14_loader_batch_enqueue_from_bufs(s14_loader *loader, s14_pool *pool, const s14_expert_key *keys,
+                                       const void *const *data, const uint64_t *bytes, size_t n,
+                                       uint32_t *slots_out);
+/* stat_loads / stat_bytes (expert_loader.rs:38-40) and transfers in flight. */
+int s14_loader_stats(const s14_loader *loader, uint64_t *loads, uint64_t *bytes, uint32_t *in_flight);
+
+/* ======================================================================
  * Route decisions and two-pool page batches — s14_vulkan.rs:500-819
  * ====================================================================== */
 enum { S14_PROFILE_S14_TOP6 = 0, S14_PROFILE_FULL_DEPTH43_TOP6 = 1 };

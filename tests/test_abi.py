@@ -46,3 +46,19 @@ def test_context_creation_fails_cleanly_without_a_gpu(native):
     h = C.c_void_p()
     rc = native.s14_ctx_create(0, C.byref(h))
     assert rc in (N.S14_ERR_HIP, N.S14_ERR_INVALID) and not h.value
+
+
+def test_loader_argument_checks(native):
+    """ExpertLoader::new_with_staging_bytes's checks (expert_loader.rs:57-66),
+    before any device call."""
+    import ctypes as C
+
+    from colormlm_amd import _native as N
+
+    out = C.c_void_p()
+    assert N.lib().s14_loader_create(None, 2, 1 << 20, C.byref(out)) == N.S14_ERR_INVALID
+    assert N.lib().s14_loader_create(C.c_void_p(1), 0, 1 << 20, C.byref(out)) == N.S14_ERR_INVALID
+    assert "pipeline depth" in N.last_error()
+    assert N.lib().s14_loader_create(C.c_void_p(1), 2, 0, C.byref(out)) == N.S14_ERR_INVALID
+    assert "staging slot size" in N.last_error()
+    assert out.value is None
