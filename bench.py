@@ -11,7 +11,10 @@ wq_a matvec) and config 4 (the 512-token prefill).
 Every leg times the EXACT (oracle-order, bit-identical) kernels and the FAST
 (order-changed) ones.  Each leg's figure is the median of --trials trials;
 a trial times exactly --steps steps (after --warmup untimed ones) between
-two device synchronisations with events on the launch stream.  Inputs are
+two device synchronisations with events on the launch stream.  The steps of
+a trial are recorded once into a HIP graph and each trial replays it, so
+the figure is the device's time for the steps without the host's launch gap
+(the K=1 and K=8 legs also report the eager, launch-per-step figure).  Inputs are
 resident in HBM before timing: `--layers` layer banks of 257 expert pages
 live in one device arena (a VramPool), and consecutive steps rotate banks,
 pages and tokens so that the working set between reuses (> 1 GB) exceeds the
@@ -250,7 +253,8 @@ def main() -> int:
         r = {}
         if only in ("k1", "all"):
             progress(f"config 2 (K=1) {name}")
-            t = timer.run(step_k1(m), args.steps, args.warmup)
+            t = timer.run_graph(step_k1(m), args.steps, args.warmup)
+            t["eager"] = timer.run(step_k1(m), args.steps, args.warmup)
             st = stages(step_k1(m), args.profile_steps)
             us = t["ms"] * 1e3
             r["k1"] = {"us_per_token": us, "timing": t, "hbm_gbps": layer_bytes_k1() / (us * 1e-6) / 1e9,
@@ -258,7 +262,8 @@ def main() -> int:
             r["k1"]["hbm_frac"] = r["k1"]["hbm_gbps"] / HBM_PEAK_GBPS
         if only in ("k8", "all"):
             progress(f"config 3 (K=8) {name}")
-            t = timer.run(step_k8(m), max(args.steps // 4, 10), max(args.warmup // 4, 5))
+            t = timer.run_graph(step_k8(m), max(args.steps // 4, 10), max(args.warmup // 4, 5))
+            t["eager"] = timer.run(step_k8(m), max(args.steps // 4, 10), max(args.warmup // 4, 5))
             st = stages(step_k8(m), max(args.profile_steps // 4, 8))
             d, ov = block_routes(m)
             ms = t["ms"]
@@ -268,7 +273,7 @@ def main() -> int:
             r["k8"]["hbm_frac"] = r["k8"]["hbm_gbps"] / HBM_PEAK_GBPS
         if only in ("config0", "all"):
             progress(f"config 0 (chain) {name}")
-            t = timer.run(step_chain(m), args.steps, args.warmup)
+            t = timer.run_graph(step_chain(m), args.steps, args.warmup)
             st = stages(step_chain(m), args.profile_steps)
             us = t["ms"] * 1e3
             r["config0"] = {"us_per_chain": us, "timing": t, "hbm_gbps": CHAIN_BYTES / (us * 1e-6) / 1e9,
@@ -341,7 +346,8 @@ def main() -> int:
                         "config 4 prefill reported beside it",
             "mode": args.mode,
             "parity": "bit-identical to the CPU oracle" if args.mode == "exact" else "order-changed f32",
-            "timing": f"median of {args.trials} trials of {args.steps} steps",
+            "timing": f"median of {args.trials} trials, each one replay of a HIP graph of {args.steps} steps "
+                      "(the eager figure, one host launch sequence per step, is in k1.timing.eager)",
             "layer_banks": NL,
             "tokens_rotated": P,
             "layer_bytes_k1": layer_bytes_k1(),
@@ -383,11 +389,10 @@ def bench_config1(args, ctx, timer, torch, np, s14, synth):
         def f(i, ds=ds):
             pipes.cmd_fp8_matvec(ds[(i * 7) % WQA_COPIES])
 
-        t = timer.run(f, args.steps, args.warmup)
+        t = timer.run_graph(f, WQA_COPIES, args.warmup)
         us = t["ms"] * 1e3
         res[name] = {"us_per_matvec": us, "timing": t, "algorithmic_bytes": WQA_BYTES,
-                     "hbm_gbps": WQA_BYTES / (us * 1e-6) / 1e9, "hbm_frac": WQA_BYTES / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
-                     "note": "back-to-back launches from Python: includes the launch gap"}
+                     "hbm_gbps": WQA_BYTES / (us * 1e-6) / 1e9, "hbm_frac": WQA_BYTES / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS}
     return res
 
 
