@@ -628,8 +628,21 @@ __global__ __launch_bounds__(64 * kMaxTokens) void k_route(RouteSpec rs, Workspa
       __hip_atomic_store(&ws.biased[t * kMaxExperts + e], s.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  // this wavefront's stores complete before the count (a device-scope
-  // release fence would write the whole L2 back: measured several us)
+  // Why the last workgroup sees every score without a release/acquire pair:
+  //  1. the scores are agent-scope atomic stores (global_store ... sc1),
+  //     written through to the device's coherence point rather than left
+  //     dirty in this XCD's L2;
+  //  2. s_waitcnt 0 returns only when this wavefront's stores are
+  //     acknowledged there, and the barrier below puts every wavefront's
+  //     wait before thread 0's counter increment;
+  //  3. the counters are agent-scope atomics, performed at that same point,
+  //     so the increment that completes the count comes after every counted
+  //     workgroup's stores;
+  //  4. the gather's loads are agent-scope atomic loads (sc1, served at the
+  //     coherence point, not from a stale L2 line), issued only after the
+  //     last increment returned (they depend on is_last through a barrier).
+  // A device-scope release fence per wavefront would do the same by writing
+  // the whole L2 back (buffer_wbl2), measured at several us per launch.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
