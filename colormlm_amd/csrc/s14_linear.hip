@@ -177,6 +177,8 @@ __shared__ __attribute__((aligned(16))) uint8_t lin_slot1[kLChunkBytes];
 __shared__ __attribute__((aligned(16))) uint8_t lin_slot2[kLChunkBytes];
 __shared__ __attribute__((aligned(16))) uint8_t lin_slot3[kLChunkBytes];
 
+// Each slot is its own LDS array, so the compiler waits for one slot's DMA
+// without draining the others.
 template <int S>
 __device__ __forceinline__ uint8_t *lin_slot() {
   if constexpr (S == 0) return lin_slot0;
@@ -188,6 +190,14 @@ template <int S>
 struct LSlot {
   static constexpr int value = S;
 };
+// f(LSlot<S>{}) for S = B .. E - 1, in order, unrolled
+template <int B, int E, class F>
+__device__ __forceinline__ void for_slots(F &&f) {
+  if constexpr (B < E) {
+    f(LSlot<B>{});
+    for_slots<B + 1, E>(f);
+  }
+}
 
 typedef __attribute__((address_space(3))) void lds_void;
 __device__ __forceinline__ void lin_dma16(Rsrc r, uint8_t *lds, uint32_t off) {
@@ -219,7 +229,7 @@ __device__ __forceinline__ v4u e4m3x4_bf16s(uint32_t w0, uint32_t w1, float s) {
              __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, s, true))};
 }
 
-template <bool kXsF32, bool kWsF32>
+template <bool kXsF32, bool kWsF32, int kRing>
 __global__ __launch_bounds__(64) void k_linear_fast(LinearArgs a, LinearWorkspace ws, uint32_t cw, uint32_t splits) {
   constexpr bool kFold = !kXsF32 && !kWsF32;  // power-of-two scales ride in the bf16 activations
   extern __shared__ __attribute__((aligned(16))) uint8_t lin_x[];  // [ntok][cw * 128] bf16, then [ntok][cw] f32
@@ -249,11 +259,8 @@ __global__ __launch_bounds__(64) void k_linear_fast(LinearArgs a, LinearWorkspac
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j) lin_dma16(rw, dst + 1024u * j, dma_off[j] + kb);
   };
-  // the first chunks' weights are in flight while the activations are staged
-  issue(LSlot<0>{}, 0);
-  issue(LSlot<1>{}, 1);
-  issue(LSlot<2>{}, 2);
-  issue(LSlot<3>{}, 3);
+  // the first kRing chunks' weights are in flight while the activations are staged
+  for_slots<0, kRing>([&](auto sl) { issue(sl, uint32_t(decltype(sl)::value)); });
   // stage: item = (token, chunk, 16-k piece), one 16-byte load per item
   const uint32_t row_elems = cw * kLinGroup;  // bf16 per staged token
   float *stage_scale = reinterpret_cast<float *>(lin_x + size_t(ntok) * row_elems * 2u);
@@ -309,23 +316,17 @@ __global__ __launch_bounds__(64) void k_linear_fast(LinearArgs a, LinearWorkspac
       for (int i = 0; i < 16; ++i) acc[i] = fmaf(part[i], s, acc[i]);
     }
   };
-  // cw is a multiple of 4 (host): whole rounds of the four-slot ring; a slot
-  // is refilled as soon as it has been read
+  // cw is a multiple of kRing (host): whole rounds of the ring; a slot is
+  // refilled as soon as it has been read
 #pragma unroll 1
-  for (uint32_t c = 0; c + 4u < cw; c += 4u) {
-    consume(LSlot<0>{}, c);
-    issue(LSlot<0>{}, c + 4u);
-    consume(LSlot<1>{}, c + 1u);
-    issue(LSlot<1>{}, c + 5u);
-    consume(LSlot<2>{}, c + 2u);
-    issue(LSlot<2>{}, c + 6u);
-    consume(LSlot<3>{}, c + 3u);
-    issue(LSlot<3>{}, c + 7u);
+  for (uint32_t c = 0; c + kRing < cw; c += kRing) {
+    for_slots<0, kRing>([&](auto sl) {
+      constexpr uint32_t S = decltype(sl)::value;
+      consume(sl, c + S);
+      issue(sl, c + kRing + S);
+    });
   }
-  consume(LSlot<0>{}, cw - 4u);
-  consume(LSlot<1>{}, cw - 3u);
-  consume(LSlot<2>{}, cw - 2u);
-  consume(LSlot<3>{}, cw - 1u);
+  for_slots<0, kRing>([&](auto sl) { consume(sl, cw - kRing + uint32_t(decltype(sl)::value)); });
   // pin the accumulators in uniform control flow before the per-lane epilogue
   asm volatile("" : "+v"(acc));
   const uint32_t token = tok0 + col;
@@ -423,6 +424,24 @@ hipError_t launch_act_quant(hipStream_t s, uint32_t rows, uint32_t k, uint32_t g
   return hipGetLastError();
 }
 
+// Slots in flight per wavefront.  Eight (a wavefront's whole K range at the
+// projections' shapes requested at once) measured slower than four at every
+// shape: wq_b 10.7 -> 12.2 us, and 12.7 -> 19.1 us for 8 tokens.
+constexpr int kLinRing = 4;
+
+template <int kRing>
+static void launch_fast_ring(hipStream_t s, const LinearArgs &a, const LinearWorkspace &ws, uint32_t cw,
+                             uint32_t splits, dim3 grid, size_t lds) {
+  if (a.x_scale_f32 && a.w_scale_f32)
+    k_linear_fast<true, true, kRing><<<grid, 64, lds, s>>>(a, ws, cw, splits);
+  else if (a.x_scale_f32)
+    k_linear_fast<true, false, kRing><<<grid, 64, lds, s>>>(a, ws, cw, splits);
+  else if (a.w_scale_f32)
+    k_linear_fast<false, true, kRing><<<grid, 64, lds, s>>>(a, ws, cw, splits);
+  else
+    k_linear_fast<false, false, kRing><<<grid, 64, lds, s>>>(a, ws, cw, splits);
+}
+
 template <int MT>
 static hipError_t launch_exact_mt(hipStream_t s, const LinearArgs &a, bool vec) {
   const uint32_t G = a.groups;
@@ -444,15 +463,7 @@ hipError_t launch_fp8_linear(hipStream_t s, const LinearArgs &a, int mode, const
     const uint32_t cw = fast_chunks(a.groups, tiles, ncb, ntok);
     const uint32_t splits = a.groups / cw;
     const dim3 grid(tiles, splits, ncb);
-    const size_t lds = lin_stage_bytes(ntok, cw);
-    if (a.x_scale_f32 && a.w_scale_f32)
-      k_linear_fast<true, true><<<grid, 64, lds, s>>>(a, ws, cw, splits);
-    else if (a.x_scale_f32)
-      k_linear_fast<true, false><<<grid, 64, lds, s>>>(a, ws, cw, splits);
-    else if (a.w_scale_f32)
-      k_linear_fast<false, true><<<grid, 64, lds, s>>>(a, ws, cw, splits);
-    else
-      k_linear_fast<false, false><<<grid, 64, lds, s>>>(a, ws, cw, splits);
+    launch_fast_ring<kLinRing>(s, a, ws, cw, splits, grid, lin_stage_bytes(ntok, cw));
     return hipGetLastError();
   }
   const bool vec = a.k % 16u == 0u &&

@@ -87,7 +87,11 @@ int s14_validate_e4m3fn_codes(const uint8_t *codes, size_t n, size_t *bad_index)
 typedef struct s14_ctx s14_ctx;
 
 /* Creates a context on `device`: a compute stream, a copy stream and a
- * device workspace sized for the largest layer/block launch. */
+ * device workspace sized for the largest layer/block launch.  The fused
+ * launches of one context share that workspace (pair table, h, route
+ * counters that each launch leaves at zero): launches of one context must
+ * not overlap on the device, so issue them on one stream (or order the
+ * streams with events), and use one context per concurrent stream. */
 int s14_ctx_create(int device, s14_ctx **out);
 void s14_ctx_destroy(s14_ctx *ctx);
 /* hipStream_t of the context's compute / copy stream, as void*. */
