@@ -110,7 +110,11 @@ __global__ __launch_bounds__(64) void k_fp8_matvec_exact(uint32_t N, uint32_t K,
     __syncthreads();
     const uint32_t soff = (scale_f32 ? 4u : 1u) * (tile_row + c0 / 128);
     if (K32) {
-      acc = fp8_row_pair(acc, src, rr * K + c0 + 16u * h, soff, scale_f32, int(n / 32), xs + 16 * h);
+      constexpr int kDeep = 8;  // batches in flight: 32 groups (the launch has N / 32 wavefronts)
+      if ((n / 32) % (4 * kDeep) == 0)
+        acc = fp8_row_pair_deep<kDeep>(acc, src, rr * K + c0 + 16u * h, soff, scale_f32, int(n / 32), xs + 16 * h);
+      else
+        acc = fp8_row_pair(acc, src, rr * K + c0 + 16u * h, soff, scale_f32, int(n / 32), xs + 16 * h);
     } else {
       for (uint32_t k = 0; k < n; ++k) {
         const float s = fp8_scale(src.s, soff, k / 128, scale_f32);
@@ -1055,6 +1059,29 @@ __global__ __launch_bounds__(64 * kP2FastWaves) void k_phase2_fast(const PairTab
   if (wave == 0) phase2_accumulate<kP2FastRows>(si, part, t, row0, Y);
 }
 
+// EXACT FP8 matvec with lane quads (k % 32 == 0, k <= kQuadMaxK): 4
+// wavefronts of 16 rows per workgroup, x staged once per workgroup as f32.
+constexpr uint32_t kQuadMaxK = 8192;
+__global__ __launch_bounds__(256) void k_fp8_matvec_exact_quad(uint32_t N, uint32_t K, const void *x, int x_bf16,
+                                                              const uint8_t *__restrict__ w,
+                                                              const void *__restrict__ sc, int scale_f32,
+                                                              float *__restrict__ y) {
+  __shared__ __attribute__((aligned(16))) float xs[kQuadMaxK];
+  for (uint32_t i = threadIdx.x; i < K; i += blockDim.x)
+    xs[i] = x_bf16 ? bf16_f32(reinterpret_cast<const uint16_t *>(x)[i]) : reinterpret_cast<const float *>(x)[i];
+  __syncthreads();
+  const uint32_t lane = threadIdx.x & 63u, q = lane & 3u;
+  const uint32_t row = blockIdx.x * 64u + (threadIdx.x >> 6) * 16u + (lane >> 2);
+  const uint32_t rr = row < N ? row : N - 1u;
+  const uint32_t kg = K / 128u + (K % 128u ? 1u : 0u);
+  const uint32_t ntile = ((N + 127u) / 128u) * kg;
+  const Rsrc rw = make_rsrc(w, N * K), rs = make_rsrc(sc, scale_f32 ? 4u * ntile : ntile);
+  const uint32_t soff = (scale_f32 ? 4u : 1u) * ((rr / 128u) * kg);
+  constexpr int kNB = 8;
+  const float v = fp8_row_quad<kNB>(rw, rs, rr * K + 8u * q, soff, scale_f32, int(K / 32u), xs + 8u * q);
+  if (q == 0 && row < N) y[row] = v;
+}
+
 inline unsigned blocks_for(size_t n, unsigned threads) { return unsigned((n + threads - 1) / threads); }
 
 }  // namespace
@@ -1093,6 +1120,9 @@ hipError_t launch_fp8_matvec(hipStream_t s, const s14_fp8_dispatch &d) {
       k_fp8_matvec_fast<4><<<grid, 256, 0, s>>>(N, K, d.x, xb, d.weight, d.scale, sf, d.y);
     else
       k_fp8_matvec_fast<8><<<grid, 256, 0, s>>>(N, K, d.x, xb, d.weight, d.scale, sf, d.y);
+  } else if (K % 32 == 0 && K <= kQuadMaxK && (K / 32) % 32 == 0) {
+    // lane quads: the standalone matvec has few rows per SIMD
+    k_fp8_matvec_exact_quad<<<blocks_for(N, 64), 256, 0, s>>>(N, K, d.x, xb, d.weight, d.scale, sf, d.y);
   } else if (K % 32 == 0) {
     k_fp8_matvec_exact<true><<<blocks_for(N, 32), 64, 0, s>>>(N, K, d.x, xb, d.weight, d.scale, sf, d.y);
   } else {

@@ -526,6 +526,107 @@ __device__ __forceinline__ float fp8_row_pair(float acc, const Src &src, uint32_
   return from_odd(acc);
 }
 
+// The same row with NB batches (4 NB groups) in flight instead of one: for
+// launches with few wavefronts (the standalone matvec at N = 1024 runs 32),
+// where one batch ahead leaves every wavefront waiting a load latency per
+// batch.  G % (4 NB) == 0; same products and order as fp8_row_pair.
+template <int NB>
+__device__ __forceinline__ float fp8_row_pair_deep(float acc, const Src1 &src, uint32_t woff, uint32_t soff,
+                                                   int scale_f32, int G, const float *__restrict__ xh) {
+  Fp8Batch b[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) fp8_load(b[j], src, woff, soff, scale_f32, 4 * j);
+  for (int g0 = 0; g0 < G; g0 += 4 * NB) {
+    const bool refill = g0 + 4 * NB < G;  // uniform
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      acc = fp8_consume(acc, b[j], xh, g0 + 4 * j);
+      if (refill) fp8_load(b[j], src, woff, soff, scale_f32, g0 + 4 * NB + 4 * j);
+    }
+  }
+  return from_odd(acc);
+}
+
+// ---------------------------------------------------------------------------
+// Lane quads, for launches with few rows (the standalone FP8 matvec at
+// N = 1024 has 1,024 row chains for 1,024 SIMDs): each row is owned by four
+// lanes, lane q forming the products of k 8q..8q+7 of every 32-k group, and
+// the running sum goes round the quad, lane q taking it from lane q - 1 (a
+// quad_perm DPP operand of its first add of the step).  A group is four
+// steps of 8 adds, each add the running sum plus one product in k order;
+// in step s only lane s's adds are kept.  Twice the lanes of a pair, so
+// half the wavefront instruction stream per row (fewer products per lane).
+// ---------------------------------------------------------------------------
+
+// Value of the previous lane of each quad, lane 0 taking lane 3's
+// (quad_perm [3,0,1,2]).
+__device__ __forceinline__ float from_prev_in_quad(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x93, 0xf, 0xf, true));
+}
+// Value of lane 3 of each quad (quad_perm [3,3,3,3]).
+__device__ __forceinline__ float from_quad_last(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xFF, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float quad_chain8(float acc, const float (&p)[8]) {
+#pragma unroll
+  for (int step = 0; step < 4; ++step) {
+    acc = __fadd_rn(from_prev_in_quad(acc), p[0]);
+#pragma unroll
+    for (int j = 1; j < 8; ++j) acc = __fadd_rn(acc, p[j]);
+  }
+  return acc;
+}
+// FP8 products of the lane's 8 code bytes: p = (x * e4m3) * s.
+__device__ __forceinline__ void fp8_products8(float (&p)[8], uint2 w, float s, const float *__restrict__ x) {
+  const float4 xa = *reinterpret_cast<const float4 *>(x), xb = *reinterpret_cast<const float4 *>(x + 4);
+  const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+  const uint32_t words[2] = {w.x, w.y};
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const v2f lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, false);
+    const v2f hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, true);
+    p[4 * d + 0] = __fmul_rn(__fmul_rn(xv[4 * d + 0], lo.x), s);
+    p[4 * d + 1] = __fmul_rn(__fmul_rn(xv[4 * d + 1], lo.y), s);
+    p[4 * d + 2] = __fmul_rn(__fmul_rn(xv[4 * d + 2], hi.x), s);
+    p[4 * d + 3] = __fmul_rn(__fmul_rn(xv[4 * d + 3], hi.y), s);
+  }
+}
+// Four groups of a quad lane's codes (one 128-wide scale tile).
+struct Fp8QBatch {
+  uint2 w[4];
+  float s;
+};
+__device__ __forceinline__ void fp8q_load(Fp8QBatch &b, Rsrc w, Rsrc sc, uint32_t woff, uint32_t soff, int scale_f32,
+                                          int g0) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b.w[i] = ld8(w, woff + 32u * uint32_t(g0 + i));
+  b.s = fp8_scale(sc, soff, uint32_t(g0) / 4u, scale_f32);
+}
+// Dot of one FP8 row of G groups (G % (4 NB) == 0) with x in LDS (xq = x +
+// 8 q); NB batches in flight.  Result in every lane of the quad.
+template <int NB>
+__device__ __forceinline__ float fp8_row_quad(Rsrc w, Rsrc sc, uint32_t woff, uint32_t soff, int scale_f32, int G,
+                                              const float *__restrict__ xq) {
+  Fp8QBatch b[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) fp8q_load(b[j], w, sc, woff, soff, scale_f32, 4 * j);
+  float acc = 0.0f;
+  for (int g0 = 0; g0 < G; g0 += 4 * NB) {
+    const bool refill = g0 + 4 * NB < G;  // uniform
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float p[8];
+        fp8_products8(p, b[j].w[i], b[j].s, xq + 32 * (g0 + 4 * j + i));
+        acc = quad_chain8(acc, p);
+      }
+      if (refill) fp8q_load(b[j], w, sc, woff, soff, scale_f32, g0 + 4 * NB + 4 * j);
+    }
+  }
+  return from_quad_last(acc);
+}
+
 // ---------------------------------------------------------------------------
 // act_quant of the official expert semantics (l42_reference.py:390-403,
 // group 128): a vector in LDS is replaced, in place, by its requantised

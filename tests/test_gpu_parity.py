@@ -183,7 +183,9 @@ def test_fp8_wq_a_config(pipes, oracle):
             assert st["max_abs"] <= 2e-5 and st["rmse"] <= 2e-6
 
 
-@pytest.mark.parametrize("n,k", [(2048, 4096), (4096, 2048), (129, 130)])
+# lane quads take k % 1024 == 0 up to 8192 (ragged n included); lane pairs the
+# other k % 32 == 0; whole-row lanes the rest
+@pytest.mark.parametrize("n,k", [(2048, 4096), (4096, 2048), (200, 1024), (96, 8192), (130, 1056), (129, 130)])
 def test_fp8_ue8m0_reference_variant_exact(pipes, oracle, n, k):
     say(f"fp8 ue8m0 f32-x exact n={n} k={k}")
     w = synth.e4m3fn_encode(synth.gen_normal(14, 1, n * k)).reshape(n, k)
