@@ -470,9 +470,20 @@ int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, con
   const PageOffsets f8 = offsets_of(l);
   const RouteSpec rs{router_args(router), tokens,      shared_format,  expert_pages_dev, shared_page,
                      ids_out,              weights_out, status_word(ws)};
+  const uint32_t n_pairs = tokens * (kTopK + 1);
+  if (tokens == 1) {
+    // one token: the route launch only scores, and every phase-1 workgroup
+    // of a routed pair selects the top-k itself (no last-arrival hand-off)
+    hipError_t e = launch_route_scores(st, ws, rs, x, ev ? ev[kStageRoute] : KernelEvents{});
+    if (e != hipSuccess) return hip_fail(e, "router launch");
+    e = launch_phase1(st, ws, nullptr, n_pairs, tokens, mx, f8, x, mode, ev ? ev[kStagePhase1] : KernelEvents{}, &rs);
+    if (e != hipSuccess) return hip_fail(e, "phase 1 launch");
+    e = launch_phase2(st, ws, tokens, mx, f8, y, mode, ev ? ev[kStagePhase2] : KernelEvents{});
+    if (e != hipSuccess) return hip_fail(e, "phase 2 launch");
+    return S14_OK;
+  }
   hipError_t e = launch_route(st, ws, rs, x, ev ? ev[kStageRoute] : KernelEvents{});
   if (e != hipSuccess) return hip_fail(e, "router launch");
-  const uint32_t n_pairs = tokens * (kTopK + 1);
   if (tokens > 1 && mode == S14_MODE_EXACT) {
     // blocks: one row per lane (enough (token, expert) chains to fill the GPU)
     e = launch_block_phase1(st, ws, n_pairs, mx, f8, x, ev ? ev[kStagePhase1] : KernelEvents{});

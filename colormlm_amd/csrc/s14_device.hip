@@ -511,14 +511,16 @@ __global__ __launch_bounds__(256) void k_router_scores(RouterArgs r, uint32_t to
 
 // Plan of one token (one wavefront): top-k of score + bias (ties to the
 // lower index) and its weights s/sum (sum sequential in selection order)
-// times route_scale (executor.py:647-667), into the LDS lists.
+// times route_scale (executor.py:647-667), into the LDS lists.  `lead`: this
+// wavefront also reports (status bits, ids_out, weights_out); several
+// workgroups may plan the same token, one of them reports.
 struct PlanLds {
   uint32_t ids[kMaxTokens][kTopK];
   float wts[kMaxTokens][kTopK];
   uint64_t pgs[kMaxTokens][kTopK];
 };
 __device__ __forceinline__ void plan_token(const RouteSpec &rs, uint32_t t, const float *biased, const float *scores,
-                                           const uint64_t *pages, PlanLds &pl) {
+                                           const uint64_t *pages, PlanLds &pl, bool lead = true) {
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t k = rs.r.topk;
   bool bad = false;
@@ -526,7 +528,8 @@ __device__ __forceinline__ void plan_token(const RouteSpec &rs, uint32_t t, cons
                               : select_topk_lds(biased, scores, pages, rs.r.n_experts, k);
   float wgt = lane < k ? route_weight(c, rs.r.route_scale) : 0.0f;
   bad = bad || !route_weights_valid(wgt, k, rs.r.route_scale);
-  if (bad && lane == 0) __hip_atomic_fetch_or(rs.status, kStatusBadRoute, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (bad && lead && lane == 0)
+    __hip_atomic_fetch_or(rs.status, kStatusBadRoute, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (lane < k) {
     uint32_t id = c.id;
     uint64_t pg = c.page;
@@ -540,15 +543,15 @@ __device__ __forceinline__ void plan_token(const RouteSpec &rs, uint32_t t, cons
       // a chosen expert without a resident page: its pair reads the shared
       // page instead (mapped memory; the result is discarded) and its NaN
       // weight makes the token's output NaN; the status word says why
-      __hip_atomic_fetch_or(rs.status, kStatusNullPage, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lead) __hip_atomic_fetch_or(rs.status, kStatusNullPage, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       pg = reinterpret_cast<uint64_t>(rs.shared_page);
       wgt = __builtin_nanf("");
     }
     pl.ids[t][lane] = id;
     pl.wts[t][lane] = wgt;
     pl.pgs[t][lane] = pg;
-    if (rs.ids_out) rs.ids_out[t * k + lane] = uint16_t(id);
-    if (rs.weights_out) rs.weights_out[t * k + lane] = wgt;
+    if (lead && rs.ids_out) rs.ids_out[t * k + lane] = uint16_t(id);
+    if (lead && rs.weights_out) rs.weights_out[t * k + lane] = wgt;
   }
 }
 
@@ -612,7 +615,12 @@ __device__ __forceinline__ void plan_publish(const RouteSpec &rs, PairTable *tab
 // kRouteGroup (by linear index), then groups; each level's last arrival
 // resets its counter.  expert_pages == NULL: route only.  Saves a dependent
 // kernel launch per layer.
+//
+// kScoresOnly (single-token layers): the launch only scores; every phase-1
+// workgroup of a routed pair then selects the top-k itself from the scores
+// (route_pair), so no workgroup waits for a last arrival.
 constexpr uint32_t kRouteGroup = 16;
+template <bool kScoresOnly>
 __global__ __launch_bounds__(64 * kMaxTokens) void k_route(RouteSpec rs, Workspace ws, const float *__restrict__ X) {
   __shared__ float sc[kMaxTokens][kMaxExperts];
   __shared__ float bs[kMaxTokens][kMaxExperts];
@@ -632,6 +640,7 @@ __global__ __launch_bounds__(64 * kMaxTokens) void k_route(RouteSpec rs, Workspa
       __hip_atomic_store(&ws.biased[t * kMaxExperts + e], s.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  if constexpr (kScoresOnly) return;  // the kernel boundary publishes the scores
   // Why the last workgroup sees every score without a release/acquire pair:
   //  1. the scores are agent-scope atomic stores (global_store ... sc1),
   //     written through to the device's coherence point rather than left
@@ -704,17 +713,69 @@ inline uint32_t route_waves(uint32_t tokens) { return tokens <= 4 ? 4u : 8u; }
 static_assert(kMaxTokens <= 8, "route_waves covers at most 8 tokens");
 
 // Pair p of phase 1: from the host plan (by value; workgroup (0,0) also
-// publishes it for phase 2) or from the table the plan kernel wrote.
+// publishes it for phase 2), from the table the route kernel wrote, or
+// planned here from the route kernel's scores (single token).
 struct PairRef {
   const uint8_t *page;
   uint32_t fmt;
   uint32_t token;
   float weight;
 };
+enum : int { kPairFromTable = 0, kPairFromHost = 1, kPairFromScores = 2 };
 
-template <bool kHostPlan>
-__device__ __forceinline__ PairRef phase1_pair(const PairTable &plan, PairTable *__restrict__ tab, uint32_t p) {
-  if (kHostPlan) {
+// Pair p of a single-token layer from the scores (whole workgroup, uniform
+// result): the token's scores, biased scores and expert pages into LDS, one
+// wavefront selects the top-k exactly as the route kernel's last workgroup
+// does (plan_token) and takes the p-th choice in expert order, which is the
+// pair table's order (plan_publish sorts pairs by expert, then token).  The
+// shared pair (p = topk) needs no plan.  Workgroup (0,0) reports the route
+// and publishes the pair table for phase 2.
+__device__ __forceinline__ PairRef route_pair(const RouteSpec &rs, const Workspace &ws, uint32_t p) {
+  __shared__ float rp_sc[kMaxExperts], rp_bs[kMaxExperts];
+  __shared__ uint64_t rp_pages[kMaxExperts];
+  __shared__ PlanLds rp_pl;
+  __shared__ PairRef rp_mine;
+  const uint32_t k = rs.r.topk, n = rs.r.n_experts;
+  if (p >= k) return PairRef{rs.shared_page, uint32_t(rs.shared_fmt), 0u, 1.0f};
+  for (uint32_t i = threadIdx.x; i < kMaxExperts; i += blockDim.x) {
+    const bool in = i < n;
+    rp_sc[i] = in ? ws.scores[i] : 0.0f;
+    rp_bs[i] = in ? ws.biased[i] : 0.0f;
+    rp_pages[i] = in ? rs.expert_pages[i] : 0ull;
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const bool lead = blockIdx.x == 0 && blockIdx.y == 0;
+    plan_token(rs, 0, rp_bs, rp_sc, rp_pages, rp_pl, lead);
+    if (lead) plan_publish(rs, ws.table, rp_pl);
+    const uint32_t lane = threadIdx.x;
+    if (lane < k) {
+      const uint32_t id = rp_pl.ids[0][lane];
+      uint32_t rank = 0;
+      for (uint32_t j = 0; j < k; ++j) rank += rp_pl.ids[0][j] < id ? 1u : 0u;
+      if (rank == p)
+        rp_mine = PairRef{reinterpret_cast<const uint8_t *>(rp_pl.pgs[0][lane]), uint32_t(S14_PAGE_MXFP4), 0u,
+                          rp_pl.wts[0][lane]};
+    }
+  }
+  __syncthreads();
+  // the same in every lane: keep it in scalar registers (a per-lane page
+  // address would put every buffer load in a readfirstlane loop)
+  const uint64_t pg = reinterpret_cast<uint64_t>(rp_mine.page);
+  return PairRef{reinterpret_cast<const uint8_t *>(
+                     (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(pg >> 32)))) << 32) |
+                     uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(pg))))),
+                 uint32_t(__builtin_amdgcn_readfirstlane(int(rp_mine.fmt))),
+                 uint32_t(__builtin_amdgcn_readfirstlane(int(rp_mine.token))),
+                 __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(rp_mine.weight)))};
+}
+
+template <int kSrc>
+__device__ __forceinline__ PairRef phase1_pair(const PairTable &plan, const RouteSpec &rs, const Workspace &ws,
+                                               uint32_t p) {
+  PairTable *__restrict__ tab = ws.table;
+  if constexpr (kSrc == kPairFromScores) return route_pair(rs, ws, p);
+  if (kSrc == kPairFromHost) {
     if (blockIdx.x == 0 && blockIdx.y == 0) {
       const uint32_t *src = reinterpret_cast<const uint32_t *>(&plan);
       uint32_t *dst = reinterpret_cast<uint32_t *>(tab);
@@ -736,8 +797,8 @@ __device__ __forceinline__ uint32_t page_bytes(uint32_t fmt) {
 // kTier (1: single-token launch, 8: block launch) names the instantiation,
 // so traces and profiles keep the two workloads apart, and picks the code
 // check (per row at batch 1, per batch of groups for blocks).
-template <bool kHostPlan, int kTier, bool kOfficial>
-__global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable plan, Workspace ws,
+template <int kSrc, int kTier, bool kOfficial>
+__global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable plan, RouteSpec rs, Workspace ws,
                                                                      const float *__restrict__ X, PageOffsets mx,
                                                                      PageOffsets f8) {
   __shared__ float xs[kHidden];
@@ -745,7 +806,7 @@ __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable p
   __shared__ int red[2 * kP1ExactWaves];
   exp_table_fill(exptab);  // published by the barrier in the x copy
   const uint32_t p = blockIdx.y;
-  const PairRef pr = phase1_pair<kHostPlan>(plan, ws.table, p);
+  const PairRef pr = phase1_pair<kSrc>(plan, rs, ws, p);
   const uint32_t lane = threadIdx.x & 63, h = lane & 1u;
   const uint32_t tile = blockIdx.x * kP1ExactWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool upper = lane >= 32;
@@ -807,14 +868,14 @@ __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable p
 // (read from one LDS copy per workgroup).
 // The grid stays within one round of resident workgroups: a workgroup that
 // starts only when another finishes costs a whole extra load latency.
-template <bool kHostPlan, int kTier>
-__global__ __launch_bounds__(256) void k_phase1_fast(PairTable plan, Workspace ws, const float *__restrict__ X,
-                                                     PageOffsets mx, PageOffsets f8) {
+template <int kSrc, int kTier>
+__global__ __launch_bounds__(256) void k_phase1_fast(PairTable plan, RouteSpec rs, Workspace ws,
+                                                     const float *__restrict__ X, PageOffsets mx, PageOffsets f8) {
   constexpr int NSEG = kHidden / 2048;
   constexpr int R = p1_fast_rows_per_wave(kTier);
   constexpr int D = kP1FastDepth;
   const uint32_t p = blockIdx.y;
-  const PairRef pr = phase1_pair<kHostPlan>(plan, ws.table, p);
+  const PairRef pr = phase1_pair<kSrc>(plan, rs, ws, p);
   const uint32_t row0 = blockIdx.x * p1_fast_rows(kTier) + (threadIdx.x >> 6) * R;
   const Rsrc r = make_rsrc(pr.page, page_bytes(pr.fmt));
   const int lane = threadIdx.x & 63;
@@ -1194,42 +1255,53 @@ hipError_t launch_route(hipStream_t s, const Workspace &ws, const RouteSpec &rs,
   const uint32_t blocks = (rs.r.n_experts + w - 1) / w * rs.tokens;
   // the workspace holds counters for at most kRouteCounters / kRouteCounterStride - 1 groups
   if ((blocks + kRouteGroup - 1) / kRouteGroup > kRouteCounters / kRouteCounterStride - 1) return hipErrorInvalidValue;
-  hipExtLaunchKernelGGL(k_route, dim3((rs.r.n_experts + w - 1) / w, rs.tokens), dim3(64 * w), 0, s, ev.start,
+  hipExtLaunchKernelGGL(k_route<false>, dim3((rs.r.n_experts + w - 1) / w, rs.tokens), dim3(64 * w), 0, s, ev.start,
+                        ev.stop, 0, rs, ws, x);
+  return hipGetLastError();
+}
+
+hipError_t launch_route_scores(hipStream_t s, const Workspace &ws, const RouteSpec &rs, const float *x,
+                               KernelEvents ev) {
+  const uint32_t w = route_waves(rs.tokens);
+  hipExtLaunchKernelGGL(k_route<true>, dim3((rs.r.n_experts + w - 1) / w, rs.tokens), dim3(64 * w), 0, s, ev.start,
                         ev.stop, 0, rs, ws, x);
   return hipGetLastError();
 }
 
 namespace {
-template <int kTier>
-void phase1_tier(hipStream_t s, const Workspace &ws, const PairTable *host_plan, uint32_t n_pairs,
-                 const PageOffsets &mx, const PageOffsets &fp8, const float *x, int mode, KernelEvents ev) {
-  PairTable plan{};
-  if (host_plan) plan = *host_plan;
+template <int kSrc, int kTier>
+void phase1_launch(hipStream_t s, const Workspace &ws, const PairTable &plan, const RouteSpec &rs, uint32_t n_pairs,
+                   const PageOffsets &mx, const PageOffsets &fp8, const float *x, int mode, KernelEvents ev) {
   if (mode == S14_MODE_FAST) {
     const dim3 grid(kInter / p1_fast_rows(kTier), n_pairs);
-    if (host_plan)
-      hipExtLaunchKernelGGL(k_phase1_fast<true, kTier>, grid, dim3(256), 0, s, ev.start, ev.stop, 0, plan, ws, x, mx,
-                            fp8);
-    else
-      hipExtLaunchKernelGGL(k_phase1_fast<false, kTier>, grid, dim3(256), 0, s, ev.start, ev.stop, 0, plan, ws, x,
-                            mx, fp8);
+    hipExtLaunchKernelGGL(k_phase1_fast<kSrc, kTier>, grid, dim3(256), 0, s, ev.start, ev.stop, 0, plan, rs, ws, x,
+                          mx, fp8);
   } else {
     const dim3 grid(kInter / (kP1ExactRows * kP1ExactWaves), n_pairs);
     const dim3 blk(64 * kP1ExactWaves);
-    if (mode == S14_MODE_OFFICIAL) {
-      if (host_plan)
-        hipExtLaunchKernelGGL(k_phase1_exact<true, kTier, true>, grid, blk, 0, s, ev.start, ev.stop, 0, plan, ws, x, mx,
-                              fp8);
-      else
-        hipExtLaunchKernelGGL(k_phase1_exact<false, kTier, true>, grid, blk, 0, s, ev.start, ev.stop, 0, plan, ws, x,
-                              mx, fp8);
-    } else if (host_plan) {
-      hipExtLaunchKernelGGL(k_phase1_exact<true, kTier, false>, grid, blk, 0, s, ev.start, ev.stop, 0, plan, ws, x, mx,
-                            fp8);
-    } else {
-      hipExtLaunchKernelGGL(k_phase1_exact<false, kTier, false>, grid, blk, 0, s, ev.start, ev.stop, 0, plan, ws, x,
+    if (mode == S14_MODE_OFFICIAL)
+      hipExtLaunchKernelGGL(k_phase1_exact<kSrc, kTier, true>, grid, blk, 0, s, ev.start, ev.stop, 0, plan, rs, ws, x,
                             mx, fp8);
-    }
+    else
+      hipExtLaunchKernelGGL(k_phase1_exact<kSrc, kTier, false>, grid, blk, 0, s, ev.start, ev.stop, 0, plan, rs, ws,
+                            x, mx, fp8);
+  }
+}
+
+template <int kTier>
+void phase1_tier(hipStream_t s, const Workspace &ws, const PairTable *host_plan, const RouteSpec *route,
+                 uint32_t n_pairs, const PageOffsets &mx, const PageOffsets &fp8, const float *x, int mode,
+                 KernelEvents ev) {
+  PairTable plan{};
+  if (host_plan) plan = *host_plan;
+  RouteSpec rs{};
+  if (route) rs = *route;
+  if (host_plan) {
+    phase1_launch<kPairFromHost, kTier>(s, ws, plan, rs, n_pairs, mx, fp8, x, mode, ev);
+  } else if (route) {
+    if constexpr (kTier == 1) phase1_launch<kPairFromScores, kTier>(s, ws, plan, rs, n_pairs, mx, fp8, x, mode, ev);
+  } else {
+    phase1_launch<kPairFromTable, kTier>(s, ws, plan, rs, n_pairs, mx, fp8, x, mode, ev);
   }
 }
 
@@ -1252,11 +1324,12 @@ void phase2_tier(hipStream_t s, const Workspace &ws, uint32_t tokens, const Page
 
 hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *host_plan, uint32_t n_pairs,
                          uint32_t tokens, const PageOffsets &mx, const PageOffsets &fp8, const float *x, int mode,
-                         KernelEvents ev) {
+                         KernelEvents ev, const RouteSpec *route) {
+  if (route && (host_plan || tokens != 1)) return hipErrorInvalidValue;  // in-kernel planning: one routed token
   if (tokens <= 1)
-    phase1_tier<1>(s, ws, host_plan, n_pairs, mx, fp8, x, mode, ev);
+    phase1_tier<1>(s, ws, host_plan, route, n_pairs, mx, fp8, x, mode, ev);
   else
-    phase1_tier<kMaxTokens>(s, ws, host_plan, n_pairs, mx, fp8, x, mode, ev);
+    phase1_tier<kMaxTokens>(s, ws, host_plan, route, n_pairs, mx, fp8, x, mode, ev);
   return hipGetLastError();
 }
 

@@ -213,12 +213,20 @@ hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const Router
 // ws.table.  One launch (the last workgroup plans).
 hipError_t launch_route(hipStream_t s, const Workspace &ws, const RouteSpec &rs, const float *x,
                         KernelEvents ev = {});
+// The same launch's scoring alone (no plan, no table): for one routed
+// token, whose phase 1 plans from the scores itself (launch_phase1 with
+// `route`).
+hipError_t launch_route_scores(hipStream_t s, const Workspace &ws, const RouteSpec &rs, const float *x,
+                               KernelEvents ev = {});
 // w1/w3 + SwiGLU of every pair.  host_plan != NULL: the pairs are given and
-// workgroup (0,0) publishes them for phase 2; otherwise they are read from
-// the table launch_route wrote.
+// workgroup (0,0) publishes them for phase 2; route != NULL (one token):
+// every workgroup of a routed pair selects the top-k from the scores of
+// launch_route_scores, and workgroup (0,0) reports the route and publishes
+// the table; otherwise the pairs are read from the table launch_route wrote.
 hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *host_plan,
                          uint32_t n_pairs, uint32_t tokens, const PageOffsets &mx,
-                         const PageOffsets &fp8, const float *x, int mode, KernelEvents ev = {});
+                         const PageOffsets &fp8, const float *x, int mode, KernelEvents ev = {},
+                         const RouteSpec *route = nullptr);
 // Blocks of 2..8 tokens in EXACT order, one row per lane (s14_block.hip):
 // phase 1 of every pair of the table the route kernel wrote, and phase 2 of
 // every token with its route-order accumulation into y [tokens][hidden].
