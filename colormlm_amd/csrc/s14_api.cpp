@@ -697,8 +697,9 @@ extern "C" int s14_requant_e4m3(s14_ctx *ctx, void *stream, uint32_t rows, uint3
 
 namespace {
 
-// FAST's split-K partials and arrival counters, allocated on the first FAST
-// call (counters zeroed once; every launch leaves them zero).
+// FAST's split-K partials and arrival counters, and EXACT's group partials,
+// allocated on the first fp8_linear call (counters zeroed once; every launch
+// leaves them zero).
 int linear_workspace(s14_ctx *ctx) {
   if (ctx->lin_base) return S14_OK;
   const size_t cnt_bytes = sizeof(uint32_t) * s14::kLinMaxCounters;
@@ -738,8 +739,7 @@ extern "C" int s14_fp8_linear(s14_ctx *ctx, void *stream, uint32_t m, uint32_t n
   if (bias.ptr)
     if (int rc = require_capacity(bias, uint64_t(n) * 4, "bias")) return rc;
   if (int rc = require_capacity(y, uint64_t(m) * n * 4, "y")) return rc;
-  if (mode == S14_MODE_FAST)
-    if (int rc = linear_workspace(ctx)) return rc;
+  if (int rc = linear_workspace(ctx)) return rc;
   const s14::LinearArgs a{m,
                           n,
                           k,

@@ -52,13 +52,6 @@ constexpr int kXcds = 8;
 static_assert(kBTileGroups % kXcds == 0, "tile groups spread evenly over the XCDs");
 static_assert(kInter / 32 <= kInter / kP1ExactRows, "32-row h windows fit the workspace's per-pair records");
 
-// x_k of the lane's 16-lane row: lane K % 16 of `v` broadcast by the DPP
-// operand of the consuming instruction.
-template <int K>
-__device__ __forceinline__ float bcast16(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + (K & 15), 0xf, 0xf, false));
-}
-
 // The 32 decoded values of one group, e2m1 * scale (scale = 2^(c-127) in
 // the scaled form, 1 in the literal one), k = 2i, 2i+1 in q[i].
 __device__ __forceinline__ void decode32(v2f (&q)[16], uint4 w, float scale) {

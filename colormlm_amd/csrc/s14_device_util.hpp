@@ -415,5 +415,12 @@ __device__ __forceinline__ bool route_weights_valid(float w, uint32_t k, float r
   return __ballot(!lane_ok) == 0ull && fabsf(__fsub_rn(sum, route_scale)) <= 1e-4f;
 }
 
+// Lane K % 16 of each 16-lane row of `v`, in every lane of that row (DPP
+// row_newbcast, folded into the consuming instruction as its operand).
+template <int K>
+__device__ __forceinline__ float bcast16(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + (K & 15), 0xf, 0xf, false));
+}
+
 }  // namespace
 }  // namespace s14

@@ -26,6 +26,9 @@
 // k_act_quant; group 128 feeds this linear, group 32 the prefill.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <utility>
+
 #include "s14_device.hpp"
 #include "s14_device_util.hpp"
 #include "s14_e4m3.h"
@@ -142,6 +145,202 @@ __global__ __launch_bounds__(256) void k_linear_exact(LinearArgs a) {
     if (a.round_bf16) acc = bf16_round(acc);
     a.y[size_t(m) * N + row] = acc;
   }
+}
+
+// ---------------------------------------------------------------------------
+// EXACT, tiled (k % 128 == 0, 16-byte aligned x and w): one wavefront per
+// (64-row tile, scale group g, block of MT tokens), four independent
+// wavefronts per workgroup.  The wavefront DMA-loads its 64 rows x 128 bytes
+// of weight into LDS (buffer_load ... lds: 8 lanes per row, whole lines per
+// quarter-wave; piece q of row r lands at piece q ^ (r & 7), so the later
+// row-per-lane reads take distinct banks), and its tokens' 128 activation
+// codes, decoded and scaled once: a = dec(x) * sa.  Lane l then owns row
+// r0 + l: per 16 k it decodes b = dec(w) * sb and, for each token, adds
+// a * b in k order, a reaching every lane as the multiply's DPP
+// row-broadcast operand (lane i of each 16-lane row holds a[16c + i]).  The
+// group partials go to the workspace, part[g][t][row]; k_linear_sum adds
+// them in group order (acc = 0; acc += partial_g), adds the bias and rounds.
+// Products and sums are the oracle's (fp8.py:173-191 with k ascending).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kLTRows = 64;                    // rows per wavefront
+constexpr uint32_t kLTWaves = 4;                    // wavefronts per workgroup
+constexpr uint32_t kLTSlot = kLTRows * kLinGroup;   // 8 KiB of weight per wavefront
+__shared__ __attribute__((aligned(16))) uint8_t lt_w[kLTWaves][kLTSlot];
+__shared__ __attribute__((aligned(16))) uint8_t lt_x[kLTWaves][8][kLinGroup];
+
+typedef __attribute__((address_space(3))) void lt_lds_void;
+
+// One 16-k block: p[t] += a[t][16c + i] * b[i], i = 0..15 ascending, for
+// MT tokens.  a reaches every lane as the DPP row-broadcast operand of the
+// multiply (lane i of each 16-lane row: row_newbcast:i), written as asm
+// because the compiler kept the broadcast as a separate move (plus a zeroed
+// register) per product.  The MT multiplies of a step come before its MT
+// adds, so no add waits on the one before it when MT > 1.  The DPP source
+// a is written long before the block (no DPP wait states needed).
+#define S14_LT_MUL(t, i) \
+  "v_mul_f32_dpp %[q" #t "], %[a" #t "], %[b" #i "] row_newbcast:" #i " row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+#define S14_LT_ADD(t) "v_add_f32 %[p" #t "], %[q" #t "], %[p" #t "]\n"
+#define S14_LT_STEP1(i) S14_LT_MUL(0, i) S14_LT_ADD(0)
+#define S14_LT_STEP2(i) S14_LT_MUL(0, i) S14_LT_MUL(1, i) S14_LT_ADD(0) S14_LT_ADD(1)
+#define S14_LT_STEP4(i) \
+  S14_LT_MUL(0, i) S14_LT_MUL(1, i) S14_LT_MUL(2, i) S14_LT_MUL(3, i) \
+  S14_LT_ADD(0) S14_LT_ADD(1) S14_LT_ADD(2) S14_LT_ADD(3)
+#define S14_LT_STEP8(i) \
+  S14_LT_MUL(0, i) S14_LT_MUL(1, i) S14_LT_MUL(2, i) S14_LT_MUL(3, i) S14_LT_MUL(4, i) S14_LT_MUL(5, i) \
+  S14_LT_MUL(6, i) S14_LT_MUL(7, i) S14_LT_ADD(0) S14_LT_ADD(1) S14_LT_ADD(2) S14_LT_ADD(3) S14_LT_ADD(4) \
+  S14_LT_ADD(5) S14_LT_ADD(6) S14_LT_ADD(7)
+#define S14_LT_BLOCK(STEP) \
+  STEP(0) STEP(1) STEP(2) STEP(3) STEP(4) STEP(5) STEP(6) STEP(7) STEP(8) STEP(9) STEP(10) STEP(11) STEP(12) \
+  STEP(13) STEP(14) STEP(15)
+#define S14_LT_B                                                                                               \
+  [b0] "v"(bv[0]), [b1] "v"(bv[1]), [b2] "v"(bv[2]), [b3] "v"(bv[3]), [b4] "v"(bv[4]), [b5] "v"(bv[5]),         \
+      [b6] "v"(bv[6]), [b7] "v"(bv[7]), [b8] "v"(bv[8]), [b9] "v"(bv[9]), [b10] "v"(bv[10]), [b11] "v"(bv[11]), \
+      [b12] "v"(bv[12]), [b13] "v"(bv[13]), [b14] "v"(bv[14]), [b15] "v"(bv[15])
+
+template <int MT>
+__device__ __forceinline__ void lt_block16(float (&p)[MT], const float (&ac)[MT], const float (&bv)[16]);
+template <>
+__device__ __forceinline__ void lt_block16<1>(float (&p)[1], const float (&ac)[1], const float (&bv)[16]) {
+  float q[1];
+  asm volatile(S14_LT_BLOCK(S14_LT_STEP1) : [p0] "+v"(p[0]), [q0] "=&v"(q[0]) : [a0] "v"(ac[0]), S14_LT_B);
+}
+template <>
+__device__ __forceinline__ void lt_block16<2>(float (&p)[2], const float (&ac)[2], const float (&bv)[16]) {
+  float q[2];
+  asm volatile(S14_LT_BLOCK(S14_LT_STEP2)
+               : [p0] "+v"(p[0]), [p1] "+v"(p[1]), [q0] "=&v"(q[0]), [q1] "=&v"(q[1])
+               : [a0] "v"(ac[0]), [a1] "v"(ac[1]), S14_LT_B);
+}
+template <>
+__device__ __forceinline__ void lt_block16<4>(float (&p)[4], const float (&ac)[4], const float (&bv)[16]) {
+  float q[4];
+  asm volatile(S14_LT_BLOCK(S14_LT_STEP4)
+               : [p0] "+v"(p[0]), [p1] "+v"(p[1]), [p2] "+v"(p[2]), [p3] "+v"(p[3]), [q0] "=&v"(q[0]),
+                 [q1] "=&v"(q[1]), [q2] "=&v"(q[2]), [q3] "=&v"(q[3])
+               : [a0] "v"(ac[0]), [a1] "v"(ac[1]), [a2] "v"(ac[2]), [a3] "v"(ac[3]), S14_LT_B);
+}
+template <>
+__device__ __forceinline__ void lt_block16<8>(float (&p)[8], const float (&ac)[8], const float (&bv)[16]) {
+  float q[8];
+  asm volatile(S14_LT_BLOCK(S14_LT_STEP8)
+               : [p0] "+v"(p[0]), [p1] "+v"(p[1]), [p2] "+v"(p[2]), [p3] "+v"(p[3]), [p4] "+v"(p[4]),
+                 [p5] "+v"(p[5]), [p6] "+v"(p[6]), [p7] "+v"(p[7]), [q0] "=&v"(q[0]), [q1] "=&v"(q[1]),
+                 [q2] "=&v"(q[2]), [q3] "=&v"(q[3]), [q4] "=&v"(q[4]), [q5] "=&v"(q[5]), [q6] "=&v"(q[6]),
+                 [q7] "=&v"(q[7])
+               : [a0] "v"(ac[0]), [a1] "v"(ac[1]), [a2] "v"(ac[2]), [a3] "v"(ac[3]), [a4] "v"(ac[4]),
+                 [a5] "v"(ac[5]), [a6] "v"(ac[6]), [a7] "v"(ac[7]), S14_LT_B);
+}
+#undef S14_LT_B
+#undef S14_LT_BLOCK
+#undef S14_LT_STEP8
+#undef S14_LT_STEP4
+#undef S14_LT_STEP2
+#undef S14_LT_STEP1
+#undef S14_LT_ADD
+#undef S14_LT_MUL
+
+template <int MT, bool kXsF32, bool kWsF32>
+__global__ __launch_bounds__(64 * kLTWaves) void k_linear_tile(LinearArgs a, float *__restrict__ part) {
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const uint32_t G = a.groups, K = a.k, N = a.n, M = a.m;
+  const uint32_t task = blockIdx.x * kLTWaves + wave;
+  const uint32_t tiles = (N + kLTRows - 1) / kLTRows;
+  if (task >= tiles * G) return;  // uniform per wavefront; no workgroup barrier below
+  const uint32_t tile = task / G, g = task % G;
+  const uint32_t r0 = tile * kLTRows, k0 = g * kLinGroup, m0 = blockIdx.y * uint32_t(MT);
+  const Rsrc rw = make_rsrc(a.w, N * K), rx = make_rsrc(a.x, M * K);
+  const uint32_t n_sw = (N + 127u) / 128u * G, n_sx = M * G;
+  const Rsrc rsw = make_rsrc(a.w_scale, kWsF32 ? 4u * n_sw : n_sw);
+  const Rsrc rsx = make_rsrc(a.x_scale, kXsF32 ? 4u * n_sx : n_sx);
+  uint8_t *slot = lt_w[wave];
+  // weight tile: instruction j moves rows 8j .. 8j+7 (lane l: row 8j + l/8,
+  // piece (l % 8) ^ (row & 7), landing at position l % 8 of that row)
+#pragma unroll
+  for (uint32_t j = 0; j < 8; ++j) {
+    const uint32_t dr = 8u * j + (lane >> 3);
+    const uint32_t off = (r0 + dr) * K + k0 + 16u * ((lane & 7u) ^ (dr & 7u));
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lt_lds_void *)(slot + 1024u * j), 16, off, 0, 0, 0);
+  }
+  // activation codes: lane l < 8 MT moves 16 bytes of token l / 8 (tokens
+  // past m read zeros through the resource's bounds; their sums are not
+  // stored)
+  uint8_t(*xs)[kLinGroup] = lt_x[wave];
+  if (lane < 8u * MT) {
+    const uint32_t t = lane >> 3, piece = lane & 7u;
+    const uint4 v = (m0 + t < M) ? ld16(rx, (m0 + t) * K + k0 + 16u * piece) : make_uint4(0u, 0u, 0u, 0u);
+    *reinterpret_cast<uint4 *>(&xs[t][16u * piece]) = v;
+  }
+  float sa[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+    sa[t] = (m0 + t < M) ? (kXsF32 ? ldf(rsx, 4u * ((m0 + t) * G + g)) : ue8m0_f32(ld1(rsx, (m0 + t) * G + g))) : 0.0f;
+  const float sb = kWsF32 ? ldf(rsw, 4u * ((r0 / 128u) * G + g)) : ue8m0_f32(ld1(rsw, (r0 / 128u) * G + g));
+  // a[t][16c + i] in lane i of each 16-lane row: dec(x) * sa, the oracle's
+  // f32 product
+  float av[MT][8];
+  const uint32_t li = lane & 15u;
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const uint32_t code = xs[t][16 * c + li];
+      const v2f d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code, 1.0f, false);
+      av[t][c] = __fmul_rn(d.x, sa[t]);
+    }
+  // the lane's row: 8 pieces of 16 codes (the DMA's writes are waited for
+  // by the compiler before these reads)
+  uint4 wr[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    wr[q] = *reinterpret_cast<const uint4 *>(slot + 128u * lane + 16u * (uint32_t(q) ^ (lane & 7u)));
+  float p[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) p[t] = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const uint32_t words[4] = {wr[c].x, wr[c].y, wr[c].z, wr[c].w};
+    float bv[16];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const v2f lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, false);
+      const v2f hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[d], 1.0f, true);
+      bv[4 * d + 0] = __fmul_rn(lo.x, sb);
+      bv[4 * d + 1] = __fmul_rn(lo.y, sb);
+      bv[4 * d + 2] = __fmul_rn(hi.x, sb);
+      bv[4 * d + 3] = __fmul_rn(hi.y, sb);
+    }
+    float ac[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) ac[t] = av[t][c];
+    lt_block16<MT>(p, ac, bv);  // k = 16c + i ascending
+  }
+  const uint32_t row = r0 + lane;
+  if (row < N) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+      if (m0 + t < M) part[(size_t(g) * M + (m0 + t)) * N + row] = p[t];
+  }
+}
+
+// y[t][row] = (((0 + part_0) + part_1) + ...) + bias, rounded to bf16 when
+// asked: one thread per (token, row), rows across lanes.
+__global__ __launch_bounds__(256) void k_linear_sum(LinearArgs a, const float *__restrict__ part) {
+  const uint32_t N = a.n, M = a.m, G = a.groups;
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= M * N) return;
+  const uint32_t t = i / N, row = i % N;
+  float acc = 0.0f;
+  for (uint32_t g0 = 0; g0 < G; g0 += 8u) {
+    float v[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8u; ++j) v[j] = g0 + j < G ? part[(size_t(g0 + j) * M + t) * N + row] : 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < 8u; ++j)
+      if (g0 + j < G) acc = __fadd_rn(acc, v[j]);
+  }
+  if (a.bias) acc = __fadd_rn(acc, a.bias[row]);
+  if (a.round_bf16) acc = bf16_round(acc);
+  a.y[size_t(t) * N + row] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -455,6 +654,47 @@ static hipError_t launch_exact_mt(hipStream_t s, const LinearArgs &a, bool vec) 
   return hipGetLastError();
 }
 
+template <int MT>
+static void launch_tile_mt(hipStream_t s, const LinearArgs &a, float *part) {
+  const uint32_t tasks = (a.n + kLTRows - 1) / kLTRows * a.groups;
+  const dim3 grid((tasks + kLTWaves - 1) / kLTWaves, (a.m + MT - 1) / MT);
+  if (a.x_scale_f32 && a.w_scale_f32)
+    k_linear_tile<MT, true, true><<<grid, 64 * kLTWaves, 0, s>>>(a, part);
+  else if (a.x_scale_f32)
+    k_linear_tile<MT, true, false><<<grid, 64 * kLTWaves, 0, s>>>(a, part);
+  else if (a.w_scale_f32)
+    k_linear_tile<MT, false, true><<<grid, 64 * kLTWaves, 0, s>>>(a, part);
+  else
+    k_linear_tile<MT, false, false><<<grid, 64 * kLTWaves, 0, s>>>(a, part);
+}
+
+// The tiled EXACT path, in token chunks whose group partials fit the
+// workspace (kLinPartBytes): tile kernel, then the ordered group sum.
+static hipError_t launch_exact_tiled(hipStream_t s, const LinearArgs &a, const LinearWorkspace &ws) {
+  const size_t per_token = size_t(a.groups) * a.n * sizeof(float);
+  const uint32_t chunk = uint32_t(std::min<size_t>(a.m, kLinPartBytes / per_token));
+  if (chunk == 0) return hipErrorInvalidValue;  // one token's partials exceed the workspace (the caller checks)
+  const uint32_t xs_stride = a.x_scale_f32 ? 4u : 1u;
+  for (uint32_t m0 = 0; m0 < a.m; m0 += chunk) {
+    LinearArgs c = a;
+    c.m = std::min(chunk, a.m - m0);
+    c.x = a.x + size_t(m0) * a.k;
+    c.x_scale = static_cast<const uint8_t *>(a.x_scale) + size_t(m0) * a.groups * xs_stride;
+    c.y = a.y + size_t(m0) * a.n;
+    if (c.m == 1)
+      launch_tile_mt<1>(s, c, ws.part);
+    else if (c.m == 2)
+      launch_tile_mt<2>(s, c, ws.part);
+    else if (c.m <= 4)
+      launch_tile_mt<4>(s, c, ws.part);
+    else
+      launch_tile_mt<8>(s, c, ws.part);
+    k_linear_sum<<<(c.m * c.n + 255u) / 256u, 256, 0, s>>>(c, ws.part);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 hipError_t launch_fp8_linear(hipStream_t s, const LinearArgs &a, int mode, const LinearWorkspace &ws) {
   const bool fast = mode == S14_MODE_FAST && a.k % (4u * kLinGroup) == 0u;
   if (fast) {
@@ -468,6 +708,11 @@ hipError_t launch_fp8_linear(hipStream_t s, const LinearArgs &a, int mode, const
   }
   const bool vec = a.k % 16u == 0u &&
                    ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.w)) & 15u) == 0u;
+  // tiled: whole groups, one token's partials within the workspace, and the
+  // last tile's row offsets within 32 bits (rows past n read zeros)
+  if (vec && a.k % kLinGroup == 0u && size_t(a.groups) * a.n * sizeof(float) <= kLinPartBytes &&
+      uint64_t(a.n + kLTRows - 1) * a.k <= 0xFFFFFFFFull)
+    return launch_exact_tiled(s, a, ws);
   if (a.m == 1) return launch_exact_mt<1>(s, a, vec);
   if (a.m == 2) return launch_exact_mt<2>(s, a, vec);
   if (a.m <= 4) return launch_exact_mt<4>(s, a, vec);

@@ -158,10 +158,11 @@ def test_fp8_linear_f32_scales_bias_bf16(ctx, oracle):
     check_fast(oracle, got, (want - b).astype(np.float64), x, xs, w, ws, "f32 scales")
 
 
-@pytest.mark.parametrize("m,n,k", [(33, 100, 1536), (1, 4000, 512), (8, 96, 16384)])
+@pytest.mark.parametrize("m,n,k", [(33, 100, 1536), (1, 4000, 512), (8, 96, 16384), (2, 300, 1024), (8, 4096, 8192)])
 def test_fp8_linear_fast_edges(ctx, oracle, m, n, k):
     """Row tiles cut by n, two token blocks (m = 33), 12 groups (chunks per
-    wavefront 4 or 12), one group-chunk round (k = 512), and k = 16384."""
+    wavefront 4 or 12), one group-chunk round (k = 512), k = 16384, two
+    tokens, and eight tokens at wo_b's shape."""
     say(f"fp8_linear fast edges m={m} n={n} k={k}")
     rng = np.random.default_rng(n)
     w, ws = codes(rng, (n, k)), rng.integers(114, 122, (-(-n // 128), k // 128), dtype=np.uint8)
@@ -172,3 +173,18 @@ def test_fp8_linear_fast_edges(ctx, oracle, m, n, k):
     assert np.array_equal(host(y).view(np.uint32), want.view(np.uint32))
     s14.fp8_linear(ctx, dev(x), dev(xs), dev(w), dev(ws), y, mode=s14.FAST)
     check_fast(oracle, host(y), want, x, xs, w, ws, f"m={m} n={n} k={k}")
+
+
+def test_fp8_linear_exact_token_chunks(ctx, oracle):
+    """EXACT keeps every group partial of a launch in the context's 32 MiB
+    workspace: at wq_b's shape (8 groups x 32768 rows x 4 bytes per token)
+    40 tokens take two launches of the tiled kernel, 32 tokens then 8."""
+    say("fp8_linear exact token chunks: wq_b m=40")
+    n, k, m = 32768, 1024, 40
+    w, ws = weight(n, k, seed=11)
+    rng = np.random.default_rng(12)
+    x, xs = codes(rng, (m, k)), rng.integers(120, 128, (m, k // 128), dtype=np.uint8)
+    want = oracle.fp8_linear(x, xs, w, ws)
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    s14.fp8_linear(ctx, dev(x), dev(xs), dev(w), dev(ws), y, mode=s14.EXACT)
+    assert np.array_equal(host(y).view(np.uint32), want.view(np.uint32))
