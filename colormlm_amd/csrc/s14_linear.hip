@@ -323,19 +323,29 @@ __global__ __launch_bounds__(64 * kLTWaves) void k_linear_tile(LinearArgs a, flo
 }
 
 // y[t][row] = (((0 + part_0) + part_1) + ...) + bias, rounded to bf16 when
-// asked: one thread per (token, row), rows across lanes.
+// asked: one thread per (token, row), rows across lanes.  kLSumBatch groups'
+// partials are requested at once (8 .. 64 by the group count: one round
+// trip for k <= 8192).
+template <uint32_t kLSumBatch>
 __global__ __launch_bounds__(256) void k_linear_sum(LinearArgs a, const float *__restrict__ part) {
   const uint32_t N = a.n, M = a.m, G = a.groups;
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
   if (i >= M * N) return;
   const uint32_t t = i / N, row = i % N;
+  // the partials (at most kLinPartBytes) through a buffer descriptor: the
+  // lane's offset in a VGPR, each group's in the scalar offset; groups past
+  // G read zeros and are not added
+  const uint32_t stride = 4u * M * N;
+  const Rsrc rp = make_rsrc(part, G * stride);
+  const uint32_t lane_off = 4u * (t * N + row);
   float acc = 0.0f;
-  for (uint32_t g0 = 0; g0 < G; g0 += 8u) {
-    float v[8];
+  for (uint32_t g0 = 0; g0 < G; g0 += kLSumBatch) {
+    float v[kLSumBatch];
 #pragma unroll
-    for (uint32_t j = 0; j < 8u; ++j) v[j] = g0 + j < G ? part[(size_t(g0 + j) * M + t) * N + row] : 0.0f;
+    for (uint32_t j = 0; j < kLSumBatch; ++j)
+      v[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, lane_off, (g0 + j) * stride, 0));
 #pragma unroll
-    for (uint32_t j = 0; j < 8u; ++j)
+    for (uint32_t j = 0; j < kLSumBatch; ++j)
       if (g0 + j < G) acc = __fadd_rn(acc, v[j]);
   }
   if (a.bias) acc = __fadd_rn(acc, a.bias[row]);
@@ -689,7 +699,15 @@ static hipError_t launch_exact_tiled(hipStream_t s, const LinearArgs &a, const L
       launch_tile_mt<4>(s, c, ws.part);
     else
       launch_tile_mt<8>(s, c, ws.part);
-    k_linear_sum<<<(c.m * c.n + 255u) / 256u, 256, 0, s>>>(c, ws.part);
+    const dim3 sum_grid((c.m * c.n + 255u) / 256u);
+    if (c.groups <= 8u)
+      k_linear_sum<8><<<sum_grid, 256, 0, s>>>(c, ws.part);
+    else if (c.groups <= 16u)
+      k_linear_sum<16><<<sum_grid, 256, 0, s>>>(c, ws.part);
+    else if (c.groups <= 32u)
+      k_linear_sum<32><<<sum_grid, 256, 0, s>>>(c, ws.part);
+    else
+      k_linear_sum<64><<<sum_grid, 256, 0, s>>>(c, ws.part);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   }
   return hipSuccess;
