@@ -399,9 +399,10 @@ enum { S14_LINEAR_ROUND_BF16 = 1 };
  * to the CPU oracle's s14o_fp8_linear.  S14_MODE_FAST computes the group
  * dot products on the MFMA (within the reference's own 2e-5 relative
  * tolerance of it); it needs k % 512 == 0 and otherwise runs the EXACT
- * kernel.  FAST keeps split-K partials and arrival counters in a 32 MiB
- * context workspace allocated on the first FAST call: FAST calls on one
- * context must not overlap (serialise them on one stream).
+ * kernel.  Both modes keep partial sums in a 32 MiB context workspace
+ * (FAST: split-K partials and arrival counters; EXACT: per-group partials)
+ * allocated on the first call: fp8_linear calls on one context must not
+ * overlap (serialise them on one stream).
  *
  * Errors (fp8.py:141-171): S14_ERR_SHAPE for m, n or k zero, k > 131072,
  * or sizes past 32-bit addressing; S14_ERR_CAPACITY for a buffer smaller
