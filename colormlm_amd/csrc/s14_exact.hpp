@@ -17,6 +17,7 @@
 
 #include "s14_device.hpp"
 #include "s14_device_util.hpp"
+#include "s14_log1pf.h"
 
 namespace s14 {
 namespace {
@@ -693,15 +694,19 @@ constexpr int kPF = 8;
 // reference uses torch F.linear, executor.py:641, whose order is the
 // BLAS's): lane l sums k = 256c + 4l + j (c ascending, j = 0..3), then the
 // xor butterfly over lanes.  Score: sigmoid (north-star config) or
-// sqrt(softplus) with torch's threshold 20 (executor.py:642).
-// Score and biased score of expert e from its logit.
+// sqrt(softplus) with torch's threshold 20 (executor.py:642), exp and log1p
+// bit-identical to the C library's (s14_expf.h, s14_log1pf.h) as the
+// oracle's.  Score and biased score of expert e from its logit.
 __device__ __forceinline__ float2 router_finish(const RouterArgs &r, float logit, uint32_t e) {
   float sc;
   if (r.score_fn == S14_SCORE_SIGMOID) {
     sc = __fdiv_rn(1.0f, __fadd_rn(1.0f, s14x::expf_glibc(-logit)));
   } else {
-    const float sp = logit > 20.0f ? logit : log1pf(s14x::expf_glibc(logit));
-    sc = __fsqrt_rn(sp);
+    const float sp = logit > 20.0f ? logit : s14x::log1pf_glibc(s14x::expf_glibc(logit));
+    // IEEE square root (HIP's __fsqrt_rn is the approximate native one unless
+    // OCML_BASIC_ROUNDED_OPERATIONS is defined; measured 15 % of results one
+    // ulp off on the softplus range)
+    sc = __builtin_sqrtf(sp);
   }
   return make_float2(sc, __fadd_rn(sc, r.bias[e]));
 }

@@ -335,9 +335,10 @@ def test_router_matches_oracle(ctx, oracle, bank):
     ref = s14.Router(bank["wr_d"], bank["bias_d"], score_fn=N.S14_SCORE_SQRT_SOFTPLUS, route_scale=1.5)
     s14.route(ctx, ref, 1, dev(xs[0]), scores, ids, wts)
     s_o, i_o, w_o = oracle.route(bank["wr"], bank["bias"], xs[0], score_fn=oracle.SCORE_SQRT_SOFTPLUS, route_scale=1.5)
-    np.testing.assert_allclose(host(scores)[0], s_o, rtol=2e-7, atol=0)
+    # exp and log1p are the C library's bit for bit (s14_expf.h, s14_log1pf.h)
+    assert_bit_exact(host(scores)[0], s_o, "sqrt-softplus scores")
     assert host(ids).astype(np.uint16)[0].tolist() == i_o.tolist()
-    np.testing.assert_allclose(host(wts)[0], w_o, rtol=1e-6)
+    assert_bit_exact(host(wts)[0], w_o, "sqrt-softplus weights")
 
 
 def test_router_ties_and_expert_counts(ctx, oracle, bank):
@@ -826,10 +827,8 @@ def test_hash_router_layer_block_prefill(ctx, oracle, bank, score_fn, scale):
     """Hash routing (the reference's layers 0-2: experts from tid2eid[token],
     weights from the chosen scores, executor.py:643-667) through the one-token
     layer (exact and fast), a block of 4, the route-only entry point and a
-    prefill of 4, against the oracle's hash route and layer.  With the
-    sqrt-softplus score the device's log1pf is not glibc's (the scores agree
-    to 1e-6 relative), so there the layers are checked bit for bit against
-    the oracle layer evaluated with the device's own route weights."""
+    prefill of 4, against the oracle's hash route and layer, bit for bit
+    for both score functions."""
     say(f"hash router score_fn={score_fn} scale={scale}")
     tab_h = _tid2eid()
     tab_d = torch.from_numpy(tab_h).cuda()
@@ -845,7 +844,6 @@ def test_hash_router_layer_block_prefill(ctx, oracle, bank, score_fn, scale):
         assert i_o.tolist() == tab_h[tok[t]].tolist()
         routes.append((i_o, w_o))
         want.append(oracle.moe_layer(xs[t], [page_host(bank, int(e)) for e in i_o], w_o, shared))
-    exact_scores = score_fn == N.S14_SCORE_SIGMOID
     # route only
     ids = torch.empty((4, 6), dtype=torch.int16, device="cuda")
     wts = torch.empty((4, 6), dtype=torch.float32, device="cuda")
@@ -853,12 +851,7 @@ def test_hash_router_layer_block_prefill(ctx, oracle, bank, score_fn, scale):
     ids_h, wts_h = host(ids).astype(np.uint16), host(wts)
     for t in range(4):
         assert ids_h[t].tolist() == routes[t][0].tolist()
-        if exact_scores:
-            assert_bit_exact(wts_h[t], routes[t][1], f"hash weights t={t}")
-        else:
-            np.testing.assert_allclose(wts_h[t], routes[t][1], rtol=1e-6)
-            routes[t] = (routes[t][0], wts_h[t])
-            want[t] = oracle.moe_layer(xs[t], [page_host(bank, int(e)) for e in routes[t][0]], wts_h[t], shared)
+        assert_bit_exact(wts_h[t], routes[t][1], f"hash weights t={t}")
     # one token (exact, then fast) and a block of 4 (exact)
     y = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
     s14.moe_layer_route(ctx, router, bank["table"], bank["pages"][256], dev(xs[0]), y, mode=s14.EXACT)
