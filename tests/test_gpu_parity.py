@@ -602,10 +602,13 @@ def _natural(mfma_rows: np.ndarray) -> np.ndarray:
 # 512-token case, rmse_rel 5.1e-3).  The stage checks below pin everything
 # else: x and h requant, the grouped GEMMs, the pair bookkeeping and the
 # combine.
-PREFILL_MAX_REL = 2e-2   # max |y - y_ref| / max |y_ref|
-PREFILL_RMSE_REL = 1e-2  # rmse(y - y_ref) / rms(y_ref)
-GEMM_REL = 2e-4          # a grouped GEMM given the GPU's own operands, vs the oracle's f32 matvec
-FLIP_FRACTION = 2e-3     # h codes allowed to differ from the oracle's requant (each by one e4m3 step)
+# Gates about 1.5-2x the measured worst cases (deterministic runs): token 510
+# max_rel 5.4e-3 / rmse_rel 5.1e-3, every other token below 6e-5; GEMM 5.7e-5;
+# h flips 5.6e-4 of codes.
+PREFILL_MAX_REL = 1e-2     # max |y - y_ref| / max |y_ref|
+PREFILL_RMSE_REL = 7.5e-3  # rmse(y - y_ref) / rms(y_ref)
+GEMM_REL = 1e-4            # a grouped GEMM given the GPU's own operands, vs the oracle's f32 matvec
+FLIP_FRACTION = 1e-3       # h codes allowed to differ from the oracle's requant (each by one e4m3 step)
 
 
 def _prefill_close(oracle, got, want, what):
