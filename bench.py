@@ -550,11 +550,16 @@ def bench_prefill(args, ctx, tables, shared, NL, torch, np, s14, synth):
         L = i % NL
         s14.moe_prefill(ctx, T, routers[L], tables[L], shared[L], xs, y)
 
+    def step_official(i):
+        L = i % NL
+        s14.moe_prefill(ctx, T, routers[L], tables[L], shared[L], xs, y, mode=s14.OFFICIAL)
+
     stats = []
     for L in range(NL):
         step(L)
         stats.append(s14.last_prefill_stats(ctx))
     t = Timer(torch, args.trials).run(step, max(args.prefill_steps, 1), 2)
+    t_off = Timer(torch, args.trials).run(step_official, max(args.prefill_steps, 1), 2)
     ms = t["ms"]
     d = float(np.mean([s["distinct"] for s in stats]))
     nbytes = prefill_bytes(round(d), T)
@@ -571,6 +576,8 @@ def bench_prefill(args, ctx, tables, shared, NL, torch, np, s14, synth):
         "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
         "tflops": flops / (ms * 1e-3) / 1e12,
         "mfma_frac_fp8": flops / (ms * 1e-3) / 1e12 / FP8_MFMA_PEAK_TFLOPS,
+        "official": {"ms_per_prefill": t_off["ms"], "us_per_token": t_off["ms"] * 1e3 / T, "timing": t_off,
+                     "hbm_gbps": nbytes / (t_off["ms"] * 1e-3) / 1e9},
     }
 
 

@@ -237,7 +237,7 @@ SIGNATURES = {
     "s14_moe_block_route_noalloc": (I, [P, U32, C.POINTER(Router), P, P, I, P, P, P, P, I]),
     "s14_noalloc_scratch_bytes": (C.c_uint64, []),
     "s14_route": (I, [P, P, C.POINTER(Router), U32, P, P, P, P]),
-    "s14_moe_prefill": (I, [P, P, U32, C.POINTER(Router), P, P, P, P, P, P]),
+    "s14_moe_prefill": (I, [P, P, U32, C.POINTER(Router), P, P, P, P, P, P, I]),
     "s14_last_prefill_stats": (I, [P, C.POINTER(U32), C.POINTER(U32), C.POINTER(U32)]),
     "s14_requant_e4m3": (I, [P, P, U32, U32, P, P, P]),
     "s14_act_quant_e4m3": (I, [P, P, U32, U32, U32, P, P, P]),

@@ -621,6 +621,8 @@ int prefill_workspace(s14_ctx *ctx) {
   const size_t o_ht = take(n_items * kHTileBytes);
   const size_t o_hts = take(n_items * kHScaleBytes);
   const size_t o_down = take(sizeof(float) * size_t(P) * kHidden);
+  const size_t o_pw = take(sizeof(float) * size_t(P));
+  const size_t o_hf = take(sizeof(float) * size_t(P) * kInter);
   S14_HIP(hipSetDevice(ctx->device), "hipSetDevice");
   S14_HIP(hipMalloc(&ctx->prefill_base, off), "hipMalloc(prefill workspace)");
   // the token bitmaps start clear; every prefill's grouping step clears them again
@@ -646,6 +648,8 @@ int prefill_workspace(s14_ctx *ctx) {
   w.ht = b + o_ht;
   w.hts = b + o_hts;
   w.down = reinterpret_cast<float *>(b + o_down);
+  w.pair_weight = reinterpret_cast<float *>(b + o_pw);
+  w.hf = reinterpret_cast<float *>(b + o_hf);
   w.bytes = off;
   return S14_OK;
 }
@@ -654,8 +658,10 @@ int prefill_workspace(s14_ctx *ctx) {
 
 extern "C" int s14_moe_prefill(s14_ctx *ctx, void *stream, uint32_t tokens, const s14_router *router,
                                const uint64_t *expert_pages_dev, const uint8_t *shared_page, const float *x,
-                               float *y, uint16_t *ids_out, float *weights_out) {
+                               float *y, uint16_t *ids_out, float *weights_out, int mode) {
   if (int rc = check_ctx(ctx)) return rc;
+  if (mode != S14_MODE_EXACT && mode != S14_MODE_FAST && mode != S14_MODE_OFFICIAL)
+    return fail(S14_ERR_INVALID, "unknown mode %d", mode);
   if (int rc = check_router(router)) return rc;
   if (router->topk != uint32_t(s14::kTopK))
     return fail(S14_ERR_SHAPE, "prefill requires topk=%d", s14::kTopK);
@@ -664,8 +670,9 @@ extern "C" int s14_moe_prefill(s14_ctx *ctx, void *stream, uint32_t tokens, cons
   if (!expert_pages_dev || !shared_page || !x || !y) return fail(S14_ERR_INVALID, "NULL prefill buffer");
   if (int rc = prefill_workspace(ctx)) return rc;
   hipStream_t st = pick(ctx, stream);
-  const s14::PrefillArgs a{router_args(router), tokens, expert_pages_dev, shared_page, ctx->mx, x, y,
-                           ids_out, weights_out, s14::status_word(ctx->ws)};
+  const s14::PrefillArgs a{router_args(router), tokens,      expert_pages_dev,          shared_page,
+                           ctx->mx,              x,           y,                         ids_out,
+                           weights_out,          s14::status_word(ctx->ws), mode == S14_MODE_OFFICIAL ? 1 : 0};
   const hipError_t e = s14::launch_prefill(st, a, ctx->pws);
   if (e != hipSuccess) return hip_fail(e, "prefill launch");
   ctx->prefill_tokens = tokens;

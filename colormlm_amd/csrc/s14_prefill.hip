@@ -51,7 +51,12 @@ constexpr uint32_t kQGroup = 32;  // requant group (k values per E8M0 scale)
 using s14x::e4m3_rne_sat;  // s14_e4m3.h: straight-line, checked against the oracle on the CPU
 
 // X [T, 4096] f32 -> Q [T, 4096] e4m3 in MFMA order + S [T, 128] E8M0.
-// One thread per 32-value group.
+// One thread per 32-value group.  kOfficial: the official act_quant's group
+// of 128 (l42_reference.py:390-403): the maximum over the four adjacent
+// threads of a 128-value group, whose four E8M0 bytes then hold the same
+// code (a token's 128 groups and a workgroup's 256 threads are whole quads,
+// so a quad returns early together or not at all).
+template <bool kOfficial>
 __global__ __launch_bounds__(256) void k_requant_x(uint32_t tokens, const float *__restrict__ X,
                                                    uint8_t *__restrict__ Q, uint8_t *__restrict__ S) {
   const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
@@ -71,6 +76,13 @@ __global__ __launch_bounds__(256) void k_requant_x(uint32_t tokens, const float 
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 32; ++i) amax = fabsf(v[i]) > amax ? fabsf(v[i]) : amax;
+  if constexpr (kOfficial) {
+    // NaN never compares greater, as in the scan above
+    const float a1 = __shfl_xor(amax, 1);
+    amax = a1 > amax ? a1 : amax;
+    const float a2 = __shfl_xor(amax, 2);
+    amax = a2 > amax ? a2 : amax;
+  }
   const uint32_t code = requant_code(amax);
   const float inv = __uint_as_float((254u - code) << 23);  // 2^-(code-127)
   uint32_t w[8];
@@ -230,10 +242,12 @@ __global__ __launch_bounds__(1024) void k_prefill_group(PrefillArgs a, PrefillWo
       const uint32_t p = off[e] + rank;
       ws.pair_token[p] = t;
       ws.token_pair[t * kSlots + s] = p;
+      ws.pair_weight[p] = ws.weights[t * kTopK + s];
     }
     const uint32_t ps = off[kMaxExperts] + t;
     ws.pair_token[ps] = t;
     ws.token_pair[t * kSlots + a.r.topk] = ps;
+    ws.pair_weight[ps] = 1.0f;
   }
 }
 
@@ -380,6 +394,10 @@ __device__ __forceinline__ void load_bchunk(BChunk &b, Rsrc tile, Rsrc scales, u
 // ahead in LDS, activations kRing chunks ahead in VGPRs.  Then h =
 // swiglu(g, u), requantised per token over the tile's 32 rows (one E8M0
 // group of phase 2's K) and stored into the item's phase-2 tile.
+// kOfficial: h = bf16(swiglu(bf16(g), bf16(u)) * w), w the pair's route
+// weight (1 for the shared expert) (executor.py:717-731), stored in f32 for
+// k_requant_h128 (its group of 128 rows spans four of these workgroups).
+template <bool kOfficial>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_prefill_up(PrefillArgs a,
                                                                                                 PrefillWorkspace ws) {
   const uint32_t n_items = ws.stats[0];
@@ -484,6 +502,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   double *exptab = reinterpret_cast<double *>(up_slot0);  // slot 0's last chunk is consumed
   if (lane < 32) exptab[lane] = exp_entry;
   __syncthreads();  // one wavefront: orders the table writes before the lookups
+  if constexpr (kOfficial) {
+    if (col >= it.count) return;
+    const uint32_t pair = it.first + col;
+    const float w = ws.pair_weight[pair];
+    float *dst = ws.hf + size_t(pair) * kInter + rt * 32u;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      float o[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int i = 4 * q4 + v;
+        o[v] = bf16_round(__fmul_rn(swiglu_exact(bf16_round(g[i]), bf16_round(u[i]), exptab), w));
+      }
+      *reinterpret_cast<float4 *>(dst + 8u * q4 + 4u * h) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+    return;
+  }
   float hv[16];
   float amax = 0.0f;
 #pragma unroll
@@ -513,9 +548,61 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       uint8_t(code);
 }
 
+// Official mode: the w2 input's act_quant (group 128) of every work item's
+// h columns into the item's phase-2 tile and scales, in the layout
+// k_prefill_up's epilogue writes otherwise (tile rt holds rows 32 rt .. +31,
+// half rt % 2 of K step rt / 2).  Eight lanes per (item, column, 128 rows),
+// each lane 16 rows (64 contiguous bytes in, one 16-byte piece out); the
+// group's maximum by xor shuffles within the eight.
+constexpr uint32_t kHGroups128 = kInter / 128;
+__global__ __launch_bounds__(256) void k_requant_h128(PrefillWorkspace ws) {
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t j = gid & 7u, grp = gid >> 3;  // 16-row piece j of group grp = (item, column, m)
+  const uint32_t item = grp / (kItemTokens * kHGroups128);
+  if (item >= ws.stats[0]) return;  // whole groups of eight lanes return together
+  const uint32_t col = (grp / kHGroups128) % kItemTokens, m = grp % kHGroups128;
+  const PrefillItem it = ws.items[item];
+  if (col >= it.count) return;  // phase 2 never reads absent columns
+  const float4 *src =
+      reinterpret_cast<const float4 *>(ws.hf + size_t(it.first + col) * kInter + 128u * m + 16u * j);
+  float4 q[4];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    q[i] = src[i];
+    amax = fabsf(q[i].x) > amax ? fabsf(q[i].x) : amax;
+    amax = fabsf(q[i].y) > amax ? fabsf(q[i].y) : amax;
+    amax = fabsf(q[i].z) > amax ? fabsf(q[i].z) : amax;
+    amax = fabsf(q[i].w) > amax ? fabsf(q[i].w) : amax;
+  }
+#pragma unroll
+  for (int d = 1; d < 8; d <<= 1) {  // NaN never compares greater, as in the scan above
+    const float o = __shfl_xor(amax, d);
+    amax = o > amax ? o : amax;
+  }
+  const uint32_t code = requant_code(amax);
+  const float inv = __uint_as_float((254u - code) << 23);
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = e4m3_rne_sat(__fmul_rn(q[i].x, inv)) | (e4m3_rne_sat(__fmul_rn(q[i].y, inv)) << 8) |
+           (e4m3_rne_sat(__fmul_rn(q[i].z, inv)) << 16) | (e4m3_rne_sat(__fmul_rn(q[i].w, inv)) << 24);
+  const uint32_t rt = 4u * m + j / 2u, s2 = rt >> 1, blk = rt & 1u;
+  const uint32_t pos = (j & 1u) == 0u ? 16u * blk : 32u + 16u * blk;  // MFMA order of the piece in its step
+  uint8_t *tile = ws.ht + size_t(item) * kHTileBytes;
+  *reinterpret_cast<uint4 *>(tile + 2048u * s2 + 1024u * ((pos >> 4) & 1u) + 16u * (col + 32u * (pos >> 5))) =
+      make_uint4(w[0], w[1], w[2], w[3]);
+  if (j < 4u) {  // the scale byte of tile 4m + j
+    const uint32_t rs = 4u * m + j, ss = rs >> 1, bs = rs & 1u;
+    ws.hts[size_t(item) * kHScaleBytes + ((ss / kChunkSteps) * 64u + col + 32u * bs) * 4u + ss % kChunkSteps] =
+        uint8_t(code);
+  }
+}
+
 // Phase 2: one wavefront per (32-row tile of w2, work item): down rows of
 // every pair of the item, f32, route weight not applied.  K = 2048 in 8
-// chunks, the same rings as phase 1.
+// chunks, the same rings as phase 1.  kOfficial: rounded to bf16.
+template <bool kOfficial>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_prefill_down(PrefillArgs a,
                                                                                              PrefillWorkspace ws) {
   const uint32_t n_items = ws.stats[0];
@@ -599,13 +686,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
   if (col >= it.count) return;
   float *dst = ws.down + size_t(it.first + col) * kHidden + rt * 32u;
 #pragma unroll
-  for (int q4 = 0; q4 < 4; ++q4)
-    *reinterpret_cast<float4 *>(dst + 8u * q4 + 4u * h) =
-        make_float4(d[0][4 * q4], d[0][4 * q4 + 1], d[0][4 * q4 + 2], d[0][4 * q4 + 3]);
+  for (int q4 = 0; q4 < 4; ++q4) {
+    float4 o = make_float4(d[0][4 * q4], d[0][4 * q4 + 1], d[0][4 * q4 + 2], d[0][4 * q4 + 3]);
+    if constexpr (kOfficial) o = make_float4(bf16_round(o.x), bf16_round(o.y), bf16_round(o.z), bf16_round(o.w));
+    *reinterpret_cast<float4 *>(dst + 8u * q4 + 4u * h) = o;
+  }
 }
 
 // y[t] = 0; y += w_s * down_s in route order; y += shared down
 // (s14_vulkan_numeric.rs:929-946).  One thread per (token, 4 features).
+// kOfficial: the route weights are already in h; y = bf16(sum of the bf16
+// outputs in route order, shared last, in f32) (executor.py:712-739).
+template <bool kOfficial>
 __global__ __launch_bounds__(256) void k_prefill_combine(PrefillArgs a, PrefillWorkspace ws) {
   const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= a.tokens * (kHidden / 4)) return;
@@ -614,7 +706,7 @@ __global__ __launch_bounds__(256) void k_prefill_combine(PrefillArgs a, PrefillW
   for (uint32_t s = 0; s <= a.r.topk; ++s) {
     const uint32_t p = ws.token_pair[t * kSlots + s];
     const float4 d = *reinterpret_cast<const float4 *>(ws.down + size_t(p) * kHidden + r);
-    if (s < a.r.topk) {
+    if (s < a.r.topk && !kOfficial) {
       const float w = ws.weights[t * kTopK + s];
       acc.x = __fadd_rn(acc.x, __fmul_rn(w, d.x));
       acc.y = __fadd_rn(acc.y, __fmul_rn(w, d.y));
@@ -627,6 +719,7 @@ __global__ __launch_bounds__(256) void k_prefill_combine(PrefillArgs a, PrefillW
       acc.w = __fadd_rn(acc.w, d.w);
     }
   }
+  if constexpr (kOfficial) acc = make_float4(bf16_round(acc.x), bf16_round(acc.y), bf16_round(acc.z), bf16_round(acc.w));
   *reinterpret_cast<float4 *>(a.y + size_t(t) * kHidden + r) = acc;
 }
 
@@ -642,12 +735,24 @@ hipError_t launch_prefill(hipStream_t s, const PrefillArgs &a, const PrefillWork
   if (e != hipSuccess) return e;
   k_prefill_topk<<<(T + 3) / 4, 256, 0, s>>>(a, ws);
   k_prefill_group<<<1, 1024, 0, s>>>(a, ws);
-  k_requant_x<<<(T * (kHidden / kQGroup) + 255) / 256, 256, 0, s>>>(T, a.x, ws.xq, ws.xs);
+  const uint32_t rq_blocks = (T * (kHidden / kQGroup) + 255) / 256;
+  if (a.official)
+    k_requant_x<true><<<rq_blocks, 256, 0, s>>>(T, a.x, ws.xq, ws.xs);
+  else
+    k_requant_x<false><<<rq_blocks, 256, 0, s>>>(T, a.x, ws.xq, ws.xs);
   const uint32_t max_items = prefill_max_items(T);
   k_tile_x<<<max_items * (kXTileBytes / 16 / 256), 256, 0, s>>>(ws);
-  k_prefill_up<<<dim3(kInter / 32, max_items), 64, 0, s>>>(a, ws);
-  k_prefill_down<<<dim3(kHidden / 32, max_items), 64, 0, s>>>(a, ws);
-  k_prefill_combine<<<(T * (kHidden / 4) + 255) / 256, 256, 0, s>>>(a, ws);
+  const uint32_t cb_blocks = (T * (kHidden / 4) + 255) / 256;
+  if (a.official) {
+    k_prefill_up<true><<<dim3(kInter / 32, max_items), 64, 0, s>>>(a, ws);
+    k_requant_h128<<<max_items * kItemTokens * kHGroups128 * 8u / 256u, 256, 0, s>>>(ws);
+    k_prefill_down<true><<<dim3(kHidden / 32, max_items), 64, 0, s>>>(a, ws);
+    k_prefill_combine<true><<<cb_blocks, 256, 0, s>>>(a, ws);
+  } else {
+    k_prefill_up<false><<<dim3(kInter / 32, max_items), 64, 0, s>>>(a, ws);
+    k_prefill_down<false><<<dim3(kHidden / 32, max_items), 64, 0, s>>>(a, ws);
+    k_prefill_combine<false><<<cb_blocks, 256, 0, s>>>(a, ws);
+  }
   return hipGetLastError();
 }
 

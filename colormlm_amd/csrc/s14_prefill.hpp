@@ -50,6 +50,7 @@ struct PrefillArgs {
   uint16_t *ids_out;
   float *weights_out;
   uint32_t *status;  // the context workspace's status word (kStatus* bits)
+  int official;      // 1: the official expert semantics (S14_MODE_OFFICIAL)
 };
 
 // Device workspace for up to kMaxPrefillTokens tokens (one allocation per
@@ -71,6 +72,8 @@ struct PrefillWorkspace {
   uint8_t *ht;            // [items][kHTileBytes] e4m3 SwiGLU output, item tile
   uint8_t *hts;           // [items][kHScaleBytes]
   float *down;            // [7T][4096]
+  float *pair_weight;     // [7T]: each pair's route weight (1 for the shared expert)
+  float *hf;              // [7T][2048]: official mode's h (bf16 values) before its group-128 requant
   size_t bytes;
 };
 

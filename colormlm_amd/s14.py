@@ -27,7 +27,7 @@ from ._native import S14Error, check, lib
 
 EXACT = N.S14_MODE_EXACT
 FAST = N.S14_MODE_FAST
-OFFICIAL = N.S14_MODE_OFFICIAL  # fused expert entry points only
+OFFICIAL = N.S14_MODE_OFFICIAL  # fused expert entry points and the prefill only
 
 
 def _ptr(t) -> int:
@@ -450,16 +450,18 @@ def route(ctx: Context, router: Router, tokens: int, x, scores_out=None, ids_out
 
 
 def moe_prefill(ctx: Context, tokens: int, router: Router, expert_pages, shared_page, x, y, ids_out=None,
-                weights_out=None, stream=None) -> None:
+                weights_out=None, stream=None, mode: int = EXACT) -> None:
     """Config 4: `tokens` rows of x [tokens, 4096] through the router and the
     top-6 routed + shared MXFP4 experts as grouped scaled-MFMA GEMMs on
     e4m3-requantised activations (per-32 E8M0); y [tokens, 4096].  Not
-    order-exact (the MFMA's own summation), see the C header."""
+    order-exact (the MFMA's own summation), see the C header.  mode=OFFICIAL:
+    the official expert semantics (group-128 act_quant, bf16 outputs, route
+    weight before w2)."""
     r = router.c()
     check(
         lib().s14_moe_prefill(
             ctx.handle, _stream(stream), tokens, C.byref(r), _ptr(expert_pages), _ptr(shared_page), _ptr(x), _ptr(y),
-            _ptr(ids_out), _ptr(weights_out)
+            _ptr(ids_out), _ptr(weights_out), mode
         )
     )
 

@@ -122,7 +122,8 @@ typedef struct {
  * so results are bit-identical to it.  S14_MODE_FAST splits K across a
  * wavefront and reduces with cross-lane adds: HBM-bound, not bit-identical.
  * S14_MODE_OFFICIAL (fused expert entry points only: expert chain, MoE
- * layer, routed layer/block, no-alloc block) computes the model's official
+ * layer, routed layer/block, no-alloc block, and the prefill, whose dot
+ * products are the MFMA's) computes the model's official
  * expert (executor.py:712-744, l42_reference.py:390-419): each linear's
  * activation requantised to e4m3 with one power-of-two scale per 128
  * values, each linear's output rounded to bf16, the route weight applied to
@@ -324,10 +325,15 @@ int s14_route(s14_ctx *ctx, void *stream, const s14_router *router, uint32_t tok
  * group 32) before w1/w3 and again (h) before w2.  Not order-exact: results
  * agree with the CPU oracle to a measured tolerance.  The shared page must
  * be MXFP4.  ids_out [T, 6] u16 and weights_out [T, 6] f32 may be NULL.
+ * mode: S14_MODE_EXACT or S14_MODE_FAST run the semantics above (one
+ * numeric path, the MFMA's); S14_MODE_OFFICIAL the model's official expert
+ * (executor.py:712-744): act_quant group 128 before every linear, g, u and
+ * each expert output rounded to bf16, the route weight applied to h before
+ * w2, y = bf16(f32 sum of the outputs in route order, shared last).
  * The first call on a context allocates its prefill workspace. */
 int s14_moe_prefill(s14_ctx *ctx, void *stream, uint32_t tokens, const s14_router *router,
                     const uint64_t *expert_pages_dev, const uint8_t *shared_page, const float *x,
-                    float *y, uint16_t *ids_out, float *weights_out);
+                    float *y, uint16_t *ids_out, float *weights_out, int mode);
 /* Distinct routed experts, the largest tokens-per-expert and the number of
  * GEMM work items of the last prefill (synchronises the device). */
 int s14_last_prefill_stats(s14_ctx *ctx, uint32_t *distinct, uint32_t *max_tokens,

@@ -754,6 +754,129 @@ def test_prefill_config4_512_properties(ctx, oracle, bank, prefill_router):
         _prefill_close(oracle, y[t], want, f"token {t}")
 
 
+def _bf16(a) -> np.ndarray:
+    """Round f32 values to bf16 (RNE, torch's cast; the oracle's own bf16
+    rounding is pinned to it in tests/test_official.py)."""
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).to(torch.float32).numpy()
+
+
+def _bf16_ulp(v) -> np.ndarray:
+    """Spacing of bf16 values at |v| (8 significand bits)."""
+    _, e = np.frexp(np.abs(np.asarray(v, np.float64)))
+    return np.ldexp(1.0, e - 8)
+
+
+# Official end to end: y is bf16, so on top of the MFMA path's tolerance a
+# token may differ by one bf16 step of its largest output (2 at |y| >= 256,
+# 0.8 % of max|y| alone).  Measured over 128 tokens (seeds 2 and 3): max-abs
+# <= 2, max_rel <= 8.4e-3, rmse_rel <= 5.4e-3 (tokens with an h flip), median
+# rmse_rel 6e-4.
+def _prefill_close_official(oracle, got, want, what):
+    st = oracle.error_stats(got, want)
+    scale = float(np.max(np.abs(want)))
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    bound = PREFILL_MAX_REL * scale + float(_bf16_ulp(scale))
+    rel = {"max_rel": st["max_abs"] / scale, "rmse_rel": st["rmse"] / rms}
+    say(f"  {what}: max_abs {st['max_abs']:.3g} (bound {bound:.3g}) rmse {st['rmse']:.3g} max|y| {scale:.1f} -> {rel}")
+    assert st["finite"]
+    assert st["max_abs"] <= bound and rel["rmse_rel"] <= PREFILL_RMSE_REL, f"{what}: {rel}"
+    return rel
+
+
+def _run_prefill_official(ctx, bank, pr, xs):
+    T = xs.shape[0]
+    y = torch.empty((T, HIDDEN), dtype=torch.float32, device="cuda")
+    ids = torch.empty((T, 6), dtype=torch.int16, device="cuda")
+    wts = torch.empty((T, 6), dtype=torch.float32, device="cuda")
+    s14.moe_prefill(ctx, T, pr["router"], bank["table"], bank["pages"][256], dev(xs), y, ids, wts,
+                    mode=s14.OFFICIAL)
+    return host(y), host(ids).astype(np.uint16), host(wts)
+
+
+def _check_prefill_official_stages(oracle, bank, view, xs, ids, wts, y, pairs_to_check):
+    """Official prefill (executor.py:712-744 on the MFMA path): x act_quant
+    (group 128) bit-exact; every token's combine (f32 sum of the bf16 expert
+    outputs in route order, shared last, then bf16) bit-exact; each checked
+    pair's h (bf16 g and u, SwiGLU times the route weight, bf16, act_quant
+    group 128) equal to the oracle's from the same x codes or one e4m3 step
+    away, at most FLIP_FRACTION of them; its bf16 w2 output, given the GPU's
+    own h, within two bf16 steps plus GEMM_REL of the oracle's."""
+    T = xs.shape[0]
+    q_o, s_o = oracle.requant_e4m3(xs, 128)
+    assert np.array_equal(_natural(view["xq"]), q_o), "x act_quant codes"
+    assert np.array_equal(view["xs"], np.repeat(s_o, 4, axis=1)), "x act_quant scales"
+    tp, pt = view["token_pair"], view["pair_token"]
+    down = view["down"]
+    for t in range(T):
+        acc = np.zeros(HIDDEN, np.float32)
+        for s_ in range(7):
+            acc = (acc + down[tp[t, s_]]).astype(np.float32)
+        assert_bit_exact(y[t], _bf16(acc), f"official combine token {t}")
+    vals, grid = _e4m3_values(oracle)
+    flips = codes = scale_miss = 0
+    worst_gemm = 0.0
+    pages = {}
+    for p in pairs_to_check:
+        t = int(pt[p])
+        slot = list(tp[t]).index(p)
+        e = int(ids[t, slot]) if slot < 6 else 256
+        if e not in pages:
+            pages[e] = mx_parts(page_host(bank, e))
+        m = pages[e]
+        w = np.float32(wts[t, slot]) if slot < 6 else np.float32(1.0)
+        xd = oracle.dequant_requant(q_o[t], s_o[t], 128)[0]
+        g = _bf16(oracle.mxfp4_matvec(xd, m["w1"], m["s1"]))
+        u = _bf16(oracle.mxfp4_matvec(xd, m["w3"], m["s3"]))
+        h_ref = _bf16((oracle.swiglu_limit(g, u) * w).astype(np.float32))
+        hq_ref, hs_ref = oracle.requant_e4m3(h_ref, 128)
+        hq, hs = _natural(view["hq"][p]), view["hs"][p]
+        assert np.all(hs.reshape(16, 4) == hs.reshape(16, 4)[:, :1]), f"pair {p}: scales differ within a group of 128"
+        ok_scale = hs.reshape(16, 4)[:, 0] == hs_ref[0]
+        scale_miss += int(np.count_nonzero(~ok_scale))
+        in_ok = np.repeat(ok_scale, 128)
+        diff = np.flatnonzero((hq != hq_ref[0]) & in_ok)
+        steps = np.abs(np.searchsorted(grid, vals[hq[diff]]) - np.searchsorted(grid, vals[hq_ref[0][diff]]))
+        assert np.all(steps <= 1), f"pair {p}: h codes more than one e4m3 step off at {diff[steps > 1][:5]}"
+        flips += diff.size
+        codes += int(np.count_nonzero(in_ok))
+        hd = oracle.dequant_requant(hq[None], hs[None])[0]
+        d_ref = oracle.mxfp4_matvec(hd, m["w2"], m["s2"])
+        scale = float(np.max(np.abs(d_ref)))
+        err = np.abs(down[p].astype(np.float64) - _bf16(d_ref))
+        worst_gemm = max(worst_gemm, float(np.max(err / (2.0 * _bf16_ulp(d_ref) + GEMM_REL * scale))))
+        assert np.all(err <= 2.0 * _bf16_ulp(d_ref) + GEMM_REL * scale), f"pair {p} (expert {e}, token {t}): w2"
+    say(f"  official stages: {len(pairs_to_check)} pairs, w2 worst {worst_gemm:.3g} of its bound, "
+        f"h flips {flips}/{codes}, h scale groups off {scale_miss}")
+    assert flips <= FLIP_FRACTION * codes
+    assert scale_miss <= 2e-3 * len(pairs_to_check) * 16
+
+
+@pytest.mark.parametrize("tokens", [64, 5])
+def test_prefill_official(ctx, oracle, bank, prefill_router, tokens):
+    """The official expert semantics on the prefill's MFMA path: routes as the
+    default prefill's, the stage checks above, and each checked token's output
+    against the oracle's official layer (s14o_moe_layer_official)."""
+    say(f"config 4 prefill T={tokens}, official semantics")
+    xs = synth.prefill_tokens(seed=2, tokens=tokens)
+    y, ids, wts = _run_prefill_official(ctx, bank, prefill_router, xs)
+    for t in range(tokens):
+        _, i_o, w_o = oracle.route(prefill_router["wr"], prefill_router["bias"], xs[t])
+        assert ids[t].tolist() == i_o.tolist(), f"route t={t}"
+        assert_bit_exact(wts[t], w_o, f"route weights t={t}")
+    view = s14.last_prefill_view(ctx)
+    check = sorted({int(p) for t in range(0, tokens, 8) for p in view["token_pair"][t]})
+    _check_prefill_official_stages(oracle, bank, view, xs, ids, wts, y, check)
+    shared = page_host(bank, 256)
+    worst = {"max_rel": 0.0, "rmse_rel": 0.0}
+    for t in sorted({0, tokens // 2, tokens - 1}):
+        want = oracle.moe_layer_official(xs[t], [page_host(bank, int(e)) for e in ids[t]], wts[t], shared)
+        rel = _prefill_close_official(oracle, y[t], want, f"official token {t}")
+        worst = {k: max(worst[k], rel[k]) for k in worst}
+    say(f"  official end to end worst {worst}")
+    y2, _, _ = _run_prefill_official(ctx, bank, prefill_router, xs)
+    assert_bit_exact(y2, y, "official repeat run")
+
+
 @pytest.mark.parametrize("tokens", [1, 5, 1024])
 def test_prefill_ragged_and_max_tokens(ctx, oracle, bank, prefill_router, tokens):
     """1 and 5 tokens (partial MFMA column tiles) and the 1024-token maximum:
