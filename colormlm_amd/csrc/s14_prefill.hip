@@ -326,7 +326,11 @@ __device__ __forceinline__ uint32_t swz(uint32_t r) { return (r + (r >> 3)) & 7u
 __device__ __forceinline__ uint32_t swz4(uint32_t r) { return (r + (r >> 2)) & 3u; }
 
 constexpr uint32_t kUpSlotBytes = 2 * 32 * 128;  // w1 and w3 chunks
-constexpr uint32_t kDnSlotBytes = 32 * 128;      // w2 chunk
+// w2 rows per phase-2 wavefront: two 32-row MFMA tiles sharing each
+// activation operand (with one tile a wavefront read twice as many
+// activation bytes as weight bytes; measured 249 -> see the design notes)
+constexpr uint32_t kDnRows = 64;
+constexpr uint32_t kDnSlotBytes = kDnRows * 128;  // w2 chunk
 __shared__ __attribute__((aligned(16))) uint8_t up_slot0[kUpSlotBytes];
 __shared__ __attribute__((aligned(16))) uint8_t up_slot1[kUpSlotBytes];
 __shared__ __attribute__((aligned(16))) uint8_t up_slot2[kUpSlotBytes];
@@ -336,7 +340,7 @@ __shared__ __attribute__((aligned(16))) uint8_t dn_slot0[kDnSlotBytes];
 __shared__ __attribute__((aligned(16))) uint8_t dn_slot1[kDnSlotBytes];
 __shared__ __attribute__((aligned(16))) uint8_t dn_slot2[kDnSlotBytes];
 __shared__ __attribute__((aligned(16))) uint8_t dn_slot3[kDnSlotBytes];
-__shared__ __attribute__((aligned(16))) uint8_t dn_scales[32 * (kInter / 32)];  // s2 of the tile
+__shared__ __attribute__((aligned(16))) uint8_t dn_scales[kDnRows * (kInter / 32)];  // s2 of the tile
 
 template <int S>
 struct Slot {
@@ -599,38 +603,41 @@ __global__ __launch_bounds__(256) void k_requant_h128(PrefillWorkspace ws) {
   }
 }
 
-// Phase 2: one wavefront per (32-row tile of w2, work item): down rows of
-// every pair of the item, f32, route weight not applied.  K = 2048 in 8
-// chunks, the same rings as phase 1.  kOfficial: rounded to bf16.
+// Phase 2: one wavefront per (64-row tile of w2, work item): down rows of
+// every pair of the item, f32, route weight not applied, as two 32-row
+// MFMA tiles that share each activation operand.  K = 2048 in 8 chunks, the
+// same rings as phase 1.  kOfficial: rounded to bf16.
 template <bool kOfficial>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_prefill_down(PrefillArgs a,
-                                                                                             PrefillWorkspace ws) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_prefill_down(PrefillArgs a,
+                                                                                                  PrefillWorkspace ws) {
   const uint32_t n_items = ws.stats[0];
   const uint32_t item = blockIdx.y;
   if (item >= n_items) return;
   const PrefillItem it = ws.items[item];
-  const uint32_t rt = blockIdx.x;
+  const uint32_t rt = blockIdx.x;  // 64-row tile
   const uint32_t lane = threadIdx.x & 63, col = lane & 31, h = lane >> 5;
   const Rsrc rp = page_rsrc(a, it.expert);
   constexpr uint32_t kRowBytes = kInter / 2, kScaleRow = kInter / 32;
   constexpr uint32_t kChunks = kInter / 64 / kChunkSteps;
+  constexpr uint32_t kDma = kDnRows / 8;  // DMA loads per chunk: 8 rows each
   const uint32_t lrow = lane >> 3;
-  uint32_t dma_off[4];
+  uint32_t dma_off[kDma];
 #pragma unroll
-  for (uint32_t j = 0; j < 4; ++j)
-    dma_off[j] = uint32_t(a.mx.w2) + (rt * 32u + 8u * j + lrow) * kRowBytes + 16u * ((lane & 7u) ^ ((j + lrow) & 7u));
+  for (uint32_t j = 0; j < kDma; ++j)
+    dma_off[j] =
+        uint32_t(a.mx.w2) + (rt * kDnRows + 8u * j + lrow) * kRowBytes + 16u * ((lane & 7u) ^ ((j + lrow) & 7u));
   auto issue = [&](auto slot_tag, uint32_t c) {
     uint8_t *dst = dn_slot<decltype(slot_tag)::value>();
     lds_reads_done();
 #pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) dma16(rp, dst + 1024u * j, dma_off[j] + 128u * c);
+    for (uint32_t j = 0; j < kDma; ++j) dma16(rp, dst + 1024u * j, dma_off[j] + 128u * c);
   };
-  // scales: 32 rows x 64 bytes; load j covers rows 16j..16j+15, 4 lanes a row
+  // scales: 64 rows x 64 bytes; load j covers rows 16j..16j+15, 4 lanes a row
 #pragma unroll
-  for (uint32_t j = 0; j < 2; ++j) {
+  for (uint32_t j = 0; j < kDnRows / 16; ++j) {
     const uint32_t row = 16u * j + (lane >> 2);
     dma16(rp, dn_scales + 1024u * j,
-          uint32_t(a.mx.s2) + (rt * 32u + row) * kScaleRow + 16u * ((lane & 3u) ^ swz4(row)));
+          uint32_t(a.mx.s2) + (rt * kDnRows + row) * kScaleRow + 16u * ((lane & 3u) ^ swz4(row)));
   }
   const Rsrc ht = make_rsrc(ws.ht + size_t(item) * kHTileBytes, kHTileBytes);
   const Rsrc hts = make_rsrc(ws.hts + size_t(item) * kHScaleBytes, kHScaleBytes);
@@ -645,22 +652,36 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
     load_bchunk(rb[j], ht, hts, uint32_t(j), tb, sbb);
     __builtin_amdgcn_sched_barrier(0);  // chunk order, so the loop's waits count the ring right
   }
-  v16f d[1];
+  constexpr int NT = int(kDnRows / 32);  // MFMA tiles
+  v16f d[NT];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) d[0][i] = 0.0f;
-  const uint32_t sw = swz(col), sw4 = swz4(col);
+  for (int tl = 0; tl < NT; ++tl)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) d[tl][i] = 0.0f;
+  // the lane's rows 32 tl + col, one per tile
+  uint32_t sw[NT], s4[NT];
+#pragma unroll
+  for (int tl = 0; tl < NT; ++tl) {
+    sw[tl] = swz(32u * uint32_t(tl) + col);
+    s4[tl] = swz4(32u * uint32_t(tl) + col);
+  }
   auto chunk = [&](auto slot_tag, uint32_t c, bool refill) {
     constexpr int S = decltype(slot_tag)::value;
-    const uint8_t *src = dn_slot<S>() + 128u * col;
+    const uint8_t *src = dn_slot<S>();
 #pragma unroll
     for (uint32_t k = 0; k < kChunkSteps; ++k) {
-      const uint32_t q = (2u * k + h) ^ sw;
-      const uint4 aw = *reinterpret_cast<const uint4 *>(src + 16u * q);
+      const uint32_t p = 2u * k + h;
       const uint32_t sb = 2u * (c * kChunkSteps + k) + h;
-      const uint32_t ca = dn_scales[64u * col + 16u * ((sb >> 4) ^ sw4) + (sb & 15u)];
       const uint32_t cb = (rb[S].sc >> (8u * k)) & 0xffu;
-      d[0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a_operand(aw), b_operand(rb[S].lo[k], rb[S].hi[k]), d[0],
-                                                              4, 0, 0, int(ca), 0, int(cb));
+      const v8i B = b_operand(rb[S].lo[k], rb[S].hi[k]);
+#pragma unroll
+      for (int tl = 0; tl < NT; ++tl) {
+        const uint32_t r = 32u * uint32_t(tl) + col;
+        const uint4 aw = *reinterpret_cast<const uint4 *>(src + 128u * r + 16u * (p ^ sw[tl]));
+        const uint32_t ca = dn_scales[64u * r + 16u * ((sb >> 4) ^ s4[tl]) + (sb & 15u)];
+        d[tl] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a_operand(aw), B, d[tl], 4, 0, 0, int(ca), 0,
+                                                                int(cb));
+      }
     }
     if (refill) load_bchunk(rb[S], ht, hts, c + kRing, tb, sbb);
     __builtin_amdgcn_sched_barrier(0);  // as in phase 1
@@ -682,14 +703,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
   chunk(Slot<1>{}, kChunks - 3, false);
   chunk(Slot<2>{}, kChunks - 2, false);
   chunk(Slot<3>{}, kChunks - 1, false);
-  mfma_settle<1>(d);
+  mfma_settle<NT>(d);
   if (col >= it.count) return;
-  float *dst = ws.down + size_t(it.first + col) * kHidden + rt * 32u;
 #pragma unroll
-  for (int q4 = 0; q4 < 4; ++q4) {
-    float4 o = make_float4(d[0][4 * q4], d[0][4 * q4 + 1], d[0][4 * q4 + 2], d[0][4 * q4 + 3]);
-    if constexpr (kOfficial) o = make_float4(bf16_round(o.x), bf16_round(o.y), bf16_round(o.z), bf16_round(o.w));
-    *reinterpret_cast<float4 *>(dst + 8u * q4 + 4u * h) = o;
+  for (int tl = 0; tl < NT; ++tl) {
+    float *dst = ws.down + size_t(it.first + col) * kHidden + rt * kDnRows + 32u * uint32_t(tl);
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      float4 o = make_float4(d[tl][4 * q4], d[tl][4 * q4 + 1], d[tl][4 * q4 + 2], d[tl][4 * q4 + 3]);
+      if constexpr (kOfficial) o = make_float4(bf16_round(o.x), bf16_round(o.y), bf16_round(o.z), bf16_round(o.w));
+      *reinterpret_cast<float4 *>(dst + 8u * q4 + 4u * h) = o;
+    }
   }
 }
 
@@ -746,11 +770,11 @@ hipError_t launch_prefill(hipStream_t s, const PrefillArgs &a, const PrefillWork
   if (a.official) {
     k_prefill_up<true><<<dim3(kInter / 32, max_items), 64, 0, s>>>(a, ws);
     k_requant_h128<<<max_items * kItemTokens * kHGroups128 * 8u / 256u, 256, 0, s>>>(ws);
-    k_prefill_down<true><<<dim3(kHidden / 32, max_items), 64, 0, s>>>(a, ws);
+    k_prefill_down<true><<<dim3(kHidden / kDnRows, max_items), 64, 0, s>>>(a, ws);
     k_prefill_combine<true><<<cb_blocks, 256, 0, s>>>(a, ws);
   } else {
     k_prefill_up<false><<<dim3(kInter / 32, max_items), 64, 0, s>>>(a, ws);
-    k_prefill_down<false><<<dim3(kHidden / 32, max_items), 64, 0, s>>>(a, ws);
+    k_prefill_down<false><<<dim3(kHidden / kDnRows, max_items), 64, 0, s>>>(a, ws);
     k_prefill_combine<false><<<cb_blocks, 256, 0, s>>>(a, ws);
   }
   return hipGetLastError();
