@@ -328,7 +328,8 @@ __device__ __forceinline__ uint32_t swz4(uint32_t r) { return (r + (r >> 2)) & 3
 constexpr uint32_t kUpSlotBytes = 2 * 32 * 128;  // w1 and w3 chunks
 // w2 rows per phase-2 wavefront: two 32-row MFMA tiles sharing each
 // activation operand (with one tile a wavefront read twice as many
-// activation bytes as weight bytes; measured 249 -> see the design notes)
+// activation bytes as weight bytes: 249 us for the down GEMM at 512 tokens
+// against 220 us; four tiles measured no faster)
 constexpr uint32_t kDnRows = 64;
 constexpr uint32_t kDnSlotBytes = kDnRows * 128;  // w2 chunk
 __shared__ __attribute__((aligned(16))) uint8_t up_slot0[kUpSlotBytes];
