@@ -409,6 +409,14 @@ extern "C" int s14_expert_chain(s14_ctx *ctx, void *stream, const uint8_t *page,
   t.npairs[0] = 1;
   hipStream_t st = pick(ctx, stream);
   stage_begin(ctx);
+  if (mode == S14_MODE_EXACT) {
+    // one pair: lane quads, so that the rows spread over the SIMDs
+    const hipError_t e = s14::launch_chain_quad(st, ctx->ws, page, ctx->mx, x, route_w, y,
+                                                stage_events(ctx, kStagePhase1), stage_events(ctx, kStagePhase2));
+    if (e != hipSuccess) return hip_fail(e, "chain launch");
+    ctx->stage_valid = ctx->stage_timing;
+    return S14_OK;
+  }
   return run_layer(ctx, st, &t, 1, 1, x, y, mode);
 }
 

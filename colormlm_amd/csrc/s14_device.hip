@@ -1120,6 +1120,59 @@ __global__ __launch_bounds__(64 * kP2FastWaves) void k_phase2_fast(const PairTab
   if (wave == 0) phase2_accumulate<kP2FastRows>(si, part, t, row0, Y);
 }
 
+// The single-expert chain in EXACT order with lane quads (config 0: one
+// pair, so lane pairs would leave seven of eight SIMDs idle).  Phase 1:
+// workgroups of 4 wavefronts, each wavefront 8 rows of w1 (lanes 0-31) and
+// the same 8 rows of w3 (lanes 32-63), x staged once per workgroup, h =
+// swiglu(g, u) into ws.h (pair 0).  Phase 2: 16 rows of w2 per wavefront,
+// h staged per workgroup, y = w * down (s14_vulkan_numeric.rs:1300).
+constexpr int kChainQNB = 8;             // batches of 4 groups in flight per lane
+constexpr uint32_t kChainP1Rows = 32;    // rows of h per workgroup
+constexpr uint32_t kChainP2Rows = 64;    // rows of y per workgroup
+__global__ __launch_bounds__(256) void k_chain_phase1_quad(const uint8_t *page, const float *__restrict__ X,
+                                                           Workspace ws, PageOffsets mx) {
+  __shared__ float xs[kHidden];
+  __shared__ double exptab[32];
+  __shared__ int red[8];
+  exp_table_fill(exptab);  // published by the barrier in the x copy
+  const uint32_t lane = threadIdx.x & 63, q = lane & 3u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool upper = lane >= 32;
+  const uint32_t row = blockIdx.x * kChainP1Rows + wave * 8u + ((lane & 31u) >> 2);
+  const Rsrc r = make_rsrc(page, uint32_t(S14_EXPERT_PAGE_BYTES));
+  const uint32_t woff = uint32_t(upper ? mx.w3 : mx.w1) + row * (kHidden / 2) + 4u * q;
+  const uint32_t soff = uint32_t(upper ? mx.s3 : mx.s1) + row * (kHidden / 32);
+  MxQBatch b[kChainQNB];
+#pragma unroll
+  for (int j = 0; j < kChainQNB; ++j) mxq_load(b[j], r, woff, soff, 4 * j);  // in flight during the x copy
+  QuadCodes<kHidden / 32> qc;
+  load_quad_codes<kHidden / 32>(qc, r, soff);
+  const CodeWindow win = stage_x_block<kHidden, 256>(xs, X, red);
+  const bool scaled = quad_codes_in<kHidden / 32>(qc, win);
+  const float acc = mx_row_quad<kChainQNB, kHidden / 32>(b, r, woff, soff, xs + 8u * q, scaled);
+  const float other = __shfl_xor(acc, 32);
+  if (!upper && q == 0) ws.h[row] = swiglu_exact(acc, other, exptab);
+}
+
+__global__ __launch_bounds__(256) void k_chain_phase2_quad(const uint8_t *page, Workspace ws, float weight,
+                                                           float *__restrict__ Y, PageOffsets mx) {
+  __shared__ float hs[kInter];
+  __shared__ int red[8];
+  const uint32_t lane = threadIdx.x & 63, q = lane & 3u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t row = blockIdx.x * kChainP2Rows + wave * 16u + (lane >> 2);
+  const Rsrc r = make_rsrc(page, uint32_t(S14_EXPERT_PAGE_BYTES));
+  const uint32_t woff = uint32_t(mx.w2) + row * (kInter / 2) + 4u * q;
+  const uint32_t soff = uint32_t(mx.s2) + row * (kInter / 32);
+  MxQBatch b[kChainQNB];
+#pragma unroll
+  for (int j = 0; j < kChainQNB; ++j) mxq_load(b[j], r, woff, soff, 4 * j);  // in flight during the h copy
+  QuadCodes<kInter / 32> qc;
+  load_quad_codes<kInter / 32>(qc, r, soff);
+  const CodeWindow win = stage_x_block<kInter, 256>(hs, ws.h, red);
+  const bool scaled = quad_codes_in<kInter / 32>(qc, win);
+  const float acc = mx_row_quad<kChainQNB, kInter / 32>(b, r, woff, soff, hs + 8u * q, scaled);
+  if (q == 0) Y[row] = __fmul_rn(weight, acc);
+}
+
 // EXACT FP8 matvec with lane quads (k % 32 == 0, k <= kQuadMaxK): 4
 // wavefronts of 16 rows per workgroup, x staged once per workgroup as f32.
 constexpr uint32_t kQuadMaxK = 8192;
@@ -1321,6 +1374,15 @@ void phase2_tier(hipStream_t s, const Workspace &ws, uint32_t tokens, const Page
                           0, s, ev.start, ev.stop, 0, tab, h, ws.hwin, y, mx, fp8);
 }
 }  // namespace
+
+hipError_t launch_chain_quad(hipStream_t s, const Workspace &ws, const uint8_t *page, const PageOffsets &mx,
+                             const float *x, float weight, float *y, KernelEvents ev1, KernelEvents ev2) {
+  hipExtLaunchKernelGGL(k_chain_phase1_quad, dim3(kInter / kChainP1Rows), dim3(256), 0, s, ev1.start, ev1.stop, 0,
+                        page, x, ws, mx);
+  hipExtLaunchKernelGGL(k_chain_phase2_quad, dim3(kHidden / kChainP2Rows), dim3(256), 0, s, ev2.start, ev2.stop, 0,
+                        page, ws, weight, y, mx);
+  return hipGetLastError();
+}
 
 hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *host_plan, uint32_t n_pairs,
                          uint32_t tokens, const PageOffsets &mx, const PageOffsets &fp8, const float *x, int mode,

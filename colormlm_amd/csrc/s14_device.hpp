@@ -234,6 +234,10 @@ hipError_t launch_block_phase1(hipStream_t s, const Workspace &ws, uint32_t n_pa
                                const PageOffsets &fp8, const float *x, KernelEvents ev = {});
 hipError_t launch_block_phase2(hipStream_t s, const Workspace &ws, uint32_t tokens, const PageOffsets &mx,
                                const PageOffsets &fp8, float *y, KernelEvents ev = {});
+// The single-expert chain (one MXFP4 page, y = weight * down) in EXACT
+// order with lane quads: its phase 1 and phase 2.
+hipError_t launch_chain_quad(hipStream_t s, const Workspace &ws, const uint8_t *page, const PageOffsets &mx,
+                             const float *x, float weight, float *y, KernelEvents ev1 = {}, KernelEvents ev2 = {});
 // w2 of every pair and the per-token accumulation into y [tokens][hidden].
 hipError_t launch_phase2(hipStream_t s, const Workspace &ws, uint32_t tokens,
                          const PageOffsets &mx, const PageOffsets &fp8, float *y, int mode,

@@ -614,18 +614,131 @@ __device__ __forceinline__ float fp8_row_quad(Rsrc w, Rsrc sc, uint32_t woff, ui
   float acc = 0.0f;
   for (int g0 = 0; g0 < G; g0 += 4 * NB) {
     const bool refill = g0 + 4 * NB < G;  // uniform
+    // software-pipelined as mx_row_quad: group n+1's products ahead of group
+    // n's chain
+    float pc[8], pn[8];
+    fp8_products8(pc, b[0].w[0], b[0].s, xq + 32 * g0);
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float p[8];
-        fp8_products8(p, b[j].w[i], b[j].s, xq + 32 * (g0 + 4 * j + i));
-        acc = quad_chain8(acc, p);
+    for (int n = 0; n < 4 * NB; ++n) {
+      const int j = n / 4, i = n % 4;
+      if (n + 1 < 4 * NB) {
+        const int jn = (n + 1) / 4, in = (n + 1) % 4;
+        fp8_products8(pn, b[jn].w[in], b[jn].s, xq + 32 * (g0 + n + 1));
       }
-      if (refill) fp8q_load(b[j], w, sc, woff, soff, scale_f32, g0 + 4 * NB + 4 * j);
+      acc = quad_chain8(acc, pc);
+      if (i == 3 && refill) fp8q_load(b[j], w, sc, woff, soff, scale_f32, g0 + 4 * NB + 4 * j);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) pc[k] = pn[k];
     }
   }
   return from_quad_last(acc);
+}
+
+// MXFP4 rows by lane quads (the single-expert chain, whose 4,096 + 4,096
+// phase-1 rows and 4,096 phase-2 rows leave most SIMDs idle with lane
+// pairs): lane q of each quad holds the 4 code bytes of k 8q .. 8q+7 of
+// every 32-k group (woff includes 4 q) and the group's scale code; xq = x +
+// 8 q.  Products as the pair engine's: scaled (one converter step per two
+// codes, then x times the decoded value) when every code of the
+// wavefront's rows is inside the window, else literal ((x * e2m1) * s).
+struct MxQBatch {
+  uint32_t w[4];  // groups g0 .. g0+3
+  uint32_t c;     // their scale codes, one byte each
+};
+__device__ __forceinline__ void mxq_load(MxQBatch &b, Rsrc r, uint32_t woff, uint32_t soff, int g0) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b.w[i] = ld4(r, woff + 16u * uint32_t(g0 + i));
+  b.c = ld4(r, soff + uint32_t(g0));
+}
+template <bool kScaled>
+__device__ __forceinline__ void mx_products8(float (&p)[8], uint32_t w, uint32_t c, const float *__restrict__ x) {
+  const float4 xa = *reinterpret_cast<const float4 *>(x), xb = *reinterpret_cast<const float4 *>(x + 4);
+  const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+  if constexpr (kScaled) {
+    const float sc = __uint_as_float(c << 23);
+    const v2f q[4] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 0),
+                      __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 1),
+                      __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 2),
+                      __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 3)};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      p[2 * s] = __fmul_rn(xv[2 * s], q[s].x);
+      p[2 * s + 1] = __fmul_rn(xv[2 * s + 1], q[s].y);
+    }
+  } else {
+    const float s = ue8m0_f32(c);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) p[j] = __fmul_rn(__fmul_rn(xv[j], e2m1_f32((w >> (4 * j)) & 15u)), s);
+  }
+}
+// A quad lane's share of its row's G scale codes (lane q: bytes G/4 q ..
+// G/4 q + G/4 - 1), loaded ahead so that one check decides the decode of
+// the whole row; quad_codes_in is true (in every lane) when every code of
+// every row of the wavefront lies in the window.
+template <int G>
+struct QuadCodes {
+  static_assert(G == 128 || G == 64, "a quad lane holds 32 or 16 codes");
+  uint4 v[G / 64];
+};
+template <int G>
+__device__ __forceinline__ void load_quad_codes(QuadCodes<G> &qc, Rsrc r, uint32_t soff_row) {
+  const uint32_t q = threadIdx.x & 3u;
+#pragma unroll
+  for (int i = 0; i < G / 64; ++i) qc.v[i] = ld16(r, soff_row + uint32_t(G / 4) * q + 16u * uint32_t(i));
+}
+template <int G>
+__device__ __forceinline__ bool quad_codes_in(const QuadCodes<G> &qc, CodeWindow win) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  u16x2 mn = {255, 255}, mx = {0, 0};
+#pragma unroll
+  for (int i = 0; i < G / 64; ++i) {
+    const uint32_t w[4] = {qc.v[i].x, qc.v[i].y, qc.v[i].z, qc.v[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u16x2 lo = __builtin_bit_cast(u16x2, w[j] & 0x00ff00ffu);
+      const u16x2 hi = __builtin_bit_cast(u16x2, (w[j] >> 8) & 0x00ff00ffu);
+      mn = __builtin_elementwise_min(mn, __builtin_elementwise_min(lo, hi));
+      mx = __builtin_elementwise_max(mx, __builtin_elementwise_max(lo, hi));
+    }
+  }
+  const bool ok = int(min(mn.x, mn.y)) >= win.cmin && int(max(mx.x, mx.y)) <= win.cmax;
+  return __builtin_amdgcn_ballot_w64(!ok) == 0;
+}
+// Dot of one MXFP4 row of G groups (G % (4 NB) == 0) with x in LDS, NB
+// batches of 4 groups in flight; the caller issued batches 0 .. NB-1.
+// Result in every lane of the quad.
+template <int NB, int G, bool kScaled>
+__device__ __forceinline__ float mx_row_quad_as(MxQBatch (&b)[NB], Rsrc r, uint32_t woff, uint32_t soff,
+                                                const float *__restrict__ xq) {
+  static_assert(G % (4 * NB) == 0, "whole rounds of batches");
+  float acc = 0.0f;
+#pragma unroll 1
+  for (int g0 = 0; g0 < G; g0 += 4 * NB) {
+    const bool refill = g0 + 4 * NB < G;  // uniform
+    // software-pipelined: group n+1's x reads and products are issued ahead
+    // of group n's chain, so they fill the gaps between its dependent adds
+    float pc[8], pn[8];
+    mx_products8<kScaled>(pc, b[0].w[0], b[0].c & 255u, xq + 32 * g0);
+#pragma unroll
+    for (int n = 0; n < 4 * NB; ++n) {
+      const int j = n / 4, i = n % 4;
+      if (n + 1 < 4 * NB) {
+        const int jn = (n + 1) / 4, in = (n + 1) % 4;
+        mx_products8<kScaled>(pn, b[jn].w[in], (b[jn].c >> (8 * in)) & 255u, xq + 32 * (g0 + n + 1));
+      }
+      acc = quad_chain8(acc, pc);
+      if (i == 3 && refill) mxq_load(b[j], r, woff, soff, g0 + 4 * NB + 4 * j);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) pc[k] = pn[k];
+    }
+  }
+  return from_quad_last(acc);
+}
+// The decode chosen once per wavefront (`scaled` uniform).
+template <int NB, int G>
+__device__ __forceinline__ float mx_row_quad(MxQBatch (&b)[NB], Rsrc r, uint32_t woff, uint32_t soff,
+                                             const float *__restrict__ xq, bool scaled) {
+  return scaled ? mx_row_quad_as<NB, G, true>(b, r, woff, soff, xq) : mx_row_quad_as<NB, G, false>(b, r, woff, soff, xq);
 }
 
 // ---------------------------------------------------------------------------

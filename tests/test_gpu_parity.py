@@ -875,6 +875,11 @@ def test_prefill_official(ctx, oracle, bank, prefill_router, tokens):
     say(f"  official end to end worst {worst}")
     y2, _, _ = _run_prefill_official(ctx, bank, prefill_router, xs)
     assert_bit_exact(y2, y, "official repeat run")
+    # tokens are independent: a subset's rows equal their rows in the full run
+    pick = sorted({0, tokens // 2, tokens - 1})
+    y3, ids3, _ = _run_prefill_official(ctx, bank, prefill_router, np.ascontiguousarray(xs[pick]))
+    assert np.array_equal(ids3, ids[pick])
+    assert_bit_exact(y3, y[pick], f"official rows {pick} vs a {len(pick)}-token run")
 
 
 @pytest.mark.parametrize("tokens", [1, 5, 1024])
