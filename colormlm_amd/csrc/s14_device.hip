@@ -470,7 +470,7 @@ __global__ __launch_bounds__(256) void k_router_scores(RouterArgs r, uint32_t to
   for (uint32_t i = 0; i < kRtE; ++i)
 #pragma unroll
     for (uint32_t j = 0; j < kRtT; ++j) acc[i][j] = 0.0f;
-#pragma unroll 2
+#pragma unroll 1
   for (uint32_t c = 0; c < kHidden / 256; ++c) {
     float4 wv[kRtE], xv[kRtT];
 #pragma unroll
@@ -482,10 +482,10 @@ __global__ __launch_bounds__(256) void k_router_scores(RouterArgs r, uint32_t to
 #pragma unroll
       for (uint32_t j = 0; j < kRtT; ++j) {
         float a = acc[i][j];
-        a = __fadd_rn(a, __fmul_rn(wv[i].x, xv[j].x));
-        a = __fadd_rn(a, __fmul_rn(wv[i].y, xv[j].y));
-        a = __fadd_rn(a, __fmul_rn(wv[i].z, xv[j].z));
-        a = __fadd_rn(a, __fmul_rn(wv[i].w, xv[j].w));
+        a = __fmaf_rn(wv[i].x, xv[j].x, a);
+        a = __fmaf_rn(wv[i].y, xv[j].y, a);
+        a = __fmaf_rn(wv[i].z, xv[j].z, a);
+        a = __fmaf_rn(wv[i].w, xv[j].w, a);
         acc[i][j] = a;
       }
   }
@@ -496,9 +496,7 @@ __global__ __launch_bounds__(256) void k_router_scores(RouterArgs r, uint32_t to
   for (uint32_t i = 0; i < kRtE; ++i)
 #pragma unroll
     for (uint32_t j = 0; j < kRtT; ++j) {
-      float a = acc[i][j];
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) a = __fadd_rn(a, __shfl_xor(a, m));
+      const float a = xor_butterfly_sum(acc[i][j]);
       mine = lane == i * kRtT + j ? a : mine;
     }
   const uint32_t e = e0 + lane / kRtT, t = t0 + lane % kRtT;

@@ -188,6 +188,37 @@ __device__ __forceinline__ float from_even(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xA0, 0xf, 0xf, true));
 }
 
+// The xor butterfly sum of a wavefront's 64 values: for m = 32, 16, 8, 4, 2,
+// 1 every lane adds the value of lane ^ m (a + a[lane ^ m], so lanes l and
+// l ^ m hold the same sum after each step and every lane ends with the
+// total).  The exchanges stay in the VALU: gfx950's permlane swaps for 32
+// and 16 (the swap returns {first operand with its upper rows replaced,
+// second operand with its lower rows replaced}; each lane takes the half that
+// holds its partner), DPP row_ror:8 for 8, two bank-masked row shifts for 4,
+// quad_perm for 2 and 1.  `__shfl_xor` would issue an LDS permute per step.
+__device__ __forceinline__ float xor_butterfly_sum(float a) {
+  const uint32_t lane = threadIdx.x & 63;
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    a = __fadd_rn(a, __uint_as_float((lane & 32u) ? r[0] : r[1]));
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    a = __fadd_rn(a, __uint_as_float((lane & 16u) ? r[0] : r[1]));
+  }
+  a = __fadd_rn(a, dpp_f<0x128>(0.0f, a));  // row_ror:8: lane ^ 8 within each 16-lane row
+  {
+    // row_shl:4 into banks 0 and 2 (lanes 0-3, 8-11 of a row), row_shr:4
+    // into banks 1 and 3
+    int t = __builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x104, 0xf, 0x5, false);
+    t = __builtin_amdgcn_update_dpp(t, __float_as_int(a), 0x114, 0xf, 0xa, false);
+    a = __fadd_rn(a, __int_as_float(t));
+  }
+  a = __fadd_rn(a, dpp_f<0x4e>(0.0f, a));  // quad_perm [2,3,0,1]: lane ^ 2
+  a = __fadd_rn(a, dpp_f<0xb1>(0.0f, a));  // quad_perm [1,0,3,2]: lane ^ 1
+  return a;
+}
+
 // Full-wavefront sum (order-changing; FAST mode only), returned to every lane.
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += dpp_f<0xb1>(0.0f, v);        // quad_perm [1,0,3,2]

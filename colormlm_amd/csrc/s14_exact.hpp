@@ -805,8 +805,10 @@ constexpr int kPF = 8;
 
 // Router: one wavefront per (expert, token).  Logit order (fixed here; the
 // reference uses torch F.linear, executor.py:641, whose order is the
-// BLAS's): lane l sums k = 256c + 4l + j (c ascending, j = 0..3), then the
-// xor butterfly over lanes.  Score: sigmoid (north-star config) or
+// BLAS's): lane l sums k = 256c + 4l + j (c ascending, j = 0..3), each
+// step one fused multiply-add acc = fma(w_k, x_k, acc) (one rounding per
+// term, as a BLAS dot kernel's FMA), then the xor butterfly over lanes
+// (plain adds).  Score: sigmoid (north-star config) or
 // sqrt(softplus) with torch's threshold 20 (executor.py:642), exp and log1p
 // bit-identical to the C library's (s14_expf.h, s14_log1pf.h) as the
 // oracle's.  Score and biased score of expert e from its logit.
@@ -841,14 +843,12 @@ __device__ __forceinline__ float2 router_score(const RouterArgs &r, const float 
   float acc = 0.0f;
 #pragma unroll
   for (uint32_t c = 0; c < K / 256; ++c) {
-    acc = __fadd_rn(acc, __fmul_rn(wv[c].x, xv[c].x));
-    acc = __fadd_rn(acc, __fmul_rn(wv[c].y, xv[c].y));
-    acc = __fadd_rn(acc, __fmul_rn(wv[c].z, xv[c].z));
-    acc = __fadd_rn(acc, __fmul_rn(wv[c].w, xv[c].w));
+    acc = __fmaf_rn(wv[c].x, xv[c].x, acc);
+    acc = __fmaf_rn(wv[c].y, xv[c].y, acc);
+    acc = __fmaf_rn(wv[c].z, xv[c].z, acc);
+    acc = __fmaf_rn(wv[c].w, xv[c].w, acc);
   }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, m));
-  return router_finish(r, acc, e);
+  return router_finish(r, xor_butterfly_sum(acc), e);
 }
 
 }  // namespace

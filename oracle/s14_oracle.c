@@ -272,7 +272,7 @@ void s14o_router_logits(uint32_t n_experts, uint32_t k, const float *wr,
       for (size_t c = 0; c < k / 256; ++c) {
         for (int j = 0; j < 4; ++j) {
           size_t kk = c * 256 + (size_t)l * 4 + (size_t)j;
-          acc += row[kk] * x[kk];
+          acc = fmaf(row[kk], x[kk], acc);
         }
       }
       p[l] = acc;

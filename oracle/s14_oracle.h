@@ -129,8 +129,10 @@ enum { S14O_SCORE_SIGMOID = 0, S14O_SCORE_SQRT_SOFTPLUS = 1 };
 /* Router logits z[e] = W_r[e,:] . x.  The reference computes this with
  * torch F.linear (executor.py:641), whose summation order is the BLAS's and
  * unspecified; this oracle fixes it: 64 lane partials, lane l summing
- * k = 256c + 4l + j (c ascending, j = 0..3) sequentially, then a xor
- * butterfly p[l] = p[l] + p[l ^ m] for m = 32,16,8,4,2,1.  Requires k%256==0. */
+ * k = 256c + 4l + j (c ascending, j = 0..3) sequentially, each term one
+ * fused multiply-add acc = fmaf(w_k, x_k, acc) (one rounding per term, as a
+ * BLAS dot kernel's FMA), then a xor butterfly of plain adds
+ * p[l] = p[l] + p[l ^ m] for m = 32,16,8,4,2,1.  Requires k%256==0. */
 void s14o_router_logits(uint32_t n_experts, uint32_t k, const float *wr,
                         const float *x, float *z);
 /* scores, top-k of (score + bias) with ties to the lower index, weights =

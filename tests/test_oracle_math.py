@@ -176,6 +176,18 @@ def test_router_logit_order_closed_form(oracle):
     assert oracle.router_logits(wr, x)[0] == 2.0**24 + 2
 
 
+def test_router_logit_fused_terms_closed_form(oracle):
+    """Each term is one fused multiply-add.  Lane 0 sums k = 0 (w = -1,
+    x = 1) then k = 1 (w = x = 1 + 2^-12, exact product 1 + 2^-11 + 2^-24):
+    fma(w, x, -1) keeps 2^-11 + 2^-24, while a separate multiply rounds the
+    product to 1 + 2^-11 first (a tie, to even) and leaves 2^-11."""
+    wr = np.zeros((1, 256), dtype=np.float32)
+    x = np.zeros(256, dtype=np.float32)
+    wr[0, 0], x[0] = -1.0, 1.0
+    wr[0, 1] = x[1] = 1.0 + 2.0**-12
+    assert oracle.router_logits(wr, x)[0] == 2.0**-11 + 2.0**-24
+
+
 def test_router_vs_f64_topk_and_ties(oracle):
     wr, bias = synth.router(seed=7)
     x = synth.token(seed=7)
