@@ -323,7 +323,7 @@ __global__ __launch_bounds__(64 * kBWaves) void k_block_phase1(const PairTable *
     acc = row_dot_fp8<kHidden / 32>(r, uint32_t(upper ? f8.w3 : f8.w1) + row * kHidden,
                                     uint32_t(upper ? f8.s3 : f8.s1) + (row / 128) * (kHidden / 128), x);
   }
-  const float u = __shfl_xor(acc, 32);
+  const float u = lane_xor32(acc);
   int lo = 255, hi = 0;
   if (!upper) {
     // once per row: expf's table from constant memory

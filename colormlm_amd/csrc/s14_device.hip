@@ -838,7 +838,7 @@ __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable p
     if constexpr (kOfficial) requant128_block<64 * kP1ExactWaves>(xs, kHidden, red);
     acc = fp8_row_pair(0.0f, src, woff, soff, 0, kHidden / 32, xs + 16 * h);
   }
-  const float other = __shfl_xor(acc, 32);
+  const float other = lane_xor32(acc);
   const bool writer = !upper && h == 0;
   int lo = 255, hi = 0;
   if (writer) {
@@ -1147,7 +1147,7 @@ __global__ __launch_bounds__(256) void k_chain_phase1_quad(const uint8_t *page, 
   const CodeWindow win = stage_x_block<kHidden, 256>(xs, X, red);
   const bool scaled = quad_codes_in<kHidden / 32>(qc, win);
   const float acc = mx_row_quad<kChainQNB, kHidden / 32>(b, r, woff, soff, xs + 8u * q, scaled);
-  const float other = __shfl_xor(acc, 32);
+  const float other = lane_xor32(acc);
   if (!upper && q == 0) ws.h[row] = swiglu_exact(acc, other, exptab);
 }
 

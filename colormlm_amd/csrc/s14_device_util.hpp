@@ -7,6 +7,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <climits>
+
 #include "s14_device.hpp"
 #include "s14_e4m3.h"
 #include "s14_expf.h"
@@ -155,17 +157,6 @@ __device__ __forceinline__ float swiglu_exact(float gate, float up, const double
 // wavefront reductions and lane movement
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ int wave_min_i(int v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = min(v, __shfl_xor(v, m));
-  return v;
-}
-__device__ __forceinline__ int wave_max_i(int v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m));
-  return v;
-}
-
 // DPP row operations.  dpp_f/dpp_i read the source lane given by CTRL; lanes
 // without a source (or in rows outside ROW_MASK) get `old`.
 template <int CTRL, int ROW_MASK = 0xf>
@@ -176,6 +167,36 @@ __device__ __forceinline__ float dpp_f(float old, float v) {
 template <int CTRL, int ROW_MASK = 0xf>
 __device__ __forceinline__ int dpp_i(int old, int v) {
   return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xf, false);
+}
+
+// Wavefront minimum / maximum of an int, returned to every lane: DPP row
+// steps (lanes without a DPP source contribute the identity), then lane 63.
+// No LDS permutes, so the dependent steps cost VALU latency only.
+__device__ __forceinline__ int wave_min_i(int v) {
+  v = min(v, dpp_i<0xb1>(INT_MAX, v));        // quad_perm [1,0,3,2]
+  v = min(v, dpp_i<0x4e>(INT_MAX, v));        // quad_perm [2,3,0,1]
+  v = min(v, dpp_i<0x114>(INT_MAX, v));       // row_shr:4
+  v = min(v, dpp_i<0x118>(INT_MAX, v));       // row_shr:8
+  v = min(v, dpp_i<0x142, 0xa>(INT_MAX, v));  // row_bcast:15
+  v = min(v, dpp_i<0x143, 0xc>(INT_MAX, v));  // row_bcast:31
+  return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+  v = max(v, dpp_i<0xb1>(INT_MIN, v));
+  v = max(v, dpp_i<0x4e>(INT_MIN, v));
+  v = max(v, dpp_i<0x114>(INT_MIN, v));
+  v = max(v, dpp_i<0x118>(INT_MIN, v));
+  v = max(v, dpp_i<0x142, 0xa>(INT_MIN, v));
+  v = max(v, dpp_i<0x143, 0xc>(INT_MIN, v));
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+// The value of lane ^ 32 (gfx950's permlane32 swap, a VALU op: the swap
+// returns {first operand with lanes 32-63 replaced by the second's lanes
+// 0-31, second operand with lanes 0-31 replaced by the first's lanes 32-63}).
+__device__ __forceinline__ float lane_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 32u) ? r[0] : r[1]);
 }
 
 // Value of the odd lane of each lane pair (quad_perm [1,1,3,3]); every lane
@@ -198,10 +219,7 @@ __device__ __forceinline__ float from_even(float v) {
 // quad_perm for 2 and 1.  `__shfl_xor` would issue an LDS permute per step.
 __device__ __forceinline__ float xor_butterfly_sum(float a) {
   const uint32_t lane = threadIdx.x & 63;
-  {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
-    a = __fadd_rn(a, __uint_as_float((lane & 32u) ? r[0] : r[1]));
-  }
+  a = __fadd_rn(a, lane_xor32(a));
   {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
     a = __fadd_rn(a, __uint_as_float((lane & 16u) ? r[0] : r[1]));
