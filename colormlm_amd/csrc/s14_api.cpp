@@ -28,6 +28,7 @@ struct s14_ctx {
   int device = 0;
   hipStream_t compute = nullptr;
   hipStream_t copy = nullptr;
+  s14::BlockFork fork{};  // side stream and events of EXACT blocks
   void *ws_base = nullptr;
   void *prefill_base = nullptr;  // prefill workspace, made on the first prefill call
   void *lin_base = nullptr;      // fp8_linear FAST split-K workspace, made on the first FAST call
@@ -116,6 +117,9 @@ extern "C" int s14_ctx_create(int device, s14_ctx **out) {
   ctx->device = device;
   hipError_t e = hipStreamCreateWithFlags(&ctx->compute, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->copy, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->fork.side, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork.fork, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork.join, hipEventDisableTiming);
   if (e != hipSuccess) {
     s14_ctx_destroy(ctx);
     return hip_fail(e, "hipStreamCreate");
@@ -150,11 +154,15 @@ extern "C" void s14_ctx_destroy(s14_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   if (ctx->compute) (void)hipStreamSynchronize(ctx->compute);
   if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
+  if (ctx->fork.side) (void)hipStreamSynchronize(ctx->fork.side);
   if (ctx->ws_base) (void)hipFree(ctx->ws_base);
   if (ctx->prefill_base) (void)hipFree(ctx->prefill_base);
   if (ctx->lin_base) (void)hipFree(ctx->lin_base);
   if (ctx->compute) (void)hipStreamDestroy(ctx->compute);
   if (ctx->copy) (void)hipStreamDestroy(ctx->copy);
+  if (ctx->fork.side) (void)hipStreamDestroy(ctx->fork.side);
+  if (ctx->fork.fork) (void)hipEventDestroy(ctx->fork.fork);
+  if (ctx->fork.join) (void)hipEventDestroy(ctx->fork.join);
   for (auto ev : ctx->stage_ev)
     if (ev) (void)hipEventDestroy(ev);
   delete ctx;
@@ -470,7 +478,7 @@ int block_route_validate(uint32_t tokens, const s14_router *router, const uint64
 int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, const s14_router *router,
                        const uint64_t *expert_pages_dev, const uint8_t *shared_page, int shared_format,
                        const float *x, float *y, uint16_t *ids_out, float *weights_out, int mode,
-                       const KernelEvents *ev) {
+                       const KernelEvents *ev, const BlockFork *fork) {
   s14_page_layout l;
   s14_page_layout_get(S14_PAGE_MXFP4, S14_HIDDEN, S14_INTER, &l);
   const PageOffsets mx = offsets_of(l);
@@ -493,11 +501,29 @@ int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, con
   hipError_t e = launch_route(st, ws, rs, x, ev ? ev[kStageRoute] : KernelEvents{});
   if (e != hipSuccess) return hip_fail(e, "router launch");
   if (tokens > 1 && mode == S14_MODE_EXACT) {
-    // blocks: one row per lane (enough (token, expert) chains to fill the GPU)
-    e = launch_block_phase1(st, ws, n_pairs, mx, f8, x, ev ? ev[kStagePhase1] : KernelEvents{});
+    // blocks: one row per lane (enough (token, expert) chains to fill the
+    // GPU).  With a side stream the pairs run as two halves, one per stream,
+    // so that the SIMDs one half's phase-1 tail leaves idle (3.5 equal
+    // wavefronts per SIMD, two resident at a time) take the other half's
+    // work: K=8 182.9 -> 170.7 us per block (an even split measured best; three
+    // or four streams were slower).  Stage events time the first half.
+    const uint32_t na = fork ? n_pairs / 2 : n_pairs, nb = n_pairs - na;
+    if (fork) {
+      if ((e = hipEventRecord(fork->fork, st)) != hipSuccess) return hip_fail(e, "hipEventRecord(fork)");
+      if ((e = hipStreamWaitEvent(fork->side, fork->fork, 0)) != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
+    }
+    e = launch_block_phase1(st, ws, 0, na, mx, f8, x, ev ? ev[kStagePhase1] : KernelEvents{});
+    if (e == hipSuccess && nb) e = launch_block_phase1(fork->side, ws, na, nb, mx, f8, x);
     if (e != hipSuccess) return hip_fail(e, "phase 1 launch");
-    e = launch_block_phase2(st, ws, tokens, mx, f8, y, ev ? ev[kStagePhase2] : KernelEvents{});
+    e = launch_block_phase2(st, ws, 0, na, mx, f8, ev ? ev[kStagePhase2].start : nullptr);
+    if (e == hipSuccess && nb) e = launch_block_phase2(fork->side, ws, na, nb, mx, f8);
     if (e != hipSuccess) return hip_fail(e, "phase 2 launch");
+    if (fork) {
+      if ((e = hipEventRecord(fork->join, fork->side)) != hipSuccess) return hip_fail(e, "hipEventRecord(join)");
+      if ((e = hipStreamWaitEvent(st, fork->join, 0)) != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
+    }
+    e = launch_block_combine(st, ws, tokens, y, ev ? ev[kStagePhase2].stop : nullptr);
+    if (e != hipSuccess) return hip_fail(e, "combine launch");
     return S14_OK;
   }
   e = launch_phase1(st, ws, nullptr, n_pairs, tokens, mx, f8, x, mode, ev ? ev[kStagePhase1] : KernelEvents{});
@@ -522,7 +548,7 @@ extern "C" int s14_moe_block_route(s14_ctx *ctx, void *stream, uint32_t tokens, 
     for (int i = 0; i < kStages; ++i) ev[i] = {ctx->stage_ev[2 * i], ctx->stage_ev[2 * i + 1]};
   const int rc = s14::block_route_launch(pick(ctx, stream), ctx->ws, tokens, router, expert_pages_dev, shared_page,
                                          shared_format, x, y, ids_out, weights_out, mode,
-                                         ctx->stage_timing ? ev : nullptr);
+                                         ctx->stage_timing ? ev : nullptr, &ctx->fork);
   if (rc == S14_OK && ctx->stage_timing) {
     ctx->stage_mask = (1u << kStageRoute) | (1u << kStagePhase1) | (1u << kStagePhase2);
     ctx->stage_valid = true;

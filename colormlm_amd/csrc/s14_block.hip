@@ -35,6 +35,11 @@
 // page's tokens (adjacent in the expert-major pair order) for the same tile
 // group get workgroup ids 8 apart, so they run on the same XCD one after the
 // other and the later tokens' reads of the rows hit that XCD's L2.
+//
+// The launches take a range of pairs [p0, p0 + n): the host may run the
+// block's pairs as two halves on two streams, so that one half's phase 2
+// fills the idle SIMDs of the other half's phase-1 tail (each phase is 3.5
+// wavefronts per SIMD of equal length, two resident at a time).
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
@@ -283,19 +288,19 @@ __device__ __forceinline__ uint32_t b_page_bytes(uint32_t fmt) {
 // Workgroup id -> (tile group q of 16, pair p): XCD id % 8 = q % 8, and one
 // XCD's ids enumerate (q / 8, p), so the pairs of one page (adjacent in the
 // expert-major order) with the same tile group run on one XCD back to back.
-__device__ __forceinline__ void b_decode_id(uint32_t n_pairs, uint32_t &q, uint32_t &p) {
+__device__ __forceinline__ void b_decode_id(uint32_t n_pairs, uint32_t p0, uint32_t &q, uint32_t &p) {
   const uint32_t id = blockIdx.x, xcd = id % kXcds, j = id / kXcds;
   q = (j / n_pairs) * kXcds + xcd;
-  p = j % n_pairs;
+  p = p0 + j % n_pairs;
 }
 
 // Phase 1: workgroup -> (pair, 128 rows of h), wavefront -> 32 rows of w1
 // (lanes 0-31) and the same rows of w3 (lanes 32-63); h = swiglu(g, u).
 __global__ __launch_bounds__(64 * kBWaves) void k_block_phase1(const PairTable *__restrict__ tab, Workspace ws,
-                                                               const float *__restrict__ X, uint32_t n_pairs,
-                                                               PageOffsets mx, PageOffsets f8) {
+                                                               const float *__restrict__ X, uint32_t p0,
+                                                               uint32_t n_pairs, PageOffsets mx, PageOffsets f8) {
   uint32_t q, p;
-  b_decode_id(n_pairs, q, p);
+  b_decode_id(n_pairs, p0, q, p);
   const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint8_t *page = reinterpret_cast<const uint8_t *>(tab->page[p]);
   const uint32_t fmt = tab->fmt[p], t = tab->token[p];
@@ -339,9 +344,10 @@ __global__ __launch_bounds__(64 * kBWaves) void k_block_phase1(const PairTable *
 // Phase 2: workgroup -> (pair, 256 rows of w2), wavefront -> 64 rows, one
 // per lane; down[pair][row] without the route weight.
 __global__ __launch_bounds__(64 * kBWaves) void k_block_phase2(const PairTable *__restrict__ tab, Workspace ws,
-                                                               uint32_t n_pairs, PageOffsets mx, PageOffsets f8) {
+                                                               uint32_t p0, uint32_t n_pairs, PageOffsets mx,
+                                                               PageOffsets f8) {
   uint32_t q, p;
-  b_decode_id(n_pairs, q, p);
+  b_decode_id(n_pairs, p0, q, p);
   const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint8_t *page = reinterpret_cast<const uint8_t *>(tab->page[p]);
   const uint32_t fmt = tab->fmt[p];
@@ -400,19 +406,22 @@ __global__ __launch_bounds__(256) void k_block_combine(const PairTable *__restri
 
 }  // namespace
 
-hipError_t launch_block_phase1(hipStream_t s, const Workspace &ws, uint32_t n_pairs, const PageOffsets &mx,
-                               const PageOffsets &fp8, const float *x, KernelEvents ev) {
+hipError_t launch_block_phase1(hipStream_t s, const Workspace &ws, uint32_t p0, uint32_t n_pairs,
+                               const PageOffsets &mx, const PageOffsets &fp8, const float *x, KernelEvents ev) {
   hipExtLaunchKernelGGL(k_block_phase1, dim3(kBTileGroups * n_pairs), dim3(64 * kBWaves), 0, s, ev.start, ev.stop, 0,
-                        ws.table, ws, x, n_pairs, mx, fp8);
+                        ws.table, ws, x, p0, n_pairs, mx, fp8);
   return hipGetLastError();
 }
 
-hipError_t launch_block_phase2(hipStream_t s, const Workspace &ws, uint32_t tokens, const PageOffsets &mx,
-                               const PageOffsets &fp8, float *y, KernelEvents ev) {
-  const uint32_t n_pairs = tokens * kSlots;
+hipError_t launch_block_phase2(hipStream_t s, const Workspace &ws, uint32_t p0, uint32_t n_pairs,
+                               const PageOffsets &mx, const PageOffsets &fp8, hipEvent_t ev_start) {
   hipExtLaunchKernelGGL(k_block_phase2, dim3((kHidden / (kBRowsW * kBWaves)) * n_pairs), dim3(64 * kBWaves), 0, s,
-                        ev.start, nullptr, 0, ws.table, ws, n_pairs, mx, fp8);
-  hipExtLaunchKernelGGL(k_block_combine, dim3((tokens * (kHidden / 4) + 255) / 256), dim3(256), 0, s, nullptr, ev.stop,
+                        ev_start, nullptr, 0, ws.table, ws, p0, n_pairs, mx, fp8);
+  return hipGetLastError();
+}
+
+hipError_t launch_block_combine(hipStream_t s, const Workspace &ws, uint32_t tokens, float *y, hipEvent_t ev_stop) {
+  hipExtLaunchKernelGGL(k_block_combine, dim3((tokens * (kHidden / 4) + 255) / 256), dim3(256), 0, s, nullptr, ev_stop,
                         0, ws.table, ws, y, tokens);
   return hipGetLastError();
 }

@@ -228,12 +228,15 @@ hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *ho
                          const PageOffsets &fp8, const float *x, int mode, KernelEvents ev = {},
                          const RouteSpec *route = nullptr);
 // Blocks of 2..8 tokens in EXACT order, one row per lane (s14_block.hip):
-// phase 1 of every pair of the table the route kernel wrote, and phase 2 of
-// every token with its route-order accumulation into y [tokens][hidden].
-hipError_t launch_block_phase1(hipStream_t s, const Workspace &ws, uint32_t n_pairs, const PageOffsets &mx,
-                               const PageOffsets &fp8, const float *x, KernelEvents ev = {});
-hipError_t launch_block_phase2(hipStream_t s, const Workspace &ws, uint32_t tokens, const PageOffsets &mx,
-                               const PageOffsets &fp8, float *y, KernelEvents ev = {});
+// phase 1 and phase 2 of the pairs [p0, p0 + n_pairs) of the table the route
+// kernel wrote, then each token's route-order accumulation of its pairs'
+// outputs into y [tokens][hidden].
+hipError_t launch_block_phase1(hipStream_t s, const Workspace &ws, uint32_t p0, uint32_t n_pairs,
+                               const PageOffsets &mx, const PageOffsets &fp8, const float *x, KernelEvents ev = {});
+hipError_t launch_block_phase2(hipStream_t s, const Workspace &ws, uint32_t p0, uint32_t n_pairs,
+                               const PageOffsets &mx, const PageOffsets &fp8, hipEvent_t ev_start = nullptr);
+hipError_t launch_block_combine(hipStream_t s, const Workspace &ws, uint32_t tokens, float *y,
+                                hipEvent_t ev_stop = nullptr);
 // The single-expert chain (one MXFP4 page, y = weight * down) in EXACT
 // order with lane quads: its phase 1 and phase 2.
 hipError_t launch_chain_quad(hipStream_t s, const Workspace &ws, const uint8_t *page, const PageOffsets &mx,

@@ -16,12 +16,19 @@ namespace s14 {
 // Argument checks of the routed layer/block entry points (s14_api.cpp).
 int block_route_validate(uint32_t tokens, const s14_router *router, const uint64_t *expert_pages_dev,
                          const uint8_t *shared_page, int shared_format, const float *x, float *y, int mode);
+// A second stream and two events (all on the context's device) over which
+// an EXACT block runs half of its pairs beside the caller's stream.
+struct BlockFork {
+  hipStream_t side;
+  hipEvent_t fork, join;
+};
 // Route -> phase 1 -> phase 2 of a routed layer/block on `st` with workspace
-// `ws` (arguments already validated); ev: per-stage timing events or NULL.
+// `ws` (arguments already validated); ev: per-stage timing events or NULL;
+// fork: the side stream for EXACT blocks, or NULL to run everything on `st`.
 int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, const s14_router *router,
                        const uint64_t *expert_pages_dev, const uint8_t *shared_page, int shared_format,
                        const float *x, float *y, uint16_t *ids_out, float *weights_out, int mode,
-                       const KernelEvents *ev);
+                       const KernelEvents *ev, const BlockFork *fork);
 // Status bits the last launches left in ws (synchronises the device and
 // clears them): S14_OK, or the error they stand for.
 int read_launch_status(const Workspace &ws, int device);

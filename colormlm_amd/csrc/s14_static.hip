@@ -79,5 +79,5 @@ extern "C" int s14_moe_block_route_noalloc(void *stream, uint32_t tokens, const 
   void *base = nullptr;
   if (int rc = device_scratch(device, st, &base)) return rc;
   return s14::block_route_launch(st, s14::workspace_carve(base), tokens, router, expert_pages_dev, shared_page,
-                                 shared_format, x, y, ids_out, weights_out, mode, nullptr);
+                                 shared_format, x, y, ids_out, weights_out, mode, nullptr, nullptr);
 }

@@ -105,7 +105,9 @@ int s14_ctx_synchronize(s14_ctx *ctx);
  * for the last such launch and returns up to 3 stage durations in ms:
  * {route (router scores and top-k plan, one launch), phase 1 (w1, w3,
  * SwiGLU), phase 2 (w2, mix)}; a stage the last launch did not run (chain
- * and given-route layers have no route) reads 0. */
+ * and given-route layers have no route) reads 0.  An EXACT block's phase 1
+ * and phase 2 are those of the half of its pairs run on the caller's stream
+ * (the other half runs beside it); its phase 2 includes the combine. */
 int s14_ctx_enable_stage_timing(s14_ctx *ctx, int enable);
 int s14_ctx_stage_times(s14_ctx *ctx, float *ms, uint32_t cap, uint32_t *n_stages);
 
@@ -271,7 +273,11 @@ int s14_moe_layer_route(s14_ctx *ctx, void *stream, const s14_router *router,
 /* Speculative-verify block: T <= 8 tokens X[T, hidden] through the routed
  * layer, grouped expert-major so each distinct expert page is read once per
  * block.  ids_out [T, topk] u16 and weights_out [T, topk] f32 (device, may be
- * NULL); s14_last_block_distinct reports the distinct routed page count. */
+ * NULL); s14_last_block_distinct reports the distinct routed page count.
+ * An EXACT block of T >= 2 runs half of its pairs on the context's own side
+ * stream, joined back into `stream` (event wait) before the output is
+ * written: work queued on `stream` afterwards sees y complete, and a graph
+ * capture of `stream` takes the side branch in. */
 int s14_moe_block_route(s14_ctx *ctx, void *stream, uint32_t tokens, const s14_router *router,
                         const uint64_t *expert_pages_dev, const uint8_t *shared_page,
                         int shared_format, const float *x, float *y, uint16_t *ids_out,
