@@ -417,6 +417,37 @@ def test_moe_block_route_config3(ctx, oracle, bank, tokens):
         assert np.max(np.abs(fast[t] - got[t])) <= 1e-3
 
 
+def test_moe_block_graph_replays(ctx, bank):
+    """An EXACT block captured in a HIP graph (its side-stream half joins the
+    capture through the fork/join events), replayed three times with other
+    eager block launches and new inputs in between: every replay equals the
+    eager launch on the same inputs bit for bit."""
+    say("config 3 block T=8 captured in a HIP graph, three replays against eager launches")
+    router = s14.Router(bank["wr_d"], bank["bias_d"])
+    blocks = [synth.block_tokens(seed=40 + i, tokens=8) for i in range(3)]
+    x_static = dev(blocks[0])
+    y_graph = torch.empty((8, HIDDEN), dtype=torch.float32, device="cuda")
+    y_eager = torch.empty_like(y_graph)
+
+    def launch(x, y):
+        s14.moe_block_route(ctx, 8, router, bank["table"], bank["pages"][256], x, y, mode=s14.EXACT)
+
+    launch(x_static, y_graph)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch(x_static, y_graph)
+    for i, xs in enumerate(blocks):
+        x_static.copy_(dev(xs))
+        g.replay()
+        torch.cuda.synchronize()
+        got = host(y_graph)
+        launch(dev(xs), y_eager)  # eager work between the replays, on the same context
+        torch.cuda.synchronize()
+        assert_bit_exact(got, host(y_eager), f"graph replay {i}")
+    del g
+
+
 def test_moe_block_fp8_shared_and_edge_codes(ctx, oracle, bank):
     """Block launches (T=4) with the reference's FP8 shared page, so every
     phase-2 wavefront that serves a routed slot beside the shared one mixes
