@@ -384,21 +384,36 @@ __global__ __launch_bounds__(256) void k_block_combine(const PairTable *__restri
   const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
   if (gid >= tokens * (kHidden / 4)) return;
   const uint32_t t = gid / (kHidden / 4), r = 4u * (gid % (kHidden / 4));
+  // every slot record in one round trip (with the count), then every used
+  // slot's down row in a second, then the adds in route order
   const uint32_t np = tab->npairs[t];
+  uint32_t sp[kSlots], sh[kSlots];
+  float sw[kSlots];
+#pragma unroll
+  for (uint32_t j = 0; j < uint32_t(kSlots); ++j) {
+    sp[j] = tab->slot_pair[t][j];
+    sh[j] = tab->slot_shared[t][j];
+    sw[j] = tab->slot_weight[t][j];
+  }
+  float4 d[kSlots];
+#pragma unroll
+  for (uint32_t j = 0; j < uint32_t(kSlots); ++j)
+    d[j] = j < np ? *reinterpret_cast<const float4 *>(ws.down + size_t(sp[j]) * kHidden + r)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (uint32_t j = 0; j < np; ++j) {
-    const float4 d = *reinterpret_cast<const float4 *>(ws.down + size_t(tab->slot_pair[t][j]) * kHidden + r);
-    if (tab->slot_shared[t][j]) {
-      acc.x = __fadd_rn(acc.x, d.x);
-      acc.y = __fadd_rn(acc.y, d.y);
-      acc.z = __fadd_rn(acc.z, d.z);
-      acc.w = __fadd_rn(acc.w, d.w);
+#pragma unroll
+  for (uint32_t j = 0; j < uint32_t(kSlots); ++j) {
+    if (j >= np) break;
+    if (sh[j]) {
+      acc.x = __fadd_rn(acc.x, d[j].x);
+      acc.y = __fadd_rn(acc.y, d[j].y);
+      acc.z = __fadd_rn(acc.z, d[j].z);
+      acc.w = __fadd_rn(acc.w, d[j].w);
     } else {
-      const float w = tab->slot_weight[t][j];
-      acc.x = __fadd_rn(acc.x, __fmul_rn(w, d.x));
-      acc.y = __fadd_rn(acc.y, __fmul_rn(w, d.y));
-      acc.z = __fadd_rn(acc.z, __fmul_rn(w, d.z));
-      acc.w = __fadd_rn(acc.w, __fmul_rn(w, d.w));
+      acc.x = __fadd_rn(acc.x, __fmul_rn(sw[j], d[j].x));
+      acc.y = __fadd_rn(acc.y, __fmul_rn(sw[j], d[j].y));
+      acc.z = __fadd_rn(acc.z, __fmul_rn(sw[j], d[j].z));
+      acc.w = __fadd_rn(acc.w, __fmul_rn(sw[j], d[j].w));
     }
   }
   *reinterpret_cast<float4 *>(Y + size_t(t) * kHidden + r) = acc;

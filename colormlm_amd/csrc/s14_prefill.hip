@@ -727,21 +727,34 @@ __global__ __launch_bounds__(256) void k_prefill_combine(PrefillArgs a, PrefillW
   const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= a.tokens * (kHidden / 4)) return;
   const uint32_t t = gid / (kHidden / 4), r = 4u * (gid % (kHidden / 4));
+  // the token's pair indices and weights in one round trip, then every slot's
+  // down row in a second (all loads issued before the first add)
+  const uint32_t k = a.r.topk;  // <= kTopK; slot k is the shared expert
+  uint32_t pr[kSlots];
+  float wt[kTopK];
+#pragma unroll
+  for (uint32_t s = 0; s < uint32_t(kSlots); ++s) pr[s] = s <= k ? ws.token_pair[t * kSlots + s] : 0u;
+#pragma unroll
+  for (uint32_t s = 0; s < uint32_t(kTopK); ++s) wt[s] = s < k ? ws.weights[t * kTopK + s] : 0.0f;
+  float4 d[kSlots];
+#pragma unroll
+  for (uint32_t s = 0; s < uint32_t(kSlots); ++s)
+    d[s] = s <= k ? *reinterpret_cast<const float4 *>(ws.down + size_t(pr[s]) * kHidden + r)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (uint32_t s = 0; s <= a.r.topk; ++s) {
-    const uint32_t p = ws.token_pair[t * kSlots + s];
-    const float4 d = *reinterpret_cast<const float4 *>(ws.down + size_t(p) * kHidden + r);
-    if (s < a.r.topk && !kOfficial) {
-      const float w = ws.weights[t * kTopK + s];
-      acc.x = __fadd_rn(acc.x, __fmul_rn(w, d.x));
-      acc.y = __fadd_rn(acc.y, __fmul_rn(w, d.y));
-      acc.z = __fadd_rn(acc.z, __fmul_rn(w, d.z));
-      acc.w = __fadd_rn(acc.w, __fmul_rn(w, d.w));
+#pragma unroll
+  for (uint32_t s = 0; s < uint32_t(kSlots); ++s) {
+    if (s > k) break;
+    if (s < k && !kOfficial) {
+      acc.x = __fadd_rn(acc.x, __fmul_rn(wt[s], d[s].x));
+      acc.y = __fadd_rn(acc.y, __fmul_rn(wt[s], d[s].y));
+      acc.z = __fadd_rn(acc.z, __fmul_rn(wt[s], d[s].z));
+      acc.w = __fadd_rn(acc.w, __fmul_rn(wt[s], d[s].w));
     } else {
-      acc.x = __fadd_rn(acc.x, d.x);
-      acc.y = __fadd_rn(acc.y, d.y);
-      acc.z = __fadd_rn(acc.z, d.z);
-      acc.w = __fadd_rn(acc.w, d.w);
+      acc.x = __fadd_rn(acc.x, d[s].x);
+      acc.y = __fadd_rn(acc.y, d[s].y);
+      acc.z = __fadd_rn(acc.z, d[s].z);
+      acc.w = __fadd_rn(acc.w, d[s].w);
     }
   }
   if constexpr (kOfficial) acc = make_float4(bf16_round(acc.x), bf16_round(acc.y), bf16_round(acc.z), bf16_round(acc.w));
