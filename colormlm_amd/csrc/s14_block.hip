@@ -267,20 +267,6 @@ __device__ __forceinline__ float row_dot_fp8(Rsrc r, uint32_t woff, uint32_t sof
   return acc;
 }
 
-// Decode window of a vector of n floats in global memory (every lane of the
-// wavefront scanning a strided share).
-__device__ __forceinline__ CodeWindow vec_window(const float *v, int n) {
-  int lo = 255, hi = 0;
-  for (int i = int(threadIdx.x & 63) * 4; i < n; i += 256) {
-    const float4 q = *reinterpret_cast<const float4 *>(v + i);
-    exp_range_acc(q.x, lo, hi);
-    exp_range_acc(q.y, lo, hi);
-    exp_range_acc(q.z, lo, hi);
-    exp_range_acc(q.w, lo, hi);
-  }
-  return mx_window(wave_min_i(lo), wave_max_i(hi));
-}
-
 __device__ __forceinline__ uint32_t b_page_bytes(uint32_t fmt) {
   return fmt == S14_PAGE_MXFP4 ? uint32_t(S14_EXPERT_PAGE_BYTES) : uint32_t(S14_SHARED_EXPERT_PAGE_BYTES);
 }
@@ -322,7 +308,9 @@ __global__ __launch_bounds__(64 * kBWaves) void k_block_phase1(const PairTable *
       const uint32_t base = uint32_t(dr < 32 ? mx.w1 : mx.w3) + (row0 + (dr & 31u)) * (kHidden / 2);
       st.dma[j] = base + 16u * ((lane & 7u) ^ (dr & 7u));
     }
-    const CodeWindow win = vec_window(x, kHidden);
+    // x's decode window: the exponent range the route kernel recorded
+    const uint32_t xw = ws.xwin[t];
+    const CodeWindow win = mx_window(int(xw & 0xffffu), int(xw >> 16));
     acc = row_dot_stream<kHidden / 32 / kBChunk>(st, wave, win);
   } else {
     acc = row_dot_fp8<kHidden / 32>(r, uint32_t(upper ? f8.w3 : f8.w1) + row * kHidden,

@@ -631,7 +631,9 @@ __global__ __launch_bounds__(64 * kMaxTokens) void k_route(RouteSpec rs, Workspa
   const uint32_t t = blockIdx.y;
   const uint32_t e = blockIdx.x * W + wave;
   if (e < rs.r.n_experts) {
-    const float2 s = router_score(rs.r, X, t, e);
+    // blocks: expert 0's wavefront also records the token's x window for
+    // the block engine's phase 1
+    const float2 s = router_score(rs.r, X, t, e, (!kScoresOnly && e == 0) ? ws.xwin + t : nullptr);
     if (lane == 0) {
       // device-coherent stores (no cache writeback needed to publish them)
       __hip_atomic_store(&ws.scores[t * kMaxExperts + e], s.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -88,6 +88,7 @@ struct Workspace {
   float *biased;  // [kMaxTokens][kMaxExperts]
   uint32_t *route_count;  // [kRouteCounters]: groups, then per-group workgroups, of the running route launch that are done (one per 128-byte line)
   uint32_t *hwin;         // [kMaxPairs][kInter / kP1ExactRows]: exponent range (lo | hi << 16) of each exact phase-1 tile's h
+  uint32_t *xwin;         // [kMaxTokens]: exponent range (lo | hi << 16) of each token's x, written by the block route
   // kSyncLines lines of kRouteCounterStride words: the status word (kStatus*
   // bits) that launches leave for s14_launch_status.
   uint32_t *sync;
@@ -104,7 +105,7 @@ enum : uint32_t { kStatusNullPage = 1u, kStatusBadRoute = 2u };
 // Layout of the workspace in one device allocation (each region 256-byte
 // aligned): table | h | scores | biased | route counters | h windows.
 struct WorkspaceLayout {
-  size_t table, h, scores, biased, count, hwin, sync, down, bytes;
+  size_t table, h, scores, biased, count, hwin, xwin, sync, down, bytes;
 };
 constexpr size_t ws_align(size_t v) { return (v + 255) / 256 * 256; }
 constexpr WorkspaceLayout workspace_layout() {
@@ -122,6 +123,8 @@ constexpr WorkspaceLayout workspace_layout() {
   off = ws_align(off + sizeof(uint32_t) * kRouteCounters);
   l.hwin = off;
   off = ws_align(off + sizeof(uint32_t) * kMaxPairs * (kInter / kP1ExactRows));
+  l.xwin = off;
+  off = ws_align(off + sizeof(uint32_t) * kMaxTokens);
   l.sync = off;
   off = ws_align(off + sizeof(uint32_t) * kSyncLines * kRouteCounterStride);
   l.down = off;
@@ -143,6 +146,7 @@ inline Workspace workspace_carve(void *base) {
   ws.biased = reinterpret_cast<float *>(b + l.biased);
   ws.route_count = reinterpret_cast<uint32_t *>(b + l.count);
   ws.hwin = reinterpret_cast<uint32_t *>(b + l.hwin);
+  ws.xwin = reinterpret_cast<uint32_t *>(b + l.xwin);
   ws.sync = reinterpret_cast<uint32_t *>(b + l.sync);
   ws.down = reinterpret_cast<float *>(b + l.down);
   ws.bytes = l.bytes;

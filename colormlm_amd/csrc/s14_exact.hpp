@@ -827,9 +827,11 @@ __device__ __forceinline__ float2 router_finish(const RouterArgs &r, float logit
 }
 
 // Score of expert e for token t, computed by one whole wavefront; valid in
-// lane 0 (the biased score in .y).
+// lane 0 (the biased score in .y).  xwin != NULL (uniform): also store the
+// exponent range of the token's x there (lo | hi << 16, as stage_x_block
+// finds it), from the registers the logit already loaded.
 __device__ __forceinline__ float2 router_score(const RouterArgs &r, const float *__restrict__ X, uint32_t t,
-                                               uint32_t e) {
+                                               uint32_t e, uint32_t *xwin = nullptr) {
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t K = kHidden;
   const float *x = X + size_t(t) * K;
@@ -847,6 +849,19 @@ __device__ __forceinline__ float2 router_score(const RouterArgs &r, const float 
     acc = __fmaf_rn(wv[c].y, xv[c].y, acc);
     acc = __fmaf_rn(wv[c].z, xv[c].z, acc);
     acc = __fmaf_rn(wv[c].w, xv[c].w, acc);
+  }
+  if (xwin) {
+    int lo = 255, hi = 0;
+#pragma unroll
+    for (uint32_t c = 0; c < K / 256; ++c) {
+      exp_range_acc(xv[c].x, lo, hi);
+      exp_range_acc(xv[c].y, lo, hi);
+      exp_range_acc(xv[c].z, lo, hi);
+      exp_range_acc(xv[c].w, lo, hi);
+    }
+    lo = wave_min_i(lo);
+    hi = wave_max_i(hi);
+    if (lane == 0) *xwin = uint32_t(lo) | (uint32_t(hi) << 16);
   }
   return router_finish(r, xor_butterfly_sum(acc), e);
 }
