@@ -176,6 +176,7 @@ extern "C" int s14_ctx_synchronize(s14_ctx *ctx) {
   if (int rc = check_ctx(ctx)) return rc;
   S14_HIP(hipStreamSynchronize(ctx->compute), "hipStreamSynchronize(compute)");
   S14_HIP(hipStreamSynchronize(ctx->copy), "hipStreamSynchronize(copy)");
+  S14_HIP(hipStreamSynchronize(ctx->fork.side), "hipStreamSynchronize(side)");
   return S14_OK;
 }
 
