@@ -288,6 +288,9 @@ __global__ __launch_bounds__(64 * kBWaves) void k_block_phase1(const PairTable *
   uint32_t q, p;
   b_decode_id(n_pairs, p0, q, p);
   const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // every token's x window (lane i: token i % 8), loaded beside the table
+  // words rather than after them
+  const uint32_t xw_all = ws.xwin[lane & uint32_t(kMaxTokens - 1)];
   const uint8_t *page = reinterpret_cast<const uint8_t *>(tab->page[p]);
   const uint32_t fmt = tab->fmt[p], t = tab->token[p];
   const float *x = X + size_t(t) * kHidden;
@@ -309,7 +312,7 @@ __global__ __launch_bounds__(64 * kBWaves) void k_block_phase1(const PairTable *
       st.dma[j] = base + 16u * ((lane & 7u) ^ (dr & 7u));
     }
     // x's decode window: the exponent range the route kernel recorded
-    const uint32_t xw = ws.xwin[t];
+    const uint32_t xw = uint32_t(__builtin_amdgcn_readlane(int(xw_all), int(t)));
     const CodeWindow win = mx_window(int(xw & 0xffffu), int(xw >> 16));
     acc = row_dot_stream<kHidden / 32 / kBChunk>(st, wave, win);
   } else {
@@ -337,6 +340,8 @@ __global__ __launch_bounds__(64 * kBWaves) void k_block_phase2(const PairTable *
   uint32_t q, p;
   b_decode_id(n_pairs, p0, q, p);
   const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // h's window records (64 tiles of 32 rows), loaded beside the table words
+  const uint32_t wrec = ws.hwin[size_t(p) * kP1Tiles + lane];
   const uint8_t *page = reinterpret_cast<const uint8_t *>(tab->page[p]);
   const uint32_t fmt = tab->fmt[p];
   const float *h = ws.h + size_t(p) * kInter;
@@ -354,8 +359,6 @@ __global__ __launch_bounds__(64 * kBWaves) void k_block_phase2(const PairTable *
       const uint32_t dr = 8u * j + (lane >> 3);
       st.dma[j] = uint32_t(mx.w2) + (row0 + dr) * (kInter / 2) + 16u * ((lane & 7u) ^ (dr & 7u));
     }
-    // h's window from the phase-1 tile records (64 tiles of 32 rows)
-    const uint32_t wrec = ws.hwin[size_t(p) * kP1Tiles + lane];
     const CodeWindow win = mx_window(wave_min_i(int(wrec & 0xffffu)), wave_max_i(int(wrec >> 16)));
     acc = row_dot_stream<kInter / 32 / kBChunk>(st, wave, win);
   } else {
