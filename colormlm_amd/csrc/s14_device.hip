@@ -723,20 +723,15 @@ struct PairRef {
 };
 enum : int { kPairFromTable = 0, kPairFromHost = 1, kPairFromScores = 2 };
 
-// Pair p of a single-token layer from the scores (whole workgroup, uniform
-// result): the token's scores, biased scores and expert pages into LDS, one
-// wavefront selects the top-k exactly as the route kernel's last workgroup
-// does (plan_token) and takes the p-th choice in expert order, which is the
-// pair table's order (plan_publish sorts pairs by expert, then token).  The
-// shared pair (p = topk) needs no plan.  Workgroup (0,0) reports the route
-// and publishes the pair table for phase 2.
-__device__ __forceinline__ PairRef route_pair(const RouteSpec &rs, const Workspace &ws, uint32_t p) {
+// The single token's plan by a whole workgroup: its scores, biased scores
+// and expert pages into LDS, then one wavefront selects the top-k exactly
+// as the route kernel's last workgroup does (plan_token).  lead: that
+// wavefront also reports the route and publishes the pair table for phase 2.
+__device__ __forceinline__ const PlanLds &token_plan(const RouteSpec &rs, const Workspace &ws, bool lead) {
   __shared__ float rp_sc[kMaxExperts], rp_bs[kMaxExperts];
   __shared__ uint64_t rp_pages[kMaxExperts];
   __shared__ PlanLds rp_pl;
-  __shared__ PairRef rp_mine;
-  const uint32_t k = rs.r.topk, n = rs.r.n_experts;
-  if (p >= k) return PairRef{rs.shared_page, uint32_t(rs.shared_fmt), 0u, 1.0f};
+  const uint32_t n = rs.r.n_experts;
   for (uint32_t i = threadIdx.x; i < kMaxExperts; i += blockDim.x) {
     const bool in = i < n;
     rp_sc[i] = in ? ws.scores[i] : 0.0f;
@@ -745,9 +740,25 @@ __device__ __forceinline__ PairRef route_pair(const RouteSpec &rs, const Workspa
   }
   __syncthreads();
   if (threadIdx.x < 64) {
-    const bool lead = blockIdx.x == 0 && blockIdx.y == 0;
     plan_token(rs, 0, rp_bs, rp_sc, rp_pages, rp_pl, lead);
     if (lead) plan_publish(rs, ws.table, rp_pl);
+  }
+  return rp_pl;
+}
+
+// Pair p of a single-token layer from the scores (whole workgroup, uniform
+// result): the token's plan (token_plan) and its p-th choice in expert
+// order, which is the pair table's order (plan_publish sorts pairs by
+// expert, then token).  The shared pair (p = topk) needs no plan; its first
+// workgroup reports the route and publishes the pair table after its rows
+// (phase1_publish), where it has time to spare: the routed workgroups'
+// rows start only after their plan.
+__device__ __forceinline__ PairRef route_pair(const RouteSpec &rs, const Workspace &ws, uint32_t p) {
+  __shared__ PairRef rp_mine;
+  const uint32_t k = rs.r.topk;
+  if (p >= k) return PairRef{rs.shared_page, uint32_t(rs.shared_fmt), 0u, 1.0f};
+  const PlanLds &rp_pl = token_plan(rs, ws, false);
+  if (threadIdx.x < 64) {
     const uint32_t lane = threadIdx.x;
     if (lane < k) {
       const uint32_t id = rp_pl.ids[0][lane];
@@ -768,6 +779,16 @@ __device__ __forceinline__ PairRef route_pair(const RouteSpec &rs, const Workspa
                  uint32_t(__builtin_amdgcn_readfirstlane(int(rp_mine.fmt))),
                  uint32_t(__builtin_amdgcn_readfirstlane(int(rp_mine.token))),
                  __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(rp_mine.weight)))};
+}
+
+// End of a phase-1 workgroup that planned from the scores: the shared
+// pair's first workgroup reports the route and publishes the pair table
+// (uniform per workgroup: every thread reaches token_plan's barrier).
+template <int kSrc>
+__device__ __forceinline__ void phase1_publish(const RouteSpec &rs, const Workspace &ws) {
+  if constexpr (kSrc == kPairFromScores) {
+    if (blockIdx.y == rs.r.topk && blockIdx.x == 0) (void)token_plan(rs, ws, true);
+  }
 }
 
 template <int kSrc>
@@ -860,6 +881,7 @@ __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable p
   lo = wave_min_i(lo);
   hi = wave_max_i(hi);
   if (lane == 0) ws.hwin[size_t(p) * kP1Tiles + tile] = uint32_t(lo) | (uint32_t(hi) << 16);
+  phase1_publish<kSrc>(rs, ws);
 }
 
 // Phase 1 FAST: 4 wavefronts per workgroup; each streams p1_fast_rows_per_wave
@@ -932,6 +954,7 @@ __global__ __launch_bounds__(256) void k_phase1_fast(PairTable plan, RouteSpec r
     }
   }
   if (lane < R) ws.h[size_t(p) * kInter + row0 + lane] = swiglu_exact(gv, uv);
+  phase1_publish<kSrc>(rs, ws);
 }
 
 // What every phase-2 workgroup needs about its token, read in one round trip
