@@ -979,22 +979,32 @@ __device__ __forceinline__ void phase2_accumulate(const SlotInfo &si, const floa
                                                   uint32_t row0, float *__restrict__ Y) {
   const uint32_t lane = threadIdx.x & 63;
   const bool row_lane = lane < uint32_t(ROWS);
+  // every slot's value first (the LDS reads pipeline), then the adds in
+  // route order
+  float d[kSlots];
+#pragma unroll
+  for (uint32_t j = 0; j < uint32_t(kSlots); ++j) d[j] = (row_lane && j < si.np) ? part[j][lane] : 0.0f;
   float acc = 0.0f;
   if constexpr (kOfficial) {
     // official semantics: each slot's bf16 output already carries its route
     // weight; acc = 0; acc += out_j in route order, shared last; y =
     // bf16(acc) (executor.py:712-739)
-    for (uint32_t j = 0; j < si.np; ++j) acc = __fadd_rn(acc, row_lane ? part[j][lane] : 0.0f);
+#pragma unroll
+    for (uint32_t j = 0; j < uint32_t(kSlots); ++j) {
+      if (j >= si.np) break;
+      acc = __fadd_rn(acc, d[j]);
+    }
     acc = bf16_round(acc);
   } else if (si.chain) {
     const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(si.w), 0));
-    acc = __fmul_rn(w, row_lane ? part[0][lane] : 0.0f);
+    acc = __fmul_rn(w, d[0]);
   } else {
-    for (uint32_t j = 0; j < si.np; ++j) {
+#pragma unroll
+    for (uint32_t j = 0; j < uint32_t(kSlots); ++j) {
+      if (j >= si.np) break;
       const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(si.w), int(j)));
       const uint32_t shared = uint32_t(__builtin_amdgcn_readlane(int(si.shared), int(j)));
-      const float d = row_lane ? part[j][lane] : 0.0f;
-      acc = shared ? __fadd_rn(acc, d) : __fadd_rn(acc, __fmul_rn(w, d));
+      acc = shared ? __fadd_rn(acc, d[j]) : __fadd_rn(acc, __fmul_rn(w, d[j]));
     }
   }
   if (row_lane) Y[size_t(t) * kHidden + row0 + lane] = acc;
