@@ -149,15 +149,21 @@ __global__ __launch_bounds__(1024) void k_prefill_group(PrefillArgs a, PrefillWo
   const uint32_t tid = threadIdx.x;
   const uint32_t T = a.tokens, words = (T + 31) / 32;
   // read the bitmaps and leave them clear for the next call's top-k (the
-  // workspace starts clear), which saves a clearing launch per call
-  for (uint32_t i = tid; i < kMaxExperts * kPrefillBitWords; i += blockDim.x) {
-    const uint32_t w = i % kPrefillBitWords;
-    uint32_t v = 0u;
-    if (w < words) {
-      v = ws.token_bits[i];
-      ws.token_bits[i] = 0u;
-    }
-    bits[i / kPrefillBitWords][w] = v;
+  // workspace starts clear), which saves a clearing launch per call; all of
+  // a thread's loads are issued before the first is used
+  constexpr uint32_t kBitIters = kMaxExperts * kPrefillBitWords / 1024;
+  static_assert(kMaxExperts * kPrefillBitWords % 1024 == 0, "whole sweeps of the 1024 threads");
+  uint32_t bv[kBitIters];
+#pragma unroll
+  for (uint32_t j = 0; j < kBitIters; ++j) {
+    const uint32_t i = tid + 1024u * j;
+    bv[j] = i % kPrefillBitWords < words ? ws.token_bits[i] : 0u;
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < kBitIters; ++j) {
+    const uint32_t i = tid + 1024u * j, w = i % kPrefillBitWords;
+    if (w < words) ws.token_bits[i] = 0u;
+    bits[i / kPrefillBitWords][w] = bv[j];
   }
   __syncthreads();
   for (uint32_t e = tid; e <= kMaxExperts; e += blockDim.x) {
@@ -234,15 +240,25 @@ __global__ __launch_bounds__(1024) void k_prefill_group(PrefillArgs a, PrefillWo
       ws.items[item_off[e] + j] = PrefillItem{e, off[e] + first, n};
     }
   }
-  // pairs: routed (token t, slot s) -> position = tokens of the expert below t
+  // pairs: routed (token t, slot s) -> position = tokens of the expert below
+  // t; the token's ids and weights loaded before the first is used
   for (uint32_t t = tid; t < T; t += blockDim.x) {
-    for (uint32_t s = 0; s < a.r.topk; ++s) {
-      const uint32_t e = ws.ids[t * kTopK + s];
+    uint32_t ids[kTopK];
+    float wts[kTopK];
+#pragma unroll
+    for (uint32_t s = 0; s < uint32_t(kTopK); ++s) {
+      ids[s] = s < a.r.topk ? ws.ids[t * kTopK + s] : 0u;
+      wts[s] = s < a.r.topk ? ws.weights[t * kTopK + s] : 0.0f;
+    }
+#pragma unroll
+    for (uint32_t s = 0; s < uint32_t(kTopK); ++s) {
+      if (s >= a.r.topk) break;
+      const uint32_t e = ids[s];
       const uint32_t rank = below[e][t >> 5] + __popc(bits[e][t >> 5] & ((1u << (t & 31)) - 1u));
       const uint32_t p = off[e] + rank;
       ws.pair_token[p] = t;
       ws.token_pair[t * kSlots + s] = p;
-      ws.pair_weight[p] = ws.weights[t * kTopK + s];
+      ws.pair_weight[p] = wts[s];
     }
     const uint32_t ps = off[kMaxExperts] + t;
     ws.pair_token[ps] = t;
