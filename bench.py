@@ -270,6 +270,10 @@ def main() -> int:
             r["k8"] = {"us_per_token": ms * 1e3 / 8, "ms_per_block": ms, "timing": t, "distinct_pages": d,
                        "adjacent_overlap": ov, "hbm_gbps": block_bytes(round(d), 8) / (ms * 1e-3) / 1e9,
                        "stage_ms": {"route": st[0], "phase1": st[1], "phase2": st[2]}}
+            if name == "exact":
+                r["k8"]["stage_note"] = ("phase1/phase2: the kernels of the half of the pairs on the caller's "
+                                         "stream (phase2 up to the combine's end); the other half runs beside "
+                                         "them on the context's side stream")
             r["k8"]["hbm_frac"] = r["k8"]["hbm_gbps"] / HBM_PEAK_GBPS
         if only in ("config0", "all"):
             progress(f"config 0 (chain) {name}")
