@@ -448,6 +448,30 @@ def test_moe_block_graph_replays(ctx, bank):
     del g
 
 
+def test_moe_block_on_caller_stream(ctx, bank):
+    """An EXACT block launched on a caller's own stream (not torch's current
+    one), with that stream's earlier work writing the block's input: the side
+    stream forks after that work and joins before the output, so the result
+    equals the launch on the current stream bit for bit."""
+    say("config 3 block T=8 on a caller stream, input written on that stream just before")
+    router = s14.Router(bank["wr_d"], bank["bias_d"])
+    xs = synth.block_tokens(seed=50, tokens=8)
+    y_ref = torch.empty((8, HIDDEN), dtype=torch.float32, device="cuda")
+    s14.moe_block_route(ctx, 8, router, bank["table"], bank["pages"][256], dev(xs), y_ref, mode=s14.EXACT)
+    torch.cuda.synchronize()
+    src = dev(xs)
+    x = torch.zeros_like(src)
+    y = torch.empty_like(y_ref)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        x.copy_(src)  # the block's input, written on the caller's stream
+        s14.moe_block_route(ctx, 8, router, bank["table"], bank["pages"][256], x, y, mode=s14.EXACT,
+                            stream=stream.cuda_stream)
+    stream.synchronize()
+    assert_bit_exact(host(y), host(y_ref), "block on a caller stream")
+
+
 def test_moe_block_fp8_shared_and_edge_codes(ctx, oracle, bank):
     """Block launches (T=4) with the reference's FP8 shared page, so every
     phase-2 wavefront that serves a routed slot beside the shared one mixes
