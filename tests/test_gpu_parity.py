@@ -388,7 +388,7 @@ def test_moe_layer_route_config2(ctx, oracle, bank):
     assert st["max_abs"] <= 1e-3 and st["rmse"] <= 1.5e-4
 
 
-@pytest.mark.parametrize("tokens", [8, 3])
+@pytest.mark.parametrize("tokens", [8, 7, 3, 2])
 def test_moe_block_route_config3(ctx, oracle, bank, tokens):
     say(f"config 3 verify block T={tokens}, exact + fast")
     xs = synth.block_tokens(seed=4, tokens=tokens)
