@@ -11,14 +11,18 @@ wq_a matvec) and config 4 (the 512-token prefill).
 Every leg times the EXACT (oracle-order, bit-identical) kernels and the FAST
 (order-changed) ones.  Each leg's figure is the median of --trials trials;
 a trial times exactly --steps steps (after --warmup untimed ones) between
-two device synchronisations with events on the launch stream.  The steps of
-a trial are recorded once into a HIP graph and each trial replays it, so
-the figure is the device's time for the steps without the host's launch gap
-(the K=1 and K=8 legs also report the eager, launch-per-step figure).  Inputs are
-resident in HBM before timing: `--layers` layer banks of 257 expert pages
-live in one device arena (a VramPool), and consecutive steps rotate banks,
-pages and tokens so that the working set between reuses (> 1 GB) exceeds the
-256 MB MALL; config 1 rotates 96 copies of its 4 MiB weight.
+two events on the launch stream, queued behind an untimed pre-roll of the
+same steps so that the events bracket the device's work and not the host's
+submission.  The
+steps of a trial are recorded once into a HIP graph and each trial replays
+it (the K=1 and K=8 legs also report eager launches, one host launch
+sequence per step).  Inputs are resident in HBM before timing: `--layers`
+layer banks of 257 expert pages live in one device arena (a VramPool), and
+consecutive steps rotate banks, pages and tokens so that the working set
+between reuses (> 1 GB) exceeds the 256 MB MALL; config 1 rotates 96 copies
+of its 4 MiB weight.  The `variants` legs time the reference's published
+layer configuration (route given, FP8 shared page), official expert
+semantics at K=1 and K=8, a hash-routed layer and a MALL-resident layer.
 
 Prints one JSON line.
 """
@@ -57,16 +61,16 @@ def layer_bytes_k1() -> int:
     return 7 * PAGE + ROUTER + X_BYTES + X_BYTES
 
 
-def block_bytes(distinct: int, tokens: int) -> int:
-    # each distinct routed page and the shared page once; router once; x, y per token
-    return (distinct + 1) * PAGE + ROUTER + tokens * 2 * X_BYTES
+def block_bytes(distinct: float, tokens: int, shared_page: int = PAGE) -> float:
+    # each distinct routed page (D, the measured mean) and the shared page once; router once; x, y per token
+    return distinct * PAGE + shared_page + ROUTER + tokens * 2 * X_BYTES
 
 
 PREFILL_TOKENS = 512
 FP8_MFMA_PEAK_TFLOPS = 5000.0  # dense FP8 (the B operand's format; MXFP4 x FP8 runs at the FP8 rate)
 
 
-def prefill_bytes(distinct: int, tokens: int) -> int:
+def prefill_bytes(distinct: float, tokens: int) -> float:
     # each distinct routed page and the shared page once; router once; x in, y out
     return (distinct + 1) * PAGE + ROUTER + tokens * 2 * X_BYTES
 
@@ -79,6 +83,9 @@ def prefill_flops(tokens: int) -> int:
 def phase1_bytes(pairs: int, tokens: int) -> int:
     # w1/s1/w3/s3 of every (token, expert) pair as launched, x read, h written
     return pairs * UP + tokens * X_BYTES + pairs * H_BYTES
+
+
+LEGS = ("k1", "k8", "config0", "config1", "variants", "prefill", "linear", "upload")
 
 
 def parse():
@@ -98,9 +105,8 @@ def parse():
                     help="only run a plain 256 MiB device copy 10 times (the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     ap.add_argument("--prefill-steps", type=int, default=20)
-    ap.add_argument("--only", choices=["k1", "k8", "config0", "config1", "prefill", "linear", "upload", "all"],
-                    default="all",
-                    help="restrict the timed work (for profiler runs)")
+    ap.add_argument("--only", default="all",
+                    help="restrict the timed work (for profiler runs): a comma-separated subset of " + ",".join(LEGS))
     return ap.parse_args()
 
 
@@ -110,37 +116,79 @@ def progress(msg: str) -> None:
 
 class Timer:
     """Median-of-trials timing of a step function on torch's current stream
-    (the stream the library launches on)."""
+    (the stream the library launches on).
+
+    Each trial first queues a pre-roll, the same steps once more, untimed,
+    then the start event, the trial's steps and the end event.  The device
+    is still running the pre-roll while the host submits the timed steps, so
+    the two events bracket the device's work alone, as the reference's
+    timestamps do (s14_vulkan_numeric.rs:1088-1101), the device runs at the
+    workload's own clocks from the first timed step, and a trial's figure
+    does not depend on how many steps it holds.  A trial whose start event
+    had already completed when the host finished submitting (the device
+    idled waiting for work) is discarded and rerun with a longer pre-roll."""
 
     def __init__(self, torch, trials: int):
         self.torch = torch
         self.trials = max(1, trials)
 
+    def _trials(self, preroll, submit) -> tuple:
+        """Per-trial (device ms between the events, host submission ms) and
+        the pre-roll repeats used."""
+        torch = self.torch
+        per, host = [], []
+        n = 1
+        attempts = 0
+        while len(per) < self.trials:
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            for _ in range(n):
+                preroll()
+            start.record()
+            t0 = time.perf_counter()
+            submit()
+            end.record()
+            host_ms = (time.perf_counter() - t0) * 1e3
+            covered = not start.query()
+            torch.cuda.synchronize()
+            if covered:
+                per.append(start.elapsed_time(end))
+                host.append(host_ms)
+                continue
+            attempts += 1
+            if attempts > 6:
+                raise RuntimeError("the pre-roll never covered the host's submission")
+            n *= 2
+        return per, host, n
+
+    @staticmethod
+    def _summary(per: list, host: list, n: int, units: int, **extra) -> dict:
+        per = [p / units for p in per]
+        out = {"ms": statistics.median(per), "ms_min": min(per), "ms_max": max(per), "trials": len(per),
+               "host_submit_ms_max": max(host), "preroll_repeats": n}
+        out.update(extra)
+        return out
+
     def run(self, fn, steps: int, warmup: int) -> dict:
+        """Eager: the host launches every step inside the trial."""
         torch = self.torch
         steps = max(1, steps)
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
-        per = []
-        k = warmup
-        for _ in range(self.trials):
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            start.record()
+        k = [warmup]
+
+        def submit():
             for i in range(steps):
-                fn(k + i)
-            end.record()
-            torch.cuda.synchronize()
-            k += steps
-            per.append(start.elapsed_time(end) / steps)
-        return {"ms": statistics.median(per), "ms_min": min(per), "ms_max": max(per), "trials": len(per),
-                "steps_per_trial": steps}
+                fn(k[0] + i)
+            k[0] += steps
+
+        per, host, n = self._trials(submit, submit)
+        return self._summary(per, host, n, steps, steps_per_trial=steps, timing="eager launches")
 
     def run_graph(self, fn, launches: int, warmup: int) -> dict:
         """Median per-launch time of `launches` calls captured in one HIP
-        graph and replayed once per trial: device time without the host's
-        launch gap (for kernels of a few microseconds)."""
+        graph and replayed once per trial."""
         torch = self.torch
         for i in range(max(1, warmup)):
             fn(i)
@@ -151,17 +199,9 @@ class Timer:
                 fn(i)
         g.replay()  # first replay uploads the graph
         torch.cuda.synchronize()
-        per = []
-        for _ in range(self.trials):
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record()
-            g.replay()
-            end.record()
-            torch.cuda.synchronize()
-            per.append(start.elapsed_time(end) / launches)
+        per, host, n = self._trials(g.replay, g.replay)
         del g
-        return {"ms": statistics.median(per), "ms_min": min(per), "ms_max": max(per), "trials": len(per),
-                "launches_per_trial": launches, "timing": "hip graph replay"}
+        return self._summary(per, host, n, launches, launches_per_trial=launches, timing="hip graph replay")
 
 
 def main() -> int:
@@ -170,6 +210,13 @@ def main() -> int:
         print(f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported "
               "(the S14 path is single-GPU; multi-GPU sharding is design-only)", file=sys.stderr)
         return 2
+    only = set(args.only.split(","))
+    bad = only - set(LEGS) - {"all"}
+    if bad:
+        print(f"unknown --only legs {sorted(bad)}; choose from {', '.join(LEGS)} or all", file=sys.stderr)
+        return 2
+    if "all" in only:
+        only = set(LEGS)
 
     import numpy as np
     import torch
@@ -185,7 +232,6 @@ def main() -> int:
     ctx = s14.Context(0)
     NL, P = args.layers, args.tokens
     timer = Timer(torch, args.trials)
-    only = args.only
 
     # ---- resident inputs ----
     progress(f"filling {NL} x 257 expert pages")
@@ -251,7 +297,7 @@ def main() -> int:
     out = {}
     for name, m in (("exact", s14.EXACT), ("fast", s14.FAST)):
         r = {}
-        if only in ("k1", "all"):
+        if "k1" in only:
             progress(f"config 2 (K=1) {name}")
             t = timer.run_graph(step_k1(m), args.steps, args.warmup)
             t["eager"] = timer.run(step_k1(m), args.steps, args.warmup)
@@ -260,7 +306,7 @@ def main() -> int:
             r["k1"] = {"us_per_token": us, "timing": t, "hbm_gbps": layer_bytes_k1() / (us * 1e-6) / 1e9,
                        "stage_ms": {"route": st[0], "phase1": st[1], "phase2": st[2]}}
             r["k1"]["hbm_frac"] = r["k1"]["hbm_gbps"] / HBM_PEAK_GBPS
-        if only in ("k8", "all"):
+        if "k8" in only:
             progress(f"config 3 (K=8) {name}")
             t = timer.run_graph(step_k8(m), max(args.steps // 4, 10), max(args.warmup // 4, 5))
             t["eager"] = timer.run(step_k8(m), max(args.steps // 4, 10), max(args.warmup // 4, 5))
@@ -268,14 +314,14 @@ def main() -> int:
             d, ov = block_routes(m)
             ms = t["ms"]
             r["k8"] = {"us_per_token": ms * 1e3 / 8, "ms_per_block": ms, "timing": t, "distinct_pages": d,
-                       "adjacent_overlap": ov, "hbm_gbps": block_bytes(round(d), 8) / (ms * 1e-3) / 1e9,
+                       "adjacent_overlap": ov, "hbm_gbps": block_bytes(d, 8) / (ms * 1e-3) / 1e9,
                        "stage_ms": {"route": st[0], "phase1": st[1], "phase2": st[2]}}
             if name == "exact":
                 r["k8"]["stage_note"] = ("phase1/phase2: the kernels of the half of the pairs on the caller's "
                                          "stream (phase2 up to the combine's end); the other half runs beside "
                                          "them on the context's side stream")
             r["k8"]["hbm_frac"] = r["k8"]["hbm_gbps"] / HBM_PEAK_GBPS
-        if only in ("config0", "all"):
+        if "config0" in only:
             progress(f"config 0 (chain) {name}")
             t = timer.run_graph(step_chain(m), args.steps, args.warmup)
             st = stages(step_chain(m), args.profile_steps)
@@ -285,26 +331,32 @@ def main() -> int:
             r["config0"]["hbm_frac"] = r["config0"]["hbm_gbps"] / HBM_PEAK_GBPS
         out[name] = r
 
-    if only in ("config1", "all"):
+    if "config1" in only:
         progress("config 1 (wq_a fp8)")
         c1 = bench_config1(args, ctx, timer, torch, np, s14, synth)
         for name in ("exact", "fast"):
             out[name]["config1"] = c1[name]
 
+    variants = None
+    if "variants" in only:
+        progress("layer variants: reference layer, official, hash-routed, MALL-resident")
+        variants = bench_variants(args, ctx, timer, torch, np, s14, synth, N, bank, tables, shared, routers_h, wr,
+                                  bias, X, XB, NL, P, stages)
     prefill = None
-    if only in ("prefill", "all"):
+    if "prefill" in only:
         progress("config 4 (prefill)")
         prefill = bench_prefill(args, ctx, tables, shared, NL, torch, np, s14, synth)
     linear = None
-    if only in ("linear", "all"):
+    if "linear" in only:
         progress("adjacent FP8 projections (fp8_linear)")
         linear = bench_linear(args, ctx, timer, torch, s14)
     upload = None
-    if only in ("upload", "all"):
+    if "upload" in only:
         progress("page upload (ExpertLoader)")
         upload = bench_upload(args, ctx, torch, np, N, step_k1(s14.EXACT))
-    if only != "all" and only not in ("k1",):
-        print(json.dumps({"only": only, "legs": out, "prefill": prefill, "fp8_linear": linear, "upload": upload}),
+    if "k1" not in only:
+        print(json.dumps({"only": sorted(only), "legs": out, "variants": variants, "prefill": prefill,
+                          "fp8_linear": linear, "upload": upload}),
               flush=True)
         return 0
 
@@ -351,7 +403,9 @@ def main() -> int:
             "mode": args.mode,
             "parity": "bit-identical to the CPU oracle" if args.mode == "exact" else "order-changed f32",
             "timing": f"median of {args.trials} trials, each one replay of a HIP graph of {args.steps} steps "
-                      "(the eager figure, one host launch sequence per step, is in k1.timing.eager)",
+                      "between two events queued behind an untimed pre-roll of the same steps (the events "
+                      "bracket the device's work; the eager figure, one host launch sequence per step, is in "
+                      "k1.timing.eager)",
             "layer_banks": NL,
             "tokens_rotated": P,
             "layer_bytes_k1": layer_bytes_k1(),
@@ -363,6 +417,7 @@ def main() -> int:
         "config0": main_r.get("config0"),
         "config1": main_r.get("config1"),
         "other_mode": {k: v for k, v in out.items() if k != args.mode},
+        "variants": variants,
         "prefill": prefill,
         "fp8_linear": linear,
         "upload": upload,
@@ -397,6 +452,145 @@ def bench_config1(args, ctx, timer, torch, np, s14, synth):
         us = t["ms"] * 1e3
         res[name] = {"us_per_matvec": us, "timing": t, "algorithmic_bytes": WQA_BYTES,
                      "hbm_gbps": WQA_BYTES / (us * 1e-6) / 1e9, "hbm_frac": WQA_BYTES / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS}
+    return res
+
+
+# The reference's one published layer figure: six routed MXFP4 experts with
+# the FP8 shared page, route [126, 12, 205, 149, 227, 174] weighted by the
+# sqrt-softplus scores x 1.5, 35 dispatches, 1.3696 ms on an RX 5700 XT
+# (evidence/s14_vulkan_numeric_rx5700xt.json:49-53).
+REF_ROUTE = [126, 12, 205, 149, 227, 174]
+REF_LAYER_US = 1369.6
+FP8_SHARED_PAGE = 25_167_360
+
+
+def fp8_shared_pages(torch, n: int, seed: int):
+    """n device copies of an FP8 shared page ([w1|s1|w3|s3|w2|s2], e4m3 of
+    N(0,1) weights, UE8M0 128x128 tile scales 2^-7..2^-5), made with torch's
+    casts on the host: timing inputs only (parity tests use the seeded
+    generator and the oracle)."""
+    g = torch.Generator().manual_seed(seed)
+    parts = []
+    for _ in range(3):
+        w = torch.randn(2048 * 4096, generator=g).clamp_(-448.0, 448.0)
+        parts.append(w.to(torch.float8_e4m3fn).view(torch.uint8))
+        parts.append(torch.randint(120, 123, (512,), dtype=torch.uint8, generator=g))
+    page = torch.cat(parts)
+    assert page.numel() == FP8_SHARED_PAGE
+    out = torch.empty((n, FP8_SHARED_PAGE), dtype=torch.uint8, device="cuda")
+    for i in range(n):
+        out[i].copy_(page)
+    return out
+
+
+def bench_variants(args, ctx, timer, torch, np, s14, synth, N, bank, tables, shared, routers_h, wr, bias, X, XB, NL,
+                   P, stages):
+    """Layer configurations beside the headline, each a HIP graph of --steps
+    steps rotating layer banks and tokens as the headline does:
+    - the reference's published layer (route given, FP8 shared page), EXACT
+      and FAST, beside its 1.3696 ms;
+    - the same with the route chosen on the device (sqrt-softplus x 1.5);
+    - official expert semantics (executor.py:705-744) at K=1 and K=8, with
+      the config-2 router and MXFP4 shared page, and with the reference's
+      router and FP8 shared page;
+    - a hash-routed K=1 layer (tid2eid rows, executor.py:643-667);
+    - the headline layer with its 97.8 MB resident in the MALL (one layer
+      bank, one token repeated), against the rotated figure."""
+    res = {}
+    steps, warm = args.steps, args.warmup
+    f8 = fp8_shared_pages(torch, NL, args.seed)
+    Y = torch.empty(4096, dtype=torch.float32, device="cuda")
+    YB = torch.empty((8, 4096), dtype=torch.float32, device="cuda")
+    x0 = X[0].cpu().numpy().astype(np.float64)
+
+    def ref_weights(L):
+        z = routers_h[L][0].astype(np.float64) @ x0
+        sc = np.sqrt(np.where(z > 20, z, np.log1p(np.exp(np.minimum(z, 20)))))
+        w = sc[REF_ROUTE]
+        return (w / w.sum() * 1.5).astype(np.float32).tolist()
+
+    k1_ref_bytes = 6 * PAGE + FP8_SHARED_PAGE + 2 * X_BYTES
+    k1_ref_routed_bytes = 6 * PAGE + FP8_SHARED_PAGE + ROUTER + 2 * X_BYTES
+
+    def record(name, t, nbytes, tokens=1, **extra):
+        us = t["ms"] * 1e3 / tokens
+        gbps = nbytes / (t["ms"] * 1e-3) / 1e9
+        res[name] = {"us_per_token": us, "algorithmic_bytes": nbytes, "hbm_gbps": gbps,
+                     "hbm_frac": gbps / HBM_PEAK_GBPS, "timing": t, **extra}
+        progress(f"  {name}: {us:.2f} us/token, {gbps:.0f} GB/s")
+
+    # reference layer, route given
+    pages = [[bank.slot_ptr(L * 257 + e) for e in REF_ROUTE] for L in range(NL)]
+    wts = [ref_weights(L) for L in range(NL)]
+    for name, m in (("exact", s14.EXACT), ("fast", s14.FAST)):
+        def f(i, m=m):
+            L = i % NL
+            s14.moe_layer(ctx, pages[L], wts[L], f8[L], X[i % P], Y, shared_format=N.S14_PAGE_FP8, mode=m)
+        t = timer.run_graph(f, steps, warm)
+        record(f"k1_reference_layer_{name}", t, k1_ref_bytes, route=REF_ROUTE,
+               reference_rx5700xt_us=REF_LAYER_US, speedup_vs_reference=REF_LAYER_US / (t["ms"] * 1e3))
+
+    ref_routers = [s14.Router(wr[L], bias[L], score_fn=N.S14_SCORE_SQRT_SOFTPLUS, route_scale=1.5)
+                   for L in range(NL)]
+    cfg_routers = [s14.Router(wr[L], bias[L]) for L in range(NL)]
+
+    def k1(routers, sh, fmt, m):
+        def f(i):
+            L = i % NL
+            s14.moe_layer_route(ctx, routers[L], tables[L], sh[L], X[i % P], Y, shared_format=fmt, mode=m)
+        return f
+
+    def k8(routers, sh, fmt, m):
+        def f(i):
+            L = i % NL
+            s14.moe_block_route(ctx, 8, routers[L], tables[L], sh[L], XB[i % P], YB, shared_format=fmt, mode=m)
+        return f
+
+    def distinct(routers, sh, fmt, m):
+        ds = []
+        for i in range(min(P, 16)):
+            k8(routers, sh, fmt, m)(i)
+            ds.append(s14.last_block_distinct(ctx))
+        return float(np.mean(ds))
+
+    t = timer.run_graph(k1(ref_routers, f8, N.S14_PAGE_FP8, s14.EXACT), steps, warm)
+    record("k1_reference_routed_exact", t, k1_ref_routed_bytes, router="sqrt-softplus x 1.5", shared="fp8")
+
+    for label, routers, sh, fmt, nb, shared_bytes in (
+            ("", cfg_routers, shared, N.S14_PAGE_MXFP4, layer_bytes_k1(), PAGE),
+            ("_reference", ref_routers, f8, N.S14_PAGE_FP8, k1_ref_routed_bytes, FP8_SHARED_PAGE)):
+        fn = k1(routers, sh, fmt, s14.OFFICIAL)
+        t = timer.run_graph(fn, steps, warm)
+        st = stages(fn, args.profile_steps)
+        record(f"k1_official{label}", t, nb, stage_ms={"route": st[0], "phase1": st[1], "phase2": st[2]})
+        fn = k8(routers, sh, fmt, s14.OFFICIAL)
+        t = timer.run_graph(fn, max(steps // 4, 10), max(warm // 4, 5))
+        d = distinct(routers, sh, fmt, s14.OFFICIAL)
+        record(f"k8_official{label}", t, block_bytes(d, 8, shared_bytes), tokens=8, distinct_pages=d,
+               ms_per_block=t["ms"])
+
+    # hash routing: tid2eid rows of six distinct experts, token ids rotated
+    rng = np.random.default_rng(args.seed + 7)
+    vocab = 4096
+    tab = torch.from_numpy(np.stack([rng.choice(256, 6, replace=False) for _ in range(vocab)]).astype(np.int64)).cuda()
+    tok = torch.from_numpy(rng.integers(0, vocab, P).astype(np.int32)).cuda()
+    hash_routers = [[s14.Router(wr[L], bias[L], score_fn=N.S14_SCORE_SQRT_SOFTPLUS, route_scale=1.5, tid2eid=tab,
+                                token_ids=tok[p:p + 1]) for p in range(P)] for L in range(NL)]
+
+    def f_hash(i):
+        L = i % NL
+        s14.moe_layer_route(ctx, hash_routers[L][i % P], tables[L], shared[L], X[i % P], Y, mode=s14.EXACT)
+
+    t = timer.run_graph(f_hash, steps, warm)
+    record("k1_hash_exact", t, layer_bytes_k1(), router="tid2eid hash rows, sqrt-softplus x 1.5 weights")
+
+    def f_hot(i):
+        s14.moe_layer_route(ctx, cfg_routers[0], tables[0], shared[0], X[0], Y, mode=s14.EXACT)
+
+    t = timer.run_graph(f_hot, steps, warm)
+    record("k1_exact_mall_resident", t, layer_bytes_k1(),
+           note="one layer bank and one token repeated: the layer's 97.8 MB stay in the 256 MB MALL")
+    del f8
     return res
 
 
@@ -532,49 +726,61 @@ def bench_upload(args, ctx, torch, np, N, layer_step):
     return res
 
 
+PREFILL_LAYERS = 4  # layer banks rotated by the prefill leg (each prefill reads ~240 pages, 3.2 GB)
+
+
 def bench_prefill(args, ctx, tables, shared, NL, torch, np, s14, synth):
     """Config 4: 512 tokens through the layer as grouped scaled-MFMA GEMMs,
-    layers rotated across steps (each prefill reads ~240 distinct pages,
-    3.2 GB, well past the MALL anyway)."""
+    routed under Zipf(1.1) expert popularity (synth.prefill_router: the
+    busiest expert takes ~380 of the 512 tokens), layers rotated across
+    steps.  Reports the per-expert token counts (M_e) the routes gave."""
     T = PREFILL_TOKENS
+    NP = min(NL, PREFILL_LAYERS)
     routers = []
     keep = []
-    for L in range(NL):
-        _, b = synth.prefill_router(args.seed, L)
-        bias = torch.from_numpy(b).cuda()
-        keep.append(bias)
-        w, _ = synth.router(args.seed, L)
-        wt = torch.from_numpy(w).cuda()
-        keep.append(wt)
+    for L in range(NP):
+        w, b = synth.prefill_router(args.seed, L)
+        wt, bias = torch.from_numpy(w).cuda(), torch.from_numpy(b).cuda()
+        keep += [wt, bias]
         routers.append(s14.Router(wt, bias))
     xs = torch.from_numpy(synth.prefill_tokens(args.seed, T)).cuda()
     y = torch.empty((T, 4096), dtype=torch.float32, device="cuda")
+    ids = torch.empty((T, 6), dtype=torch.int16, device="cuda")
 
     def step(i):
-        L = i % NL
+        L = i % NP
         s14.moe_prefill(ctx, T, routers[L], tables[L], shared[L], xs, y)
 
     def step_official(i):
-        L = i % NL
+        L = i % NP
         s14.moe_prefill(ctx, T, routers[L], tables[L], shared[L], xs, y, mode=s14.OFFICIAL)
 
-    stats = []
-    for L in range(NL):
-        step(L)
+    stats, me = [], []
+    for L in range(NP):
+        s14.moe_prefill(ctx, T, routers[L], tables[L], shared[L], xs, y, ids_out=ids)
         stats.append(s14.last_prefill_stats(ctx))
+        c = np.bincount(ids.cpu().numpy().astype(np.int64).ravel() & 0xFFFF, minlength=256)
+        me.append(c[c > 0])
     t = Timer(torch, args.trials).run(step, max(args.prefill_steps, 1), 2)
     t_off = Timer(torch, args.trials).run(step_official, max(args.prefill_steps, 1), 2)
     ms = t["ms"]
     d = float(np.mean([s["distinct"] for s in stats]))
-    nbytes = prefill_bytes(round(d), T)
+    nbytes = prefill_bytes(d, T)
     flops = prefill_flops(T)
+    allme = np.concatenate(me)
     return {
         "tokens": T,
         "ms_per_prefill": ms,
         "us_per_token": ms * 1e3 / T,
         "timing": t,
+        "layers_rotated": NP,
+        "routing": "sigmoid router with per-expert bias calibrated to Zipf(1.1) top-6 popularity",
         "distinct_experts": d,
         "max_tokens_per_expert": max(s["max_tokens_per_expert"] for s in stats),
+        "tokens_per_expert": {"max_per_layer": [int(m.max()) for m in me],
+                              "p50": float(np.percentile(allme, 50)), "p90": float(np.percentile(allme, 90)),
+                              "mean": float(allme.mean())},
+        "work_items": float(np.mean([s["items"] for s in stats])),
         "algorithmic_bytes": nbytes,
         "hbm_gbps": nbytes / (ms * 1e-3) / 1e9,
         "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,

@@ -513,16 +513,28 @@ int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, con
       if ((e = hipEventRecord(fork->fork, st)) != hipSuccess) return hip_fail(e, "hipEventRecord(fork)");
       if ((e = hipStreamWaitEvent(fork->side, fork->fork, 0)) != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
     }
+    const char *failed = nullptr;
     e = launch_block_phase1(st, ws, 0, na, mx, f8, x, ev ? ev[kStagePhase1] : KernelEvents{});
     if (e == hipSuccess && nb) e = launch_block_phase1(fork->side, ws, na, nb, mx, f8, x);
-    if (e != hipSuccess) return hip_fail(e, "phase 1 launch");
-    e = launch_block_phase2(st, ws, 0, na, mx, f8, ev ? ev[kStagePhase2].start : nullptr);
-    if (e == hipSuccess && nb) e = launch_block_phase2(fork->side, ws, na, nb, mx, f8);
-    if (e != hipSuccess) return hip_fail(e, "phase 2 launch");
-    if (fork) {
-      if ((e = hipEventRecord(fork->join, fork->side)) != hipSuccess) return hip_fail(e, "hipEventRecord(join)");
-      if ((e = hipStreamWaitEvent(st, fork->join, 0)) != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
+    if (e != hipSuccess) {
+      failed = "phase 1 launch";
+    } else {
+      e = launch_block_phase2(st, ws, 0, na, mx, f8, ev ? ev[kStagePhase2].start : nullptr);
+      if (e == hipSuccess && nb) e = launch_block_phase2(fork->side, ws, na, nb, mx, f8);
+      if (e != hipSuccess) failed = "phase 2 launch";
     }
+    if (fork) {
+      // the side stream joins the caller's also after a failed launch, so a
+      // capture never ends with an unjoined branch (the launch error is the
+      // one reported)
+      hipError_t j = hipEventRecord(fork->join, fork->side);
+      if (j == hipSuccess) j = hipStreamWaitEvent(st, fork->join, 0);
+      if (!failed && j != hipSuccess) {
+        e = j;
+        failed = "side stream join";
+      }
+    }
+    if (failed) return hip_fail(e, failed);
     e = launch_block_combine(st, ws, tokens, y, ev ? ev[kStagePhase2].stop : nullptr);
     if (e != hipSuccess) return hip_fail(e, "combine launch");
     return S14_OK;

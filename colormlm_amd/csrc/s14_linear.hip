@@ -423,13 +423,6 @@ __device__ __forceinline__ uint32_t lin_swz(uint32_t r) { return (r + (r >> 3)) 
 // with the write-through stores of the other XCDs.
 constexpr int kCacheAgent = 0x10;
 
-// Staged activations per wavefront: ntok x cw chunks x 128 bf16, plus the
-// f32 scale of every (token, chunk) when the scales are f32 (host bound).
-constexpr uint32_t kLinStageBytes = 40u * 1024u;
-__host__ __device__ constexpr uint32_t lin_stage_bytes(uint32_t ntok, uint32_t cw) {
-  return ntok * cw * (kLinGroup * 2u + 4u);
-}
-
 // Sixteen e4m3 codes times a power of two (or 1) as sixteen bf16, exact.
 __device__ __forceinline__ v4u e4m3x4_bf16s(uint32_t w0, uint32_t w1, float s) {
   return v4u{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, s, false)),
@@ -602,28 +595,6 @@ __global__ __launch_bounds__(64) void k_linear_fast(LinearArgs a, LinearWorkspac
   }
 }
 
-// Chunks per FAST wavefront: the smallest multiple of 4 dividing G that
-// keeps the grid within kFastWaves wavefronts (more K splits fill the GPU for
-// short, wide weights; fewer amortise the ring's prologue), limited by the
-// staged activations, the partial buffer and the counters.
-constexpr uint32_t kFastWaves = 1024;
-
-uint32_t fast_chunks(uint32_t G, uint32_t tiles, uint32_t ncb, uint32_t ntok) {
-  const uint64_t tiles_all = uint64_t(tiles) * ncb;
-  uint32_t best = 4;  // G % 4 == 0 (host): always a divisor, and it fits the stage for 32 tokens
-  for (uint32_t cw = 4; cw <= G; cw += 4) {
-    if (G % cw) continue;
-    if (lin_stage_bytes(ntok, cw) > kLinStageBytes) break;
-    best = cw;
-    const uint64_t splits = G / cw;
-    if (splits > 1 && (tiles_all > kLinMaxCounters ||
-                       tiles_all * splits * kLinTile * kLinTile * sizeof(float) > kLinPartBytes))
-      continue;
-    if (tiles_all * splits <= kFastWaves) return cw;
-  }
-  return best;
-}
-
 }  // namespace
 
 hipError_t launch_act_quant(hipStream_t s, uint32_t rows, uint32_t k, uint32_t group, const float *x, uint8_t *q,
@@ -715,14 +686,28 @@ static hipError_t launch_exact_tiled(hipStream_t s, const LinearArgs &a, const L
 
 hipError_t launch_fp8_linear(hipStream_t s, const LinearArgs &a, int mode, const LinearWorkspace &ws) {
   const bool fast = mode == S14_MODE_FAST && a.k % (4u * kLinGroup) == 0u;
-  if (fast) {
-    const uint32_t tiles = (a.n + kLinTile - 1) / kLinTile, ncb = (a.m + kLinTile - 1) / kLinTile;
-    const uint32_t ntok = min(a.m, kLinTile);
-    const uint32_t cw = fast_chunks(a.groups, tiles, ncb, ntok);
-    const uint32_t splits = a.groups / cw;
-    const dim3 grid(tiles, splits, ncb);
-    launch_fast_ring<kLinRing>(s, a, ws, cw, splits, grid, lin_stage_bytes(ntok, cw));
-    return hipGetLastError();
+  const LinFastPlan plan = fast ? lin_fast_plan(a.m, a.n, a.groups) : LinFastPlan{0, 0};
+  if (plan.cw) {
+    // one launch per plan.blocks token blocks, each within the workspace's
+    // partials and counters (a smaller last launch fits whatever fits more)
+    const uint32_t tiles = (a.n + kLinTile - 1) / kLinTile, per = plan.blocks * kLinTile;
+    const uint32_t xs_stride = a.x_scale_f32 ? 4u : 1u;
+    for (uint32_t m0 = 0; m0 < a.m; m0 += per) {
+      LinearArgs c = a;
+      c.m = std::min(per, a.m - m0);
+      c.x = a.x + size_t(m0) * a.k;
+      c.x_scale = static_cast<const uint8_t *>(a.x_scale) + size_t(m0) * a.groups * xs_stride;
+      c.y = a.y + size_t(m0) * a.n;
+      const uint32_t ncb = (c.m + kLinTile - 1) / kLinTile, ntok = std::min(c.m, kLinTile);
+      const uint32_t cw = lin_fast_chunks(a.groups, tiles, ncb, ntok);
+      const uint32_t splits = cw ? a.groups / cw : 0u;
+      if (!cw || lin_part_bytes(tiles, ncb, splits) > kLinPartBytes ||
+          (splits > 1u && uint64_t(tiles) * ncb > kLinMaxCounters))
+        return hipErrorInvalidValue;  // unreachable: the plan fits every launch
+      launch_fast_ring<kLinRing>(s, c, ws, cw, splits, dim3(tiles, splits, ncb), lin_stage_bytes(ntok, cw));
+      if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    }
+    return hipSuccess;
   }
   const bool vec = a.k % 16u == 0u &&
                    ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.w)) & 15u) == 0u;

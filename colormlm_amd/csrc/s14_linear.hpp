@@ -7,13 +7,11 @@
 
 #include <cstdint>
 
+#include "s14_linear_plan.h"
+
 namespace s14 {
 
-constexpr uint32_t kLinGroup = 128;            // k values per activation / weight scale (fp8.py:14)
-constexpr uint32_t kLinMaxK = 128u * 1024u;    // EXACT keeps a row's group partials in LDS
-constexpr uint32_t kLinTile = 32;              // FAST: output rows (and token columns) per MFMA tile
-constexpr size_t kLinPartBytes = size_t(32) << 20;  // FAST split-K partials (per context)
-constexpr uint32_t kLinMaxCounters = 65536;    // FAST: one arrival counter per (row tile, token block)
+constexpr uint32_t kLinMaxK = 128u * 1024u;  // EXACT keeps a row's group partials in LDS
 
 struct LinearArgs {
   uint32_t m, n, k, groups;  // tokens, output rows, input features, ceil(k / 128)

@@ -8,16 +8,25 @@
 // device array `scratch`, one copy per GPU, held until the process ends.  In
 // host code `scratch` names a host-side stand-in, not a device address, so
 // host code never passes it to a kernel: the first call on a device, with
-// that device current, looks up its device address once with
-// hipGetSymbolAddress and keeps it per device, and every launch uses that
-// pointer.  That first call also enqueues, on the caller's stream, a kernel
-// that zeroes the route completion counters (every route launch leaves them
-// at zero again).
+// that device current, looks up its device address with hipGetSymbolAddress
+// and keeps it per device, and every launch uses that pointer.  Only a
+// successful set-up is kept: a call whose set-up fails returns the error and
+// the next call on that device tries again.  The set-up also enqueues, on
+// the caller's stream, a kernel that zeroes the route completion counters
+// and the status line (the array starts zeroed as static storage; every
+// route launch leaves the counters at zero again).  When the caller is
+// capturing that stream into a graph, the lookup runs with this thread's
+// capture mode relaxed (it is no stream operation) and the clear is
+// recorded into the graph, where it runs ahead of the captured route on
+// every replay.
 //
 // Every call on a GPU shares that GPU's array: calls that overlap on one GPU
-// (different streams or threads) race on it.
+// (different streams or threads) race on it.  Bad routes and non-resident
+// pages are reported only as NaN outputs of the affected tokens: the status
+// bits the launches leave in the array have no reader here.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "s14_device.hpp"
@@ -30,31 +39,37 @@ static __device__ __align__(256) uint8_t scratch[s14::kWorkspaceBytes];
 constexpr int kMaxDevices = 64;
 
 struct DeviceScratch {
-  std::once_flag once;
-  int rc = S14_OK;
-  void *ptr = nullptr;  // device address of this GPU's `scratch`
+  std::mutex mu;
+  std::atomic<void *> ptr{nullptr};  // device address of this GPU's `scratch`, once set up
 };
 DeviceScratch g_devices[kMaxDevices];
 
-// Set-up of one device (the calling thread's current device), once.
+// The device address of the calling thread's current device's `scratch`,
+// set up on the first successful call.
 int device_scratch(int device, hipStream_t stream, void **out) {
   DeviceScratch &d = g_devices[device];
-  std::call_once(d.once, [&d, stream]() {
-    void *p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !p) {
-      d.rc = s14::fail(S14_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
-      return;
-    }
-    const hipError_t c = s14::launch_clear_route_counters(stream, s14::workspace_carve(p));
-    if (c != hipSuccess) {
-      d.rc = s14::fail(S14_ERR_HIP, "route counter clear: %s", hipGetErrorString(c));
-      return;
-    }
-    d.ptr = p;
-  });
-  if (d.rc != S14_OK) return d.rc;
-  *out = d.ptr;
+  if (void *p = d.ptr.load(std::memory_order_acquire)) {
+    *out = p;
+    return S14_OK;
+  }
+  std::lock_guard<std::mutex> lock(d.mu);
+  if (void *p = d.ptr.load(std::memory_order_relaxed)) {
+    *out = p;
+    return S14_OK;
+  }
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  hipError_t e = hipThreadExchangeStreamCaptureMode(&mode);
+  if (e != hipSuccess) return s14::fail(S14_ERR_HIP, "hipThreadExchangeStreamCaptureMode: %s", hipGetErrorString(e));
+  void *p = nullptr;
+  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  const hipError_t r = hipThreadExchangeStreamCaptureMode(&mode);  // the caller's mode again
+  if (e != hipSuccess || !p)
+    return s14::fail(S14_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+  if (r != hipSuccess) return s14::fail(S14_ERR_HIP, "hipThreadExchangeStreamCaptureMode: %s", hipGetErrorString(r));
+  const hipError_t c = s14::launch_clear_route_counters(stream, s14::workspace_carve(p));
+  if (c != hipSuccess) return s14::fail(S14_ERR_HIP, "route counter clear: %s", hipGetErrorString(c));
+  d.ptr.store(p, std::memory_order_release);
+  *out = p;
   return S14_OK;
 }
 

@@ -19,6 +19,8 @@ Configs (the north-star list):
 
 from __future__ import annotations
 
+import functools
+
 import numpy as np
 
 MASK = (1 << 64) - 1
@@ -236,16 +238,43 @@ def prefill_tokens(seed: int = 0, tokens: int = 512) -> np.ndarray:
     return np.stack([gen_normal(seed, STREAM_PREFILL + t, HIDDEN) for t in range(tokens)])
 
 
-def prefill_router(seed: int = 0, layer: int = 0, beta: float = 0.04, s: float = 1.1):
-    """Config 4 router: W_r as config 2, bias_e = beta * log(zipf_pmf(rank_e))
-    over a seeded permutation of the experts, so expert popularity is skewed
-    Zipf(s)-like.  beta = 0.04 gives, over 512 tokens, about 240 distinct
-    experts with the busiest at about 100 tokens (mean about 13)."""
+@functools.lru_cache(maxsize=4)
+def zipf_top6_inclusion(s: float = 1.1, n_experts: int = N_EXPERTS, topk: int = 6, samples: int = 40000) -> np.ndarray:
+    """P(rank r is among a token's topk experts) when each token draws its
+    topk distinct experts with probability proportional to Zipf(s) over
+    ranks (sampling without replacement, drawn as the top-k of log p + Gumbel
+    noise; seeded Monte Carlo)."""
+    rng = np.random.default_rng(0x5A1F)
+    logp = -s * np.log(np.arange(1, n_experts + 1, dtype=np.float64))
+    hits = np.zeros(n_experts)
+    for lo in range(0, samples, 10000):
+        g = rng.gumbel(size=(min(10000, samples - lo), n_experts)) + logp
+        hits += np.bincount(np.argpartition(-g, topk, axis=1)[:, :topk].ravel(), minlength=n_experts)
+    return hits / samples
+
+
+def prefill_router(seed: int = 0, layer: int = 0, s: float = 1.1, iters: int = 300):
+    """Config 4 router: W_r as config 2 and a bias per expert calibrated so
+    that top6(sigmoid(W_r x) + bias) over x ~ N(0, 1) picks each expert as
+    often as top-6 sampling under Zipf(s) popularity would (experts ranked by
+    a seeded permutation).  The calibration nudges each expert's bias by the
+    log ratio of its target and observed inclusion rates over 4,096 seeded
+    calibration tokens.  Measured on the bench's 512 prefill tokens (seed 0):
+    busiest expert 376-389 tokens and 235-243 distinct experts over layers
+    0-3, per-expert tokens p50 4 and p90 21-25; pure Zipf(1.1) top-6
+    sampling gives 394, 242, 4 and 22 on average."""
     wr, _ = router(seed, layer)
     keys = rand_u64(seed, STREAM_ZIPF_PERM + (layer << 8), np.arange(N_EXPERTS, dtype=np.uint64))
     rank = np.empty(N_EXPERTS, dtype=np.int64)
     rank[np.argsort(keys, kind="stable")] = np.arange(N_EXPERTS)
-    pmf = 1.0 / np.power(rank + 1.0, s)
-    pmf /= pmf.sum()
-    bias = (beta * np.log(pmf)).astype(np.float32)
-    return wr, bias
+    target = zipf_top6_inclusion(s)[rank]
+    rng = np.random.default_rng([seed & 0xFFFFFFFF, layer, 0x2F])
+    xc = rng.standard_normal((4096, HIDDEN), dtype=np.float32)
+    scores = 1.0 / (1.0 + np.exp(-(xc @ wr.T).astype(np.float64)))
+    bias = 0.05 * np.log(target)
+    lt = np.log(target + 1e-4)
+    for _ in range(iters):
+        top = np.argpartition(-(scores + bias), 6, axis=1)[:, :6]
+        seen = np.bincount(top.ravel(), minlength=N_EXPERTS) / scores.shape[0]
+        bias += 0.025 * (lt - np.log(seen + 1e-4))
+    return wr, bias.astype(np.float32)

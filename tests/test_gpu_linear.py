@@ -188,3 +188,19 @@ def test_fp8_linear_exact_token_chunks(ctx, oracle):
     y = torch.empty((m, n), dtype=torch.float32, device="cuda")
     s14.fp8_linear(ctx, dev(x), dev(xs), dev(w), dev(ws), y, mode=s14.EXACT)
     assert np.array_equal(host(y).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("m", [129, 512])
+def test_fp8_linear_fast_token_blocks_in_several_launches(ctx, oracle, m):
+    """wq_b's FAST split-K partials take 8 MiB per 32-token block, so the
+    32 MiB workspace holds 4 blocks: 129 tokens run as launches of 96 and 33
+    tokens, 512 as four of 128.  Every token's row matches the oracle."""
+    n, k = SHAPES["wq_b"]
+    say(f"fp8_linear fast wq_b m={m} (several launches)")
+    w, ws = weight(n, k, seed=21)
+    rng = np.random.default_rng(m)
+    x, xs = codes(rng, (m, k)), rng.integers(120, 128, (m, k // 128), dtype=np.uint8)
+    want = oracle.fp8_linear(x, xs, w, ws)
+    y = torch.full((m, n), np.nan, dtype=torch.float32, device="cuda")
+    s14.fp8_linear(ctx, dev(x), dev(xs), dev(w), dev(ws), y, mode=s14.FAST)
+    check_fast(oracle, host(y), want, x, xs, w, ws, f"wq_b m={m}")

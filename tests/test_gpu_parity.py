@@ -775,8 +775,10 @@ def test_prefill_config4_512_properties(ctx, oracle, bank, prefill_router):
     (an MFMA column does not see its neighbours), so the first 64 tokens
     must equal a 64-token run bit for bit, whatever tiles and work items the
     grouping gave them; repeat runs are identical; all 512 routes match the
-    oracle; and the stages of the busiest expert's pairs (split over several
-    32-token work items) and of the shared expert's pairs check out."""
+    oracle; and the stages check out for one pair of every 32-token work
+    item of the busiest expert (the routes follow Zipf(1.1) popularity, so
+    that expert takes about 380 of the 512 tokens: 12 work items streaming
+    its page) and for pairs of the shared expert."""
     T = 512
     say(f"config 4 prefill T={T}: properties, stages of the busiest experts")
     xs = synth.prefill_tokens(seed=0, tokens=T)
@@ -794,7 +796,9 @@ def test_prefill_config4_512_properties(ctx, oracle, bank, prefill_router):
     say(f"  stats {st}; tokens/expert mean {counts[counts > 0].mean():.2f}")
     busiest = int(np.argmax(counts))
     on_busiest = np.flatnonzero((ids == busiest).any(axis=1))
-    check = [int(view["token_pair"][t][list(ids[t]).index(busiest)]) for t in on_busiest[[0, 40, -1]]]
+    assert len(on_busiest) >= 300, f"busiest expert has {len(on_busiest)} tokens (Zipf(1.1) head: ~380)"
+    firsts = list(on_busiest[::32]) + [on_busiest[-1]]
+    check = [int(view["token_pair"][t][list(ids[t]).index(busiest)]) for t in firsts]
     check += [int(view["token_pair"][t][6]) for t in (0, 127, 128, 300, 511)]
     _check_prefill_stages(oracle, bank, view, xs, ids, wts, y, sorted(check))
     y2, ids2, _ = _run_prefill(ctx, bank, prefill_router, xs)
@@ -1151,9 +1155,9 @@ def test_official_chain_weight_before_w2(ctx, oracle, bank):
                                                    (N.S14_SCORE_SQRT_SOFTPLUS, 1.5, 3)])
 def test_official_block(ctx, oracle, bank, score_fn, scale, tokens):
     """Official blocks through the device router, token by token against the
-    oracle's official layer evaluated with the device's route (bit for bit
-    for the sigmoid score; sqrt-softplus weights within 1e-6 relative, the
-    device's log1pf not being glibc's)."""
+    oracle: ids and weights bit for bit with the oracle's own route (both
+    score functions), and the output bit for bit with the oracle's official
+    layer evaluated on that route."""
     say(f"official block T={tokens} score_fn={score_fn}")
     xs = synth.block_tokens(seed=9, tokens=tokens)
     router = s14.Router(bank["wr_d"], bank["bias_d"], score_fn=score_fn, route_scale=scale)
@@ -1167,10 +1171,7 @@ def test_official_block(ctx, oracle, bank, score_fn, scale, tokens):
     for t in range(tokens):
         _, i_o, w_o = oracle.route(bank["wr"], bank["bias"], xs[t], score_fn=score_fn, route_scale=scale)
         assert ids_h[t].tolist() == i_o.tolist()
-        if score_fn == N.S14_SCORE_SIGMOID:
-            assert_bit_exact(wts_h[t], w_o, f"weights t={t}")
-        else:
-            np.testing.assert_allclose(wts_h[t], w_o, rtol=1e-6)
-        want = oracle.moe_layer_official(xs[t], [page_host(bank, int(e)) for e in i_o], wts_h[t], shared)
+        assert_bit_exact(wts_h[t], w_o, f"weights t={t}")
+        want = oracle.moe_layer_official(xs[t], [page_host(bank, int(e)) for e in i_o], w_o, shared)
         assert_bit_exact(got[t], want, f"official block t={t}")
 
