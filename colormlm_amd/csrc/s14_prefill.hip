@@ -1,33 +1,32 @@
 // Prefill through the S14 MoE layer (config 4) on gfx950: T tokens, each
 // routed to its top-k experts plus the shared expert, computed per expert as
-// grouped GEMMs on the CDNA4 scaled MFMA (v_mfma_scale_f32_32x32x64_f8f6f4):
-// MXFP4 weights (A, E8M0 per 32 k) times e4m3-requantised activations (B,
-// E8M0 per 32 k), f32 accumulation.
+// grouped GEMMs on the CDNA4 bf16 MFMA (v_mfma_f32_32x32x16_bf16): MXFP4
+// weights (A, E8M0 per 32 k) and e4m3-requantised activations (B, E8M0 per
+// 32 k) are decoded to bf16 in registers by the gfx950 scaled converters,
+// exactly (an e2m1 value has two significant bits, an e4m3 value four, the
+// E8M0 scale is a power of two), so every product is exact in f32 and only
+// the f32 accumulation order differs from the CPU oracle's sequential sum.
 //
 // There is no reference GPU code for this row; its semantics are the layer's
 // (s14_vulkan_numeric.rs:929-946 accumulation, :1543-1556 SwiGLU) with the
 // activation requant the north-star config names (e4m3 RNE, saturating,
 // per-32 scale 2^ceil(log2(max(amax, 1e-4) / 448)), l42_reference.py:390-403
-// with group 32).  The MFMA sums each 64-k step in its own precision, so
-// this path is not order-exact; its tolerance against the CPU oracle is
-// measured (tests/test_gpu_parity.py).
+// with group 32).  Its tolerance against the CPU oracle is measured
+// (tests/test_gpu_parity.py).
 //
-// Operand layout of the 32x32x64 scaled MFMA (established on the hardware,
-// lane l, half h = l / 32):
-//   A (fp4, 16 bytes)  row l % 32; bytes 0..7 hold k 16h..16h+15 and bytes
-//                      8..15 hold k 32+16h..32+16h+15 (low nibble first)
-//                      when B is laid out as below; scale_a of lane l covers
-//                      the 32 k it holds, i.e. weight block h of the step.
-//   B (fp8, 32 bytes)  column l % 32; byte j pairs with A as above, so B must
-//                      hold {k 16h..16h+15, k 32+16h..32+16h+15} of the step;
-//                      a product from A half h is scaled by scale_b of lane
-//                      (column, h).
-//   D (16 f32)         element i of lane l is row 8(i/4) + 4h + i%4, column
-//                      l % 32.
-// Loading each weight row's 16 contiguous bytes per lane-half (32 k, one
-// E8M0 block) therefore pairs with activations stored per 64-k step in the
-// order [k 0..15 | 32..47 | 16..31 | 48..63]: requant_x and the phase-1
-// epilogue write x and h in that order.
+// The gfx950 scaled MFMA (v_mfma_scale_f32_32x32x64_f8f6f4) would take the
+// MXFP4 and e4m3 operands undecoded, but it sums each 64-k step at its own
+// internal precision (it returns 256 * 256 + 1 * 1 as 65,536 when the two
+// products share a step): GEMM results 5.7e-5 of the output's scale away
+// from the oracle's, against 8e-7 here.
+//
+// Operand layout of v_mfma_f32_32x32x16_bf16 (lane l, half h = l / 32):
+// A is row l % 32, B column l % 32, each 8 bf16 at k 8h..8h+7 of the MFMA's
+// 16; D element i of lane l is row 8(i/4) + 4h + i%4, column l % 32.  A 64-k
+// step is four MFMAs: in MFMA j, lane half h supplies k 32h + 8j .. +7 of
+// the step, so a lane's 16 weight bytes (k 32h..32h+31 of its row, one
+// E8M0 block) and its column's 32 activations at the same k (one E8M0
+// block) feed it.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
@@ -39,8 +38,8 @@
 namespace s14 {
 namespace {
 
-typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 constexpr uint32_t kQGroup = 32;  // requant group (k values per E8M0 scale)
 
@@ -50,7 +49,7 @@ constexpr uint32_t kQGroup = 32;  // requant group (k values per E8M0 scale)
 
 using s14x::e4m3_rne_sat;  // s14_e4m3.h: straight-line, checked against the oracle on the CPU
 
-// X [T, 4096] f32 -> Q [T, 4096] e4m3 in MFMA order + S [T, 128] E8M0.
+// X [T, 4096] f32 -> Q [T, 4096] e4m3 + S [T, 128] E8M0.
 // One thread per 32-value group.  kOfficial: the official act_quant's group
 // of 128 (l42_reference.py:390-403): the maximum over the four adjacent
 // threads of a 128-value group, whose four E8M0 bytes then hold the same
@@ -93,11 +92,9 @@ __global__ __launch_bounds__(256) void k_requant_x(uint32_t tokens, const float 
     for (int j = 0; j < 4; ++j) word |= e4m3_rne_sat(__fmul_rn(v[4 * i + j], inv)) << (8 * j);
     w[i] = word;
   }
-  // group g = 32 consecutive k at offset 32*(g%2) of step g/2
-  uint8_t *dst = Q + size_t(t) * kHidden + 64u * (g >> 1);
-  const uint32_t b = g & 1u;
-  *reinterpret_cast<uint4 *>(dst + 16u * b) = make_uint4(w[0], w[1], w[2], w[3]);        // k 0..15 of the group
-  *reinterpret_cast<uint4 *>(dst + 32u + 16u * b) = make_uint4(w[4], w[5], w[6], w[7]);  // k 16..31
+  uint8_t *dst = Q + size_t(t) * kHidden + kQGroup * g;
+  *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+  *reinterpret_cast<uint4 *>(dst + 16u) = make_uint4(w[4], w[5], w[6], w[7]);
   S[size_t(t) * groups + g] = uint8_t(code);
 }
 
@@ -271,7 +268,7 @@ __global__ __launch_bounds__(1024) void k_prefill_group(PrefillArgs a, PrefillWo
 // grouped GEMMs
 // ---------------------------------------------------------------------------
 
-// Each work item's x rows (MFMA order, from requant_x) into the item's tile.
+// Each work item's x rows into the item's tile.
 // Columns past the item's count are not written: the GEMMs never read them.
 // One thread per 16 tile bytes; the thread holding part 0 of the first step
 // of a chunk also writes that chunk's scale word.
@@ -306,13 +303,48 @@ __device__ __forceinline__ Rsrc page_rsrc(const PrefillArgs &a, uint32_t e) {
   return make_rsrc(page, uint32_t(S14_EXPERT_PAGE_BYTES));
 }
 
-__device__ __forceinline__ v8i a_operand(uint4 w) {
-  v8i v = {int(w.x), int(w.y), int(w.z), int(w.w), 0, 0, 0, 0};
-  return v;
+// E8M0 code c as the scale operand of the gfx950 scaled converters (they
+// take only its exponent field: 2^(c-127), code 0 included).
+__device__ __forceinline__ float e8m0_operand(uint32_t c) { return __uint_as_float(c << 23); }
+
+// Eight fp4 (four bytes, low nibble first: k ascending) times 2^(c-127) as
+// eight bf16, exact.
+__device__ __forceinline__ v8bf fp4x8_bf16(uint32_t w, float s) {
+  const v4u v = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 0)),
+                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 1)),
+                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 2)),
+                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 3))};
+  return __builtin_bit_cast(v8bf, v);
 }
-__device__ __forceinline__ v8i b_operand(uint4 lo, uint4 hi) {
-  v8i v = {int(lo.x), int(lo.y), int(lo.z), int(lo.w), int(hi.x), int(hi.y), int(hi.z), int(hi.w)};
-  return v;
+// Eight e4m3 (two words, byte order = k order) times 2^(c-127) as eight
+// bf16, exact.
+__device__ __forceinline__ v8bf fp8x8_bf16(uint32_t w0, uint32_t w1, float s) {
+  const v4u v = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, s, false)),
+                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, s, true)),
+                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, s, false)),
+                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, s, true))};
+  return __builtin_bit_cast(v8bf, v);
+}
+// One 64-k step of a lane's activations (lo: k 32h..32h+15 of the step, hi:
+// k 32h+16..32h+31, one E8M0 block) as the B operands of the step's four
+// MFMAs: MFMA j takes k 32h+8j..32h+8j+7.
+struct BStep {
+  v8bf b[4];
+};
+__device__ __forceinline__ BStep b_step(uint4 lo, uint4 hi, uint32_t code) {
+  const float s = e8m0_operand(code);
+  return BStep{{fp8x8_bf16(lo.x, lo.y, s), fp8x8_bf16(lo.z, lo.w, s), fp8x8_bf16(hi.x, hi.y, s),
+                fp8x8_bf16(hi.z, hi.w, s)}};
+}
+// acc += A . B over one 64-k step: the lane's 16 weight bytes (k 32h..32h+31
+// of its row, one E8M0 block) decoded exactly to bf16 against the step's
+// activations, four MFMAs (exact products, f32 accumulation).
+__device__ __forceinline__ v16f mfma_step(uint4 w, uint32_t code, const BStep &b, v16f acc) {
+  const float s = e8m0_operand(code);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp4x8_bf16(w.x, s), b.b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp4x8_bf16(w.y, s), b.b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp4x8_bf16(w.z, s), b.b[2], acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp4x8_bf16(w.w, s), b.b[3], acc, 0, 0, 0);
 }
 
 // Pins the accumulators in uniform control flow.  The epilogues store only
@@ -486,10 +518,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       const uint32_t sb = 2u * (c * kChunkSteps + k) + h;  // scale byte of this lane's weight block
       const uint32_t sp = 128u * col + 16u * ((sb >> 4) ^ sw) + (sb & 15u);
       const uint32_t c1 = up_scales[sp], c3 = up_scales[4096u + sp];
-      const uint32_t cb = (rb[S].sc >> (8u * k)) & 0xffu;
-      const v8i B = b_operand(rb[S].lo[k], rb[S].hi[k]);
-      g = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a_operand(a1), B, g, 4, 0, 0, int(c1), 0, int(cb));
-      u = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a_operand(a3), B, u, 4, 0, 0, int(c3), 0, int(cb));
+      const BStep B = b_step(rb[S].lo[k], rb[S].hi[k], (rb[S].sc >> (8u * k)) & 0xffu);
+      g = mfma_step(a1, c1, B, g);
+      u = mfma_step(a3, c3, B, u);
     }
     if (refill) load_bchunk(rb[S], xt, xts, c + kRing, tb, sbb);
     // keep the refill here: left free, the scheduler sinks loads to the end
@@ -560,8 +591,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     uint32_t word = 0;
 #pragma unroll
     for (int v = 0; v < 4; ++v) word |= e4m3_rne_sat(__fmul_rn(hv[4 * q4 + v], inv)) << (8 * v);
-    const uint32_t r0 = 8u * q4 + 4u * h;  // first of 4 consecutive rows (k of the group)
-    const uint32_t pos = r0 < 16u ? 16u * blk + r0 : 32u + 16u * blk + (r0 - 16u);  // MFMA order in the step
+    const uint32_t pos = 32u * blk + 8u * q4 + 4u * h;  // k in the step of the first of 4 consecutive rows
     *reinterpret_cast<uint32_t *>(tile + 1024u * ((pos >> 4) & 1u) + 16u * (col + 32u * (pos >> 5)) + (pos & 15u)) =
         word;
   }
@@ -609,7 +639,7 @@ __global__ __launch_bounds__(256) void k_requant_h128(PrefillWorkspace ws) {
     w[i] = e4m3_rne_sat(__fmul_rn(q[i].x, inv)) | (e4m3_rne_sat(__fmul_rn(q[i].y, inv)) << 8) |
            (e4m3_rne_sat(__fmul_rn(q[i].z, inv)) << 16) | (e4m3_rne_sat(__fmul_rn(q[i].w, inv)) << 24);
   const uint32_t rt = 4u * m + j / 2u, s2 = rt >> 1, blk = rt & 1u;
-  const uint32_t pos = (j & 1u) == 0u ? 16u * blk : 32u + 16u * blk;  // MFMA order of the piece in its step
+  const uint32_t pos = 32u * blk + 16u * (j & 1u);  // k in the step of the piece's first row
   uint8_t *tile = ws.ht + size_t(item) * kHTileBytes;
   *reinterpret_cast<uint4 *>(tile + 2048u * s2 + 1024u * ((pos >> 4) & 1u) + 16u * (col + 32u * (pos >> 5))) =
       make_uint4(w[0], w[1], w[2], w[3]);
@@ -689,15 +719,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     for (uint32_t k = 0; k < kChunkSteps; ++k) {
       const uint32_t p = 2u * k + h;
       const uint32_t sb = 2u * (c * kChunkSteps + k) + h;
-      const uint32_t cb = (rb[S].sc >> (8u * k)) & 0xffu;
-      const v8i B = b_operand(rb[S].lo[k], rb[S].hi[k]);
+      const BStep B = b_step(rb[S].lo[k], rb[S].hi[k], (rb[S].sc >> (8u * k)) & 0xffu);
 #pragma unroll
       for (int tl = 0; tl < NT; ++tl) {
         const uint32_t r = 32u * uint32_t(tl) + col;
         const uint4 aw = *reinterpret_cast<const uint4 *>(src + 128u * r + 16u * (p ^ sw[tl]));
         const uint32_t ca = dn_scales[64u * r + 16u * ((sb >> 4) ^ s4[tl]) + (sb & 15u)];
-        d[tl] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a_operand(aw), B, d[tl], 4, 0, 0, int(ca), 0,
-                                                                int(cb));
+        d[tl] = mfma_step(aw, ca, B, d[tl]);
       }
     }
     if (refill) load_bchunk(rb[S], ht, hts, c + kRing, tb, sbb);

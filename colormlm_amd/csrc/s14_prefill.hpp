@@ -23,10 +23,11 @@ struct PrefillItem {
 
 // Item tiles: the activation operand (B) of one work item laid out so each
 // K step is two coalesced 1 KiB loads: tile[step][part][lane][16 bytes],
-// lane = column + 32 h holding bytes 32 h + 16 part .. +15 of the column's
-// 64-byte step block in MFMA order (columns past the item's count are
-// neither written nor read).  Scales: [chunk of kChunkSteps steps][lane] u32, byte k = the E8M0
-// of step kChunkSteps * chunk + k for the lane's half.
+// lane = column + 32 h holding the e4m3 codes of k 32 h + 16 part .. +15 of
+// the step for its column, one E8M0 block per lane (columns past the item's
+// count are neither written nor read).  Scales: [chunk of kChunkSteps
+// steps][lane] u32, byte k = the E8M0 of step kChunkSteps * chunk + k for
+// the lane's half.
 constexpr uint32_t kChunkSteps = 4;
 constexpr uint32_t kXTileBytes = (kHidden / 64) * 2048;                      // phase 1: 128 KiB
 constexpr uint32_t kXScaleBytes = (kHidden / 64 / kChunkSteps) * 64 * 4;     // 4 KiB
@@ -65,7 +66,7 @@ struct PrefillWorkspace {
   uint32_t *stats;        // {items, distinct routed experts, max tokens per expert, pairs}
   uint32_t *pair_token;   // [7T]
   uint32_t *token_pair;   // [T][kSlots]
-  uint8_t *xq;            // [T][4096] e4m3, MFMA order per 64-k step
+  uint8_t *xq;            // [T][4096] e4m3
   uint8_t *xs;            // [T][128] E8M0
   uint8_t *xt;            // [items][kXTileBytes] x of each item's pairs, item tile
   uint8_t *xts;           // [items][kXScaleBytes]

@@ -476,8 +476,8 @@ def last_prefill_stats(ctx: Context) -> dict:
 
 def last_prefill_view(ctx: Context) -> dict:
     """Host copies of the last prefill's intermediates (synchronises): xq/xs
-    and hq/hs in MFMA step order, down [pairs, 4096], pair_token and
-    token_pair [tokens, 7]."""
+    and, per pair, hq/hs (codes and E8M0 scales of the requantised SwiGLU
+    output), down [pairs, 4096], pair_token and token_pair [tokens, 7]."""
     import torch
 
     v = N.PrefillView()
@@ -498,7 +498,7 @@ def last_prefill_view(ctx: Context) -> dict:
     hq = np.zeros((P, N.INTER), np.uint8)
     hs = np.zeros((P, N.INTER // 32), np.uint8)
     for i, (_, first, count) in enumerate(items.tolist()):
-        # pair first + col, step s: 64 bytes ordered [h][part][b]
+        # pair first + col, step s: value 32 h + 16 part + b
         blk = tiles[i, :, :, :, :count].transpose(3, 0, 2, 1, 4)  # [col][s][h][part][b]
         hq[first:first + count] = blk.reshape(count, N.INTER)
         sc = tscales[i, :, :, :count].transpose(2, 0, 3, 1)  # [col][c][k][h] -> group 2 (4c + k) + h

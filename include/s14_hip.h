@@ -349,15 +349,14 @@ int s14_last_prefill_stats(s14_ctx *ctx, uint32_t *distinct, uint32_t *max_token
  * (valid until the next prefill on it), for stage-by-stage verification.
  * No counterpart in the reference, whose GPU code has no prefill.
  *   xq [tokens][4096] e4m3 and xs [tokens][128] E8M0: the requantised
- *     activations; within each 64-value step the bytes are ordered
- *     k 0-15, 32-47, 16-31, 48-63 (the MFMA operand order);
+ *     activations;
  *   ht, hts: the SwiGLU output of each (token, expert) pair, requantised
  *     the same way, in work-item tiles: item i's tile is 65536 bytes at
  *     ht + 65536 i, byte (s, part, lane, b) at 2048 s + 1024 part +
- *     16 lane + b holding byte 32 h + 16 part + b of step s of the pair
- *     first_i + (lane % 32), h = lane / 32; its scales are 2048 bytes at
- *     hts + 2048 i, u32 [s / 4][lane] with byte s % 4 = the E8M0 of step s,
- *     half h;
+ *     16 lane + b holding the code of h value 64 s + 32 (lane / 32) +
+ *     16 part + b of the pair first_i + (lane % 32); its scales are 2048
+ *     bytes at hts + 2048 i, u32 [s / 4][lane] with byte s % 4 = the E8M0
+ *     of h values 64 s + 32 (lane / 32) .. +31;
  *   down [n_pairs][4096] f32: each pair's w2 output, route weight not applied;
  *   pair_token [n_pairs]: the token of each pair; token_pair [tokens][7]:
  *     each token's pairs in route order, the shared expert's last;
