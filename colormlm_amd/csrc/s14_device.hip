@@ -1016,6 +1016,52 @@ __device__ __forceinline__ void phase2_accumulate(const SlotInfo &si, const floa
 // LDS (row stride padded so the two slots' reads fall in different banks).
 constexpr int kHStride = kInter + 8;
 
+// Official mode: the w2 input's act_quant (group 128, l42_reference.py:390-403)
+// of every pair's h, in place, once per launch, between phase 1 and phase
+// 2 (each phase-2 workgroup requantising its own copies of its slots' h
+// took phase 2 from 12.5 to 26 us at K=1).  Eight lanes per (pair, 128
+// values), each lane one 16-value phase-1 tile: the group's maximum by xor
+// shuffles within the eight (a NaN never compares greater, as in the
+// oracle's scan), and the tile's exponent range into hwin, which gives
+// phase 2 the decode window of the requantised h.
+constexpr uint32_t kHGroups128 = kInter / 128;
+__global__ __launch_bounds__(256) void k_requant_h_official(Workspace ws, uint32_t n_pairs) {
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t j = gid & 7u, grp = gid >> 3;  // tile j of group grp = (pair, m)
+  const uint32_t p = grp / kHGroups128, m = grp % kHGroups128;
+  if (p >= n_pairs) return;  // whole groups of eight lanes return together
+  float4 *v = reinterpret_cast<float4 *>(ws.h + size_t(p) * kInter + 128u * m + 16u * j);
+  float4 q[4];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    q[i] = v[i];
+    amax = fabsf(q[i].x) > amax ? fabsf(q[i].x) : amax;
+    amax = fabsf(q[i].y) > amax ? fabsf(q[i].y) : amax;
+    amax = fabsf(q[i].z) > amax ? fabsf(q[i].z) : amax;
+    amax = fabsf(q[i].w) > amax ? fabsf(q[i].w) : amax;
+  }
+#pragma unroll
+  for (int d = 1; d < 8; d <<= 1) {
+    const float o = __shfl_xor(amax, d);
+    amax = o > amax ? o : amax;
+  }
+  const uint32_t code = requant_code(amax);
+  const float inv = __uint_as_float((254u - code) << 23), sc = __uint_as_float(code << 23);
+  auto rq = [&](float a) { return __fmul_rn(e4m3_f32(s14x::e4m3_rne_sat(__fmul_rn(a, inv))), sc); };
+  int lo = 255, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    q[i] = make_float4(rq(q[i].x), rq(q[i].y), rq(q[i].z), rq(q[i].w));
+    exp_range_acc(q[i].x, lo, hi);
+    exp_range_acc(q[i].y, lo, hi);
+    exp_range_acc(q[i].z, lo, hi);
+    exp_range_acc(q[i].w, lo, hi);
+    v[i] = q[i];
+  }
+  ws.hwin[size_t(p) * kP1Tiles + 8u * m + j] = uint32_t(lo) | (uint32_t(hi) << 16);
+}
+
 template <int kTier, bool kOfficial>
 __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairTable *__restrict__ tab,
                                                                      const float *__restrict__ H,
@@ -1061,24 +1107,16 @@ __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairT
     const float *const srch[2] = {H + size_t(pa) * kInter, H + size_t(pb) * kInter};
     StageRegs<kInter, 2> hr;
     stage_load_wave<kInter, 2>(hr, srch);
-    if constexpr (!kOfficial) {
-      win[0] = h_window(hwin + size_t(pa) * kP1Tiles);
-      win[1] = h_window(hwin + size_t(pb) * kP1Tiles);
-    }
+    win[0] = h_window(hwin + size_t(pa) * kP1Tiles);
+    win[1] = h_window(hwin + size_t(pb) * kP1Tiles);
     stage_store_wave<kInter, 2>(dst, hr);
-    if constexpr (kOfficial) {
-      // act_quant of each slot's h before w2 (this wavefront's own copies)
-      win[0] = requant128_wave(hs[sa], kInter);
-      win[1] = requant128_wave(hs[sb], kInter);
-    }
   } else if (has_a) {
     float *const dst[1] = {hs[sa]};
     const float *const srch[1] = {H + size_t(pa) * kInter};
     StageRegs<kInter, 1> hr;
     stage_load_wave<kInter, 1>(hr, srch);
-    if constexpr (!kOfficial) win[0] = win[1] = h_window(hwin + size_t(pa) * kP1Tiles);
+    win[0] = win[1] = h_window(hwin + size_t(pa) * kP1Tiles);
     stage_store_wave<kInter, 1>(dst, hr);
-    if constexpr (kOfficial) win[0] = win[1] = requant128_wave(hs[sa], kInter);
   }
   __syncthreads();
   if (has_a) {
@@ -1365,10 +1403,13 @@ void phase1_launch(hipStream_t s, const Workspace &ws, const PairTable &plan, co
   } else {
     const dim3 grid(kInter / (kP1ExactRows * kP1ExactWaves), n_pairs);
     const dim3 blk(64 * kP1ExactWaves);
-    if (mode == S14_MODE_OFFICIAL)
-      hipExtLaunchKernelGGL(k_phase1_exact<kSrc, kTier, true>, grid, blk, 0, s, ev.start, ev.stop, 0, plan, rs, ws, x,
+    if (mode == S14_MODE_OFFICIAL) {
+      // the phase-1 stage includes the h requant that follows it
+      hipExtLaunchKernelGGL(k_phase1_exact<kSrc, kTier, true>, grid, blk, 0, s, ev.start, nullptr, 0, plan, rs, ws, x,
                             mx, fp8);
-    else
+      hipExtLaunchKernelGGL(k_requant_h_official, dim3((n_pairs * kHGroups128 * 8u + 255u) / 256u), dim3(256), 0, s,
+                            nullptr, ev.stop, 0, ws, n_pairs);
+    } else
       hipExtLaunchKernelGGL(k_phase1_exact<kSrc, kTier, false>, grid, blk, 0, s, ev.start, ev.stop, 0, plan, rs, ws,
                             x, mx, fp8);
   }

@@ -755,8 +755,11 @@ __device__ __forceinline__ void requant128_groups(float *v, int n_groups, int fi
   for (int g = first; g < n_groups; g += stride) {
     float2 *p = reinterpret_cast<float2 *>(v + 128 * g) + lane;
     const float2 a = *p;
-    // amax over the group (NaN ignored, as the oracle's strict '>' scan does)
-    const float m = fmaxf(fabsf(a.x), fabsf(a.y));
+    // amax over the group (NaN ignored, as the oracle's strict '>' scan does:
+    // a lane whose two values are NaN contributes 0)
+    float m = 0.0f;
+    m = fabsf(a.x) > m ? fabsf(a.x) : m;
+    m = fabsf(a.y) > m ? fabsf(a.y) : m;
     const float amax = __uint_as_float(uint32_t(wave_max_i(int(__float_as_uint(m)))));  // m >= 0: bits order as values
     const uint32_t code = requant_code(amax);
     const float inv = __uint_as_float((254u - code) << 23), sc = __uint_as_float(code << 23);
@@ -766,12 +769,6 @@ __device__ __forceinline__ void requant128_groups(float *v, int n_groups, int fi
     exp_range_acc(qa, lo, hi);
     exp_range_acc(qb, lo, hi);
   }
-}
-// A whole vector of n values (n % 128 == 0) by one wavefront.
-__device__ __forceinline__ CodeWindow requant128_wave(float *v, int n) {
-  int lo = 255, hi = 0;
-  requant128_groups(v, n / 128, 0, 1, lo, hi);
-  return mx_window(wave_min_i(lo), wave_max_i(hi));
 }
 // A whole vector by the W = NT / 64 wavefronts of a workgroup (groups
 // strided over the wavefronts), between two barriers; red: LDS scratch of
