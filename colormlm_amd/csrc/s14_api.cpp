@@ -491,7 +491,7 @@ int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, con
   if (tokens == 1) {
     // one token: the route launch only scores, and every phase-1 workgroup
     // of a routed pair selects the top-k itself (no last-arrival hand-off)
-    hipError_t e = launch_route_scores(st, ws, rs, x, ev ? ev[kStageRoute] : KernelEvents{});
+    hipError_t e = launch_route_scores(st, ws, rs, x, ev ? ev[kStageRoute] : KernelEvents{}, mode == S14_MODE_OFFICIAL);
     if (e != hipSuccess) return hip_fail(e, "router launch");
     e = launch_phase1(st, ws, nullptr, n_pairs, tokens, mx, f8, x, mode, ev ? ev[kStagePhase1] : KernelEvents{}, &rs);
     if (e != hipSuccess) return hip_fail(e, "phase 1 launch");

@@ -617,9 +617,30 @@ __device__ __forceinline__ void plan_publish(const RouteSpec &rs, PairTable *tab
 // kScoresOnly (single-token layers): the launch only scores; every phase-1
 // workgroup of a routed pair then selects the top-k itself from the scores
 // (route_pair), so no workgroup waits for a last arrival.
+//
+// kRequantX (single-token official layers): one more workgroup, past the
+// scoring ones, requantises the token's x for the official expert (group
+// 128, l42_reference.py:390-403) into ws.xq, in parallel with the scoring;
+// the official phase 1 then stages those values as the exact phase 1
+// stages x, instead of every phase-1 workgroup requantising x itself.
 constexpr uint32_t kRouteGroup = 16;
-template <bool kScoresOnly>
+constexpr uint32_t kSingleRouteWaves = 4;  // route_waves(1)
+template <bool kScoresOnly, bool kRequantX = false>
 __global__ __launch_bounds__(64 * kMaxTokens) void k_route(RouteSpec rs, Workspace ws, const float *__restrict__ X) {
+  if constexpr (kRequantX) {
+    static_assert(kScoresOnly, "the requant rides on the single-token launch");
+    if (blockIdx.x * kSingleRouteWaves >= rs.r.n_experts) {  // the requant workgroup (uniform)
+      __shared__ float xs[kHidden];
+      __shared__ int red[2 * kSingleRouteWaves];
+      const uint32_t t = blockIdx.y;
+      stage_x_block<kHidden, 64 * kSingleRouteWaves>(xs, X + size_t(t) * kHidden, red);
+      requant128_block<64 * kSingleRouteWaves>(xs, kHidden, red);  // ends with a barrier
+      float *dst = ws.xq + size_t(t) * kHidden;
+      for (uint32_t i = threadIdx.x; i < kHidden / 4; i += blockDim.x)
+        reinterpret_cast<float4 *>(dst)[i] = reinterpret_cast<const float4 *>(xs)[i];
+      return;
+    }
+  }
   __shared__ float sc[kMaxTokens][kMaxExperts];
   __shared__ float bs[kMaxTokens][kMaxExperts];
   __shared__ uint64_t pages[kMaxExperts];
@@ -834,7 +855,9 @@ __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable p
   const uint32_t row = tile * kP1ExactRows + ((lane & 31u) >> 1);
   const Rsrc r = make_rsrc(pr.page, page_bytes(pr.fmt));
   const Src1 src{r, r};
-  const float *const srcx = X + size_t(pr.token) * kHidden;
+  // official, one token: the route launch already requantised x (ws.xq)
+  constexpr bool kXq = kOfficial && kSrc == kPairFromScores;
+  const float *const srcx = (kXq ? ws.xq : X) + size_t(pr.token) * kHidden;
   float acc;
   if (pr.fmt == S14_PAGE_MXFP4) {
     const uint32_t woff = uint32_t(upper ? mx.w3 : mx.w1) + row * (kHidden / 2) + 8u * h;
@@ -846,19 +869,19 @@ __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable p
       RowCodes<kHidden / 32> rc;
       load_row_codes<kHidden / 32>(rc, src, soff);
       CodeWindow win = stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
-      if constexpr (kOfficial) win = requant128_block<64 * kP1ExactWaves>(xs, kHidden, red);
+      if constexpr (kOfficial && !kXq) win = requant128_block<64 * kP1ExactWaves>(xs, kHidden, red);
       acc = mx_row_pair_fixed<kPF, kHidden / 32>(0.0f, ba, src, woff, soff, xs + 16 * h, win, rc);
     } else {
       // blocks: per-batch code checks measured faster here
       CodeWindow win = stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
-      if constexpr (kOfficial) win = requant128_block<64 * kP1ExactWaves>(xs, kHidden, red);
+      if constexpr (kOfficial && !kXq) win = requant128_block<64 * kP1ExactWaves>(xs, kHidden, red);
       acc = mx_row_pair_fixed<kPF, kHidden / 32>(0.0f, ba, src, woff, soff, xs + 16 * h, win);
     }
   } else {
     const uint32_t woff = uint32_t(upper ? f8.w3 : f8.w1) + row * kHidden + 16u * h;
     const uint32_t soff = uint32_t(upper ? f8.s3 : f8.s1) + (row / 128) * (kHidden / 128);
     stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
-    if constexpr (kOfficial) requant128_block<64 * kP1ExactWaves>(xs, kHidden, red);
+    if constexpr (kOfficial && !kXq) requant128_block<64 * kP1ExactWaves>(xs, kHidden, red);
     acc = fp8_row_pair(0.0f, src, woff, soff, 0, kHidden / 32, xs + 16 * h);
   }
   const float other = lane_xor32(acc);
@@ -1385,10 +1408,17 @@ hipError_t launch_route(hipStream_t s, const Workspace &ws, const RouteSpec &rs,
 }
 
 hipError_t launch_route_scores(hipStream_t s, const Workspace &ws, const RouteSpec &rs, const float *x,
-                               KernelEvents ev) {
+                               KernelEvents ev, bool official) {
   const uint32_t w = route_waves(rs.tokens);
-  hipExtLaunchKernelGGL(k_route<true>, dim3((rs.r.n_experts + w - 1) / w, rs.tokens), dim3(64 * w), 0, s, ev.start,
-                        ev.stop, 0, rs, ws, x);
+  const uint32_t groups = (rs.r.n_experts + w - 1) / w;
+  if (official) {
+    if (rs.tokens != 1 || w != kSingleRouteWaves) return hipErrorInvalidValue;
+    hipExtLaunchKernelGGL(k_route<true, true>, dim3(groups + 1, rs.tokens), dim3(64 * w), 0, s, ev.start, ev.stop,
+                          0, rs, ws, x);
+  } else {
+    hipExtLaunchKernelGGL(k_route<true>, dim3(groups, rs.tokens), dim3(64 * w), 0, s, ev.start, ev.stop, 0, rs, ws,
+                          x);
+  }
   return hipGetLastError();
 }
 

@@ -93,6 +93,7 @@ struct Workspace {
   // bits) that launches leave for s14_launch_status.
   uint32_t *sync;
   float *down;  // [kMaxPairs][kHidden]: each pair's w2 output of a block launch (before its route weight)
+  float *xq;    // [kMaxTokens][kHidden]: official mode's act_quant of x (dequantised), written by the single-token route
   size_t bytes;
 };
 constexpr uint32_t kSyncLines = 1;
@@ -105,7 +106,7 @@ enum : uint32_t { kStatusNullPage = 1u, kStatusBadRoute = 2u };
 // Layout of the workspace in one device allocation (each region 256-byte
 // aligned): table | h | scores | biased | route counters | h windows.
 struct WorkspaceLayout {
-  size_t table, h, scores, biased, count, hwin, xwin, sync, down, bytes;
+  size_t table, h, scores, biased, count, hwin, xwin, sync, down, xq, bytes;
 };
 constexpr size_t ws_align(size_t v) { return (v + 255) / 256 * 256; }
 constexpr WorkspaceLayout workspace_layout() {
@@ -129,6 +130,8 @@ constexpr WorkspaceLayout workspace_layout() {
   off = ws_align(off + sizeof(uint32_t) * kSyncLines * kRouteCounterStride);
   l.down = off;
   off = ws_align(off + sizeof(float) * kMaxPairs * kHidden);
+  l.xq = off;
+  off = ws_align(off + sizeof(float) * kMaxTokens * kHidden);
   l.bytes = off;
   return l;
 }
@@ -149,6 +152,7 @@ inline Workspace workspace_carve(void *base) {
   ws.xwin = reinterpret_cast<uint32_t *>(b + l.xwin);
   ws.sync = reinterpret_cast<uint32_t *>(b + l.sync);
   ws.down = reinterpret_cast<float *>(b + l.down);
+  ws.xq = reinterpret_cast<float *>(b + l.xq);
   ws.bytes = l.bytes;
   return ws;
 }
@@ -219,9 +223,11 @@ hipError_t launch_route(hipStream_t s, const Workspace &ws, const RouteSpec &rs,
                         KernelEvents ev = {});
 // The same launch's scoring alone (no plan, no table): for one routed
 // token, whose phase 1 plans from the scores itself (launch_phase1 with
-// `route`).
+// `route`).  official: one more workgroup writes the official act_quant of
+// x (group 128, dequantised) to ws.xq, which the official phase 1 stages
+// instead of requantising x in every workgroup.
 hipError_t launch_route_scores(hipStream_t s, const Workspace &ws, const RouteSpec &rs, const float *x,
-                               KernelEvents ev = {});
+                               KernelEvents ev = {}, bool official = false);
 // w1/w3 + SwiGLU of every pair.  host_plan != NULL: the pairs are given and
 // workgroup (0,0) publishes them for phase 2; route != NULL (one token):
 // every workgroup of a routed pair selects the top-k from the scores of

@@ -291,7 +291,7 @@ int s14_last_block_distinct(s14_ctx *ctx, uint32_t *n_distinct);
  * bit-identical results) for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  It calls no hipMalloc/hipFree: its workspace is a static
- * device array of s14_noalloc_scratch_bytes() bytes (about 1.4 MB) per GPU,
+ * device array of s14_noalloc_scratch_bytes() bytes (about 1.6 MB) per GPU,
  * held until the process ends, whose device address the first call on each
  * GPU looks up (hipGetSymbolAddress) with that GPU current.  The limit is
  * the block size: tokens > S14_MAX_BLOCK_TOKENS is S14_ERR_SHAPE.  Launches
