@@ -595,6 +595,122 @@ __global__ __launch_bounds__(64) void k_linear_fast(LinearArgs a, LinearWorkspac
   }
 }
 
+// FAST for one or two tokens (up to four where n is small) and k a multiple
+// of 1,024: a VALU GEMV,
+// where the MFMA path would spend 32-token tiles on one token.  One
+// wavefront per R rows, R = 8 / (k / 1,024) (at least 1), so that a
+// wavefront's eight coalesced 1 KiB code loads (R rows x its k / 1,024
+// chunks) are all in flight at once and every projection shape gets ~4,096
+// wavefronts, four per SIMD; a longer k takes its chunks in batches of
+// eight, the next batch in flight during this one.  In chunk c (1,024 k)
+// lane l holds k 1024 c + 16 l .. + 15, which lie in group 8 c + l / 8.
+// e4m3 x e4m3 products are exact in f32; each lane sums its 16 per (row,
+// token) by fused multiply-adds, scales the sum by the group's two scales
+// and accumulates; the wavefront sum (DPP) gives the row.  (Splitting k
+// across wavefronts instead, with the split partials met as k_linear_fast
+// meets them, was slower at wo_a and wo_b: 13.3 and 14.9 us.)
+constexpr uint32_t kGvChunk = 1024, kGvLoads = 8, kGvWaves = 4;
+template <int MT, int R, bool kXsF32, bool kWsF32>
+__global__ __launch_bounds__(64 * kGvWaves) void k_linear_gemv(LinearArgs a) {
+  constexpr uint32_t kB = kGvLoads / uint32_t(R);  // chunks per batch
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t r0 = (blockIdx.x * kGvWaves + (threadIdx.x >> 6)) * uint32_t(R);
+  const uint32_t K = a.k, N = a.n, M = a.m, G = a.groups;
+  if (r0 >= N) return;  // whole wavefronts
+  const uint32_t chunks = K / kGvChunk;
+  const Rsrc rw = make_rsrc(a.w, N * K);
+  const Rsrc rx = make_rsrc(a.x, M * K);
+  const uint32_t n_sw = (N + 127u) / 128u * G, n_sx = M * G;
+  const Rsrc rsw = make_rsrc(a.w_scale, kWsF32 ? 4u * n_sw : n_sw);
+  const Rsrc rsx = make_rsrc(a.x_scale, kXsF32 ? 4u * n_sx : n_sx);
+  const uint32_t sbrow = (r0 / 128u) * G;  // the R rows share a 128-row scale block
+  uint32_t woff[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) woff[r] = min(r0 + uint32_t(r), N - 1u) * K + 16u * lane;  // rows past n: unused
+  float acc[R][MT];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[r][t] = 0.0f;
+  uint4 cur[kB][R], nxt[kB][R];
+  auto load = [&](uint4 (&dst)[kB][R], uint32_t c0) {
+#pragma unroll
+    for (uint32_t b = 0; b < kB; ++b)
+#pragma unroll
+      for (int r = 0; r < R; ++r) dst[b][r] = ld16(rw, woff[r] + min(c0 + b, chunks - 1u) * kGvChunk);
+  };
+  load(cur, 0);
+#pragma unroll 1
+  for (uint32_t c0 = 0; c0 < chunks; c0 += kB) {
+    if (c0 + kB < chunks) load(nxt, c0 + kB);
+#pragma unroll
+    for (uint32_t b = 0; b < kB; ++b) {
+      const uint32_t c = c0 + b;
+      if (c >= chunks) break;  // uniform (a shorter last batch)
+      const uint32_t g = c * (kGvChunk / kLinGroup) + lane / 8u;  // this lane's group
+      const float sb = kWsF32 ? ldf(rsw, 4u * (sbrow + g)) : ue8m0_f32(ld1(rsw, sbrow + g));
+      float xv[MT][16], s[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const uint32_t tt = min(uint32_t(t), M - 1u);  // tokens past m: unused
+        const uint4 q = ld16(rx, tt * K + c * kGvChunk + 16u * lane);
+        const float sa = kXsF32 ? ldf(rsx, 4u * (tt * G + g)) : ue8m0_f32(ld1(rsx, tt * G + g));
+        s[t] = sa * sb;
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const auto lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(qw[j], 1.0f, false);
+          const auto hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(qw[j], 1.0f, true);
+          xv[t][4 * j] = lo[0];
+          xv[t][4 * j + 1] = lo[1];
+          xv[t][4 * j + 2] = hi[0];
+          xv[t][4 * j + 3] = hi[1];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t ww[4] = {cur[b][r].x, cur[b][r].y, cur[b][r].z, cur[b][r].w};
+        float wf[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const auto lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(ww[j], 1.0f, false);
+          const auto hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(ww[j], 1.0f, true);
+          wf[4 * j] = lo[0];
+          wf[4 * j + 1] = lo[1];
+          wf[4 * j + 2] = hi[0];
+          wf[4 * j + 3] = hi[1];
+        }
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          float p = 0.0f;
+#pragma unroll
+          for (int j = 0; j < 16; ++j) p = fmaf(xv[t][j], wf[j], p);
+          acc[r][t] = fmaf(p, s[t], acc[r][t]);
+        }
+      }
+    }
+#pragma unroll
+    for (uint32_t b = 0; b < kB; ++b)
+#pragma unroll
+      for (int r = 0; r < R; ++r) cur[b][r] = nxt[b][r];
+  }
+  // every lane gets every (row, token) total; lane r MT + t writes (r, t)
+  float mine = 0.0f;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const float v = wave_sum_dpp(acc[r][t]);
+      mine = lane == uint32_t(r * MT + t) ? v : mine;
+    }
+  const uint32_t orow = r0 + lane / uint32_t(MT), otok = lane % uint32_t(MT);
+  if (lane >= uint32_t(R * MT) || orow >= N || otok >= M) return;
+  float v = mine;
+  if (a.bias) v += a.bias[orow];
+  if (a.round_bf16) v = bf16_round(v);
+  a.y[size_t(otok) * N + orow] = v;
+}
+
 }  // namespace
 
 hipError_t launch_act_quant(hipStream_t s, uint32_t rows, uint32_t k, uint32_t group, const float *x, uint8_t *q,
@@ -684,7 +800,46 @@ static hipError_t launch_exact_tiled(hipStream_t s, const LinearArgs &a, const L
   return hipSuccess;
 }
 
+template <int MT, int R>
+static void launch_gemv(hipStream_t s, const LinearArgs &a) {
+  const uint32_t waves = (a.n + R - 1) / R;
+  const dim3 grid((waves + kGvWaves - 1) / kGvWaves);
+  if (a.x_scale_f32 && a.w_scale_f32)
+    k_linear_gemv<MT, R, true, true><<<grid, 64 * kGvWaves, 0, s>>>(a);
+  else if (a.x_scale_f32)
+    k_linear_gemv<MT, R, true, false><<<grid, 64 * kGvWaves, 0, s>>>(a);
+  else if (a.w_scale_f32)
+    k_linear_gemv<MT, R, false, true><<<grid, 64 * kGvWaves, 0, s>>>(a);
+  else
+    k_linear_gemv<MT, R, false, false><<<grid, 64 * kGvWaves, 0, s>>>(a);
+}
+template <int MT>
+static void launch_gemv_mt(hipStream_t s, const LinearArgs &a) {
+  const uint32_t chunks = a.k / kGvChunk;
+  if (chunks == 1)
+    launch_gemv<MT, 8>(s, a);
+  else if (chunks == 2)
+    launch_gemv<MT, 4>(s, a);
+  else if (chunks <= 4)
+    launch_gemv<MT, 2>(s, a);
+  else
+    launch_gemv<MT, 1>(s, a);
+}
+
 hipError_t launch_fp8_linear(hipStream_t s, const LinearArgs &a, int mode, const LinearWorkspace &ws) {
+  // the GEMV where it measured faster than the MFMA tiles (graph replays,
+  // us: wq_b m = 1 8.5 against 10.4, m = 2 10.9 against 10.7; wo_a m = 2 11.2
+  // against 12.6, m = 3 14.7 against 13.1; wkv m = 4 4.9 against 7.9)
+  const bool gemv = a.m == 1u || (a.m == 2u && a.n <= 8192u) || (a.m <= 4u && a.n <= 1024u);
+  if (mode == S14_MODE_FAST && gemv && a.k % kGvChunk == 0u && uint64_t(a.n) * a.k <= 0xFFFFFFFFull) {
+    if (a.m == 1)
+      launch_gemv_mt<1>(s, a);
+    else if (a.m == 2)
+      launch_gemv_mt<2>(s, a);
+    else
+      launch_gemv_mt<4>(s, a);
+    return hipGetLastError();
+  }
   const bool fast = mode == S14_MODE_FAST && a.k % (4u * kLinGroup) == 0u;
   const LinFastPlan plan = fast ? lin_fast_plan(a.m, a.n, a.groups) : LinFastPlan{0, 0};
   if (plan.cw) {

@@ -158,11 +158,14 @@ def test_fp8_linear_f32_scales_bias_bf16(ctx, oracle):
     check_fast(oracle, got, (want - b).astype(np.float64), x, xs, w, ws, "f32 scales")
 
 
-@pytest.mark.parametrize("m,n,k", [(33, 100, 1536), (1, 4000, 512), (8, 96, 16384), (2, 300, 1024), (8, 4096, 8192)])
+@pytest.mark.parametrize("m,n,k", [(33, 100, 1536), (1, 4000, 512), (8, 96, 16384), (2, 300, 1024), (8, 4096, 8192),
+                                   (3, 130, 16384), (1, 4099, 2048), (4, 1000, 4096)])
 def test_fp8_linear_fast_edges(ctx, oracle, m, n, k):
     """Row tiles cut by n, two token blocks (m = 33), 12 groups (chunks per
     wavefront 4 or 12), one group-chunk round (k = 512), k = 16384, two
-    tokens, and eight tokens at wo_b's shape."""
+    tokens, and eight tokens at wo_b's shape; for the few-token GEMV, three
+    tokens over k = 16384 (two batches of eight chunks) with rows cut by n,
+    a last four-row group cut by n, and four tokens at a short n."""
     say(f"fp8_linear fast edges m={m} n={n} k={k}")
     rng = np.random.default_rng(n)
     w, ws = codes(rng, (n, k)), rng.integers(114, 122, (-(-n // 128), k // 128), dtype=np.uint8)
