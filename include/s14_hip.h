@@ -408,9 +408,11 @@ enum { S14_LINEAR_ROUND_BF16 = 1 };
  * S14_MODE_EXACT sums each group's products k ascending (multiply, then
  * add; the reference's addmm leaves that order to the BLAS): bit-identical
  * to the CPU oracle's s14o_fp8_linear.  S14_MODE_FAST computes the group
- * dot products on the MFMA (within the reference's own 2e-5 relative
- * tolerance of it); it needs k % 512 == 0 and otherwise runs the EXACT
- * kernel.  Both modes keep partial sums in a 32 MiB context workspace
+ * dot products in another order (within the reference's own 2e-5 relative
+ * tolerance of it): for one or two tokens (up to four where n <= 1024) and
+ * k % 1024 == 0 as a VALU GEMV, otherwise on the MFMA; it needs k % 512 == 0
+ * and otherwise runs the EXACT kernel.  Both modes keep partial sums in a
+ * 32 MiB context workspace
  * (FAST: split-K partials and arrival counters; EXACT: per-group partials)
  * allocated on the first call: fp8_linear calls on one context must not
  * overlap (serialise them on one stream).
