@@ -27,6 +27,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <utility>
 
 #include "s14_device.hpp"
@@ -711,6 +712,112 @@ __global__ __launch_bounds__(64 * kGvWaves) void k_linear_gemv(LinearArgs a) {
   a.y[size_t(otok) * N + orow] = v;
 }
 
+// EXACT for one token and k of 1,024, 2,048, 4,096 or 8,192 (G = k / 128
+// groups): one launch where the tiled kernel takes two.  A wavefront owns
+// R = 64 / G rows, lane (r, g) = (lane / G, lane % G) one group of one row,
+// summed in the oracle's order (k ascending; a = dec(x) * sa, b = dec(w) *
+// sb, partial += a * b; with UE8M0 scales the scaled converter forms each
+// exactly); the row's lanes then fold their partials in group order
+// (acc = 0; acc += partial_g) and one lane adds the bias.  The wavefront's
+// R x k weight block (8 KiB) arrives by eight coalesced DMA loads into LDS,
+// x's codes once per workgroup; piece q of a group's 128 bytes sits at
+// q ^ swz (w: (swz8(g) + r) % 8, x: swz8(g)), so a read pass of 16 lanes
+// hits distinct banks.
+constexpr uint32_t kGxWaves = 4;
+__device__ __forceinline__ uint32_t gx_swz8(uint32_t g) { return (g + (g >> 3)) & 7u; }
+template <int R, bool kXsF32, bool kWsF32>
+__global__ __launch_bounds__(64 * kGxWaves) void k_linear_gemv_exact(LinearArgs a) {
+  constexpr uint32_t G = 64u / uint32_t(R), K = G * kLinGroup;
+  __shared__ __attribute__((aligned(16))) uint8_t gx_w[kGxWaves][uint32_t(R) * K];
+  __shared__ __attribute__((aligned(16))) uint8_t gx_x[K];
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
+  const uint32_t N = a.n;
+  const uint32_t r0 = (blockIdx.x * kGxWaves + wave) * uint32_t(R);
+  const Rsrc rw = make_rsrc(a.w, N * K), rx = make_rsrc(a.x, K);
+  const uint32_t n_sw = (N + 127u) / 128u * G;
+  const Rsrc rsw = make_rsrc(a.w_scale, kWsF32 ? 4u * n_sw : n_sw);
+  const Rsrc rsx = make_rsrc(a.x_scale, kXsF32 ? 4u * G : G);
+  if (r0 < N) {  // uniform per wavefront: its weight block, in flight during the x copy
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) {
+      const uint32_t r = (1024u * j) / K, u = (1024u * j) % K / 16u + lane;  // row, 16-byte unit of the row
+      const uint32_t g = u / 8u, q = (u % 8u) ^ ((gx_swz8(g) + r) & 7u);
+      const uint32_t off = min(r0 + r, N - 1u) * K + kLinGroup * g + 16u * q;  // rows past n: unused
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lt_lds_void *)(gx_w[wave] + 1024u * j), 16, off, 0, 0, 0);
+    }
+  }
+  for (uint32_t i = threadIdx.x; i < K / 16u; i += 64u * kGxWaves) {
+    const uint32_t g = i / 8u, q = i % 8u;
+    *reinterpret_cast<uint4 *>(gx_x + kLinGroup * g + 16u * (q ^ gx_swz8(g))) = ld16(rx, 16u * i);
+  }
+  __syncthreads();
+  if (r0 >= N) return;
+  const uint32_t r = lane / G, g = lane % G;
+  const uint32_t row = min(r0 + r, N - 1u);
+  const uint32_t si = (row / 128u) * G + g;
+  const uint32_t cx = kXsF32 ? 0u : ld1(rsx, g), cw = kWsF32 ? 0u : ld1(rsw, si);
+  const float sa = kXsF32 ? ldf(rsx, 4u * g) : ue8m0_f32(cx);
+  const float sb = kWsF32 ? ldf(rsw, 4u * si) : ue8m0_f32(cw);
+  // UE8M0 scales whose every a, b and a * b stays normal or zero (|dec| in
+  // [2^-9, 448]): the converters' scale operand forms a and b exactly, the
+  // same values as the separate multiplies
+  const bool scaled = !kXsF32 && !kWsF32 && cx >= 10u && cx <= 246u && cw >= 10u && cw <= 246u &&
+                      cx + cw >= 146u && cx + cw <= 364u;
+  const uint8_t *wp = gx_w[wave] + r * K + kLinGroup * g;
+  const uint8_t *xp = gx_x + kLinGroup * g;
+  const uint32_t sw = (gx_swz8(g) + r) & 7u, sx = gx_swz8(g);
+  float partial = 0.0f;
+  auto group_sum = [&](auto scaled_tag) {
+    constexpr bool kScaled = decltype(scaled_tag)::value;
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) {
+      const uint4 wq = *reinterpret_cast<const uint4 *>(wp + 16u * (j ^ sw));
+      const uint4 xq = *reinterpret_cast<const uint4 *>(xp + 16u * (j ^ sx));
+      const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w}, xw[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        float av[4], bv[4];
+        if constexpr (kScaled) {
+          const v2f xl = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(xw[d], sa, false);
+          const v2f xh = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(xw[d], sa, true);
+          const v2f wl = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(ww[d], sb, false);
+          const v2f wh = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(ww[d], sb, true);
+          av[0] = xl.x, av[1] = xl.y, av[2] = xh.x, av[3] = xh.y;
+          bv[0] = wl.x, bv[1] = wl.y, bv[2] = wh.x, bv[3] = wh.y;
+        } else {
+          const v2f xl = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(xw[d], 1.0f, false);
+          const v2f xh = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(xw[d], 1.0f, true);
+          const v2f wl = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(ww[d], 1.0f, false);
+          const v2f wh = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(ww[d], 1.0f, true);
+          av[0] = __fmul_rn(xl.x, sa), av[1] = __fmul_rn(xl.y, sa), av[2] = __fmul_rn(xh.x, sa), av[3] = __fmul_rn(xh.y, sa);
+          bv[0] = __fmul_rn(wl.x, sb), bv[1] = __fmul_rn(wl.y, sb), bv[2] = __fmul_rn(wh.x, sb), bv[3] = __fmul_rn(wh.y, sb);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) partial = __fadd_rn(partial, __fmul_rn(av[e], bv[e]));  // k ascending
+      }
+    }
+  };
+  if (scaled)
+    group_sum(std::true_type{});
+  else
+    group_sum(std::false_type{});
+  // row rr's sum in group order, the same in every lane; lane rr writes it
+  float mine = 0.0f;
+#pragma unroll
+  for (int rr = 0; rr < R; ++rr) {
+    float acc = 0.0f;
+#pragma unroll
+    for (uint32_t gg = 0; gg < G; ++gg)
+      acc = __fadd_rn(acc, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(partial), int(uint32_t(rr) * G + gg))));
+    mine = lane == uint32_t(rr) ? acc : mine;
+  }
+  if (lane >= uint32_t(R) || r0 + lane >= N) return;
+  float v = mine;
+  if (a.bias) v = __fadd_rn(v, a.bias[r0 + lane]);
+  if (a.round_bf16) v = bf16_round(v);
+  a.y[r0 + lane] = v;
+}
+
 }  // namespace
 
 hipError_t launch_act_quant(hipStream_t s, uint32_t rows, uint32_t k, uint32_t group, const float *x, uint8_t *q,
@@ -826,6 +933,20 @@ static void launch_gemv_mt(hipStream_t s, const LinearArgs &a) {
     launch_gemv<MT, 1>(s, a);
 }
 
+template <int R>
+static void launch_gemv_exact(hipStream_t s, const LinearArgs &a) {
+  const uint32_t waves = (a.n + R - 1) / R;
+  const dim3 grid((waves + kGxWaves - 1) / kGxWaves);
+  if (a.x_scale_f32 && a.w_scale_f32)
+    k_linear_gemv_exact<R, true, true><<<grid, 64 * kGxWaves, 0, s>>>(a);
+  else if (a.x_scale_f32)
+    k_linear_gemv_exact<R, true, false><<<grid, 64 * kGxWaves, 0, s>>>(a);
+  else if (a.w_scale_f32)
+    k_linear_gemv_exact<R, false, true><<<grid, 64 * kGxWaves, 0, s>>>(a);
+  else
+    k_linear_gemv_exact<R, false, false><<<grid, 64 * kGxWaves, 0, s>>>(a);
+}
+
 hipError_t launch_fp8_linear(hipStream_t s, const LinearArgs &a, int mode, const LinearWorkspace &ws) {
   // the GEMV where it measured faster than the MFMA tiles (graph replays,
   // us: wq_b m = 1 8.5 against 10.4, m = 2 10.9 against 10.7; wo_a m = 2 11.2
@@ -866,6 +987,16 @@ hipError_t launch_fp8_linear(hipStream_t s, const LinearArgs &a, int mode, const
   }
   const bool vec = a.k % 16u == 0u &&
                    ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.w)) & 15u) == 0u;
+  if (a.m == 1u && vec && uint64_t(a.n) * a.k <= 0xFFFFFFFFull &&
+      (a.k == 1024u || a.k == 2048u || a.k == 4096u || a.k == 8192u)) {
+    switch (a.k) {
+      case 1024u: launch_gemv_exact<8>(s, a); break;
+      case 2048u: launch_gemv_exact<4>(s, a); break;
+      case 4096u: launch_gemv_exact<2>(s, a); break;
+      default: launch_gemv_exact<1>(s, a); break;
+    }
+    return hipGetLastError();
+  }
   // tiled: whole groups, one token's partials within the workspace, and the
   // last tile's row offsets within 32 bits (rows past n read zeros)
   if (vec && a.k % kLinGroup == 0u && size_t(a.groups) * a.n * sizeof(float) <= kLinPartBytes &&

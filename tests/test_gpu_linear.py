@@ -136,11 +136,12 @@ def test_fp8_linear_reference_known_answer_shape(ctx, oracle):
         assert np.array_equal(host(y).view(np.uint32), want.view(np.uint32)), mode
 
 
-def test_fp8_linear_f32_scales_bias_bf16(ctx, oracle):
+@pytest.mark.parametrize("m", [1, 3])
+def test_fp8_linear_f32_scales_bias_bf16(ctx, oracle, m):
     """f32 scales (fp8.py:37-46's float form), a bias and the official bf16
-    output rounding, at wkv's shape."""
-    say("fp8_linear f32 scales + bias + bf16 output")
-    n, k, m = 512, 4096, 3
+    output rounding, at wkv's shape (one token: the single-token kernels)."""
+    say(f"fp8_linear f32 scales + bias + bf16 output, m={m}")
+    n, k = 512, 4096
     rng = np.random.default_rng(9)
     w = codes(rng, (n, k))
     ws = rng.uniform(1e-3, 4e-3, (n // 128, k // 128)).astype(np.float32)
@@ -176,6 +177,32 @@ def test_fp8_linear_fast_edges(ctx, oracle, m, n, k):
     assert np.array_equal(host(y).view(np.uint32), want.view(np.uint32))
     s14.fp8_linear(ctx, dev(x), dev(xs), dev(w), dev(ws), y, mode=s14.FAST)
     check_fast(oracle, host(y), want, x, xs, w, ws, f"m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("k", [1024, 2048, 8192])
+def test_fp8_linear_exact_one_token_extreme_scales(ctx, oracle, k):
+    """The single-token EXACT kernel at each of its four k (4,096 in the
+    shape tests) with UE8M0 codes 0..12 mixed with ordinary ones, so that
+    products fall to subnormals or zero (the kernel's separate-multiply
+    branch; the top of the code range would overflow to inf and NaN, whose
+    payloads the CPU and the GPU form differently), rows cut by n; bit for
+    bit."""
+    say(f"fp8_linear exact m=1 extreme scales k={k}")
+    n = 777
+    rng = np.random.default_rng(k)
+    w, x = codes(rng, (n, k)), codes(rng, (1, k))
+    ends = np.arange(0, 13).astype(np.uint8)
+    ws = rng.integers(118, 124, (-(-n // 128), k // 128), dtype=np.uint8)
+    xs = rng.integers(118, 124, (1, k // 128), dtype=np.uint8)
+    sel = rng.random(ws.shape) < 0.4
+    ws[sel] = rng.choice(ends, size=int(sel.sum()))
+    sel = rng.random(xs.shape) < 0.4
+    xs[sel] = rng.choice(ends, size=int(sel.sum()))
+    want = oracle.fp8_linear(x, xs, w, ws)
+    y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    s14.fp8_linear(ctx, dev(x), dev(xs), dev(w), dev(ws), y, mode=s14.EXACT)
+    got = host(y)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), np.count_nonzero(got != want)
 
 
 def test_fp8_linear_exact_token_chunks(ctx, oracle):
