@@ -326,7 +326,8 @@ int s14_route(s14_ctx *ctx, void *stream, const s14_router *router, uint32_t tok
 /* Prefill (config 4; the reference has no GPU code for it, its layer
  * semantics are s14_vulkan_numeric.rs:929-946): tokens <= 1024 through the
  * router and the top-6 routed + shared MXFP4 experts as grouped GEMMs on
- * the gfx950 scaled MFMA, activations requantised to e4m3 with per-32 E8M0
+ * the bf16 MFMA, both operands decoded exactly to bf16 by the gfx950 scaled
+ * converters (products exact, f32 sums), activations requantised to e4m3 with per-32 E8M0
  * scales 2^ceil(log2(max(amax,1e-4)/448)) (l42_reference.py:390-403 with
  * group 32) before w1/w3 and again (h) before w2.  Not order-exact: results
  * agree with the CPU oracle to a measured tolerance.  The shared page must
