@@ -491,8 +491,22 @@ __device__ __forceinline__ void rt_reduce_step(const float (&v)[2 * H], float (&
     }
   }
 }
+// kRq (1: default, 2: official): the grid's rows past the token tiles
+// requantise X into Q and S (requant_x_group, 256 groups a workgroup) beside
+// the scoring, which does not depend on them (a launch of its own took
+// ~6 us of the prefill).
+template <int kRq>
 __global__ __launch_bounds__(256) void k_router_scores(RouterArgs r, uint32_t tokens, const float *__restrict__ X,
-                                                       float *__restrict__ scores, float *__restrict__ biased) {
+                                                       float *__restrict__ scores, float *__restrict__ biased,
+                                                       uint8_t *__restrict__ Q, uint8_t *__restrict__ S) {
+  if constexpr (kRq != 0) {
+    const uint32_t tiles = (tokens + kRtT - 1) / kRtT;
+    if (blockIdx.y >= tiles) {  // uniform per workgroup
+      const uint32_t b = (blockIdx.y - tiles) * gridDim.x + blockIdx.x;
+      requant_x_group<kRq == 2>(b * 256u + threadIdx.x, tokens, X, Q, S);
+      return;
+    }
+  }
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t e0 = (blockIdx.x * 4u + wave) * kRtE, t0 = blockIdx.y * kRtT;
   if (e0 >= r.n_experts) return;
@@ -1431,9 +1445,21 @@ hipError_t launch_clear_route_counters(hipStream_t s, const Workspace &ws) {
 }
 
 hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const RouterArgs &r, uint32_t tokens,
-                                const float *x, KernelEvents ev) {
-  hipExtLaunchKernelGGL(k_router_scores, dim3((r.n_experts + 4 * kRtE - 1) / (4 * kRtE), (tokens + kRtT - 1) / kRtT),
-                        dim3(256), 0, s, ev.start, ev.stop, 0, r, tokens, x, ws.scores, ws.biased);
+                                const float *x, KernelEvents ev, int requant, uint8_t *q, uint8_t *qs) {
+  const uint32_t gx = (r.n_experts + 4 * kRtE - 1) / (4 * kRtE), tiles = (tokens + kRtT - 1) / kRtT;
+  if (requant == 0) {
+    hipExtLaunchKernelGGL(k_router_scores<0>, dim3(gx, tiles), dim3(256), 0, s, ev.start, ev.stop, 0, r, tokens, x,
+                          ws.scores, ws.biased, q, qs);
+    return hipGetLastError();
+  }
+  const uint32_t rq_blocks = (tokens * (kHidden / 32) + 255) / 256;
+  const dim3 grid(gx, tiles + (rq_blocks + gx - 1) / gx);
+  if (requant == 2)
+    hipExtLaunchKernelGGL(k_router_scores<2>, grid, dim3(256), 0, s, ev.start, ev.stop, 0, r, tokens, x, ws.scores,
+                          ws.biased, q, qs);
+  else
+    hipExtLaunchKernelGGL(k_router_scores<1>, grid, dim3(256), 0, s, ev.start, ev.stop, 0, r, tokens, x, ws.scores,
+                          ws.biased, q, qs);
   return hipGetLastError();
 }
 

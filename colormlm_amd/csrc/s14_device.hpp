@@ -213,9 +213,12 @@ hipError_t launch_clear_route_counters(hipStream_t s, const Workspace &ws);
 
 // --- fused layer / block path: route (router + plan) -> phase 1 -> phase 2 ---
 // Scores and biased scores of every (token, expert) into ws.scores/biased
-// (the prefill's router; the layer path uses launch_route).
+// (the prefill's router; the layer path uses launch_route).  requant 1 / 2:
+// the same launch also requantises x into q [tokens][4096] e4m3 and qs
+// [tokens][128] E8M0 (groups of 32 / the official groups of 128).
 hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const RouterArgs &r,
-                                uint32_t tokens, const float *x, KernelEvents ev = {});
+                                uint32_t tokens, const float *x, KernelEvents ev = {}, int requant = 0,
+                                uint8_t *q = nullptr, uint8_t *qs = nullptr);
 // Scores, then the top-k and weights of every token to rs.ids_out /
 // weights_out when given; with rs.expert_pages also the pair table in
 // ws.table.  One launch (the last workgroup plans).

@@ -124,6 +124,55 @@ __device__ __forceinline__ uint32_t requant_code(float amax) {
   return uint32_t(c + 127);
 }
 
+// The prefill's activation requant (bit-identical to the oracle's
+// s14o_requant_e4m3): X [T, 4096] f32 -> Q [T, 4096] e4m3 + S [T, 128]
+// E8M0, one thread (gid) per 32-value group.  kOfficial: the official
+// act_quant's group of 128 (l42_reference.py:390-403): the maximum over the
+// four adjacent threads of a 128-value group, whose four E8M0 bytes then
+// hold the same code (a token's 128 groups and a workgroup's 256 threads are
+// whole quads, so a quad returns early together or not at all).
+template <bool kOfficial>
+__device__ __forceinline__ void requant_x_group(uint32_t gid, uint32_t tokens, const float *__restrict__ X,
+                                                uint8_t *__restrict__ Q, uint8_t *__restrict__ S) {
+  constexpr uint32_t kGroup = 32, groups = kHidden / kGroup;
+  if (gid >= tokens * groups) return;
+  const uint32_t t = gid / groups, g = gid % groups;
+  const float4 *src = reinterpret_cast<const float4 *>(X + size_t(t) * kHidden + g * kGroup);
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 q = src[i];
+    v[4 * i] = q.x;
+    v[4 * i + 1] = q.y;
+    v[4 * i + 2] = q.z;
+    v[4 * i + 3] = q.w;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fabsf(v[i]) > amax ? fabsf(v[i]) : amax;
+  if constexpr (kOfficial) {
+    // NaN never compares greater, as in the scan above
+    const float a1 = __shfl_xor(amax, 1);
+    amax = a1 > amax ? a1 : amax;
+    const float a2 = __shfl_xor(amax, 2);
+    amax = a2 > amax ? a2 : amax;
+  }
+  const uint32_t code = requant_code(amax);
+  const float inv = __uint_as_float((254u - code) << 23);  // 2^-(code-127)
+  uint32_t w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) word |= s14x::e4m3_rne_sat(__fmul_rn(v[4 * i + j], inv)) << (8 * j);
+    w[i] = word;
+  }
+  uint8_t *dst = Q + size_t(t) * kHidden + kGroup * g;
+  *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+  *reinterpret_cast<uint4 *>(dst + 16u) = make_uint4(w[4], w[5], w[6], w[7]);
+  S[size_t(t) * groups + g] = uint8_t(code);
+}
+
 // expf's 32 table entries in LDS (see s14x::expf_glibc_with): filled by the
 // first 32 lanes of a wavefront, then a barrier before any use.
 struct LdsExpTable {

@@ -49,54 +49,9 @@ constexpr uint32_t kQGroup = 32;  // requant group (k values per E8M0 scale)
 
 using s14x::e4m3_rne_sat;  // s14_e4m3.h: straight-line, checked against the oracle on the CPU
 
-// X [T, 4096] f32 -> Q [T, 4096] e4m3 + S [T, 128] E8M0.
-// One thread per 32-value group.  kOfficial: the official act_quant's group
-// of 128 (l42_reference.py:390-403): the maximum over the four adjacent
-// threads of a 128-value group, whose four E8M0 bytes then hold the same
-// code (a token's 128 groups and a workgroup's 256 threads are whole quads,
-// so a quad returns early together or not at all).
-template <bool kOfficial>
-__global__ __launch_bounds__(256) void k_requant_x(uint32_t tokens, const float *__restrict__ X,
-                                                   uint8_t *__restrict__ Q, uint8_t *__restrict__ S) {
-  const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
-  const uint32_t groups = kHidden / kQGroup;
-  if (gid >= tokens * groups) return;
-  const uint32_t t = gid / groups, g = gid % groups;
-  const float4 *src = reinterpret_cast<const float4 *>(X + size_t(t) * kHidden + g * kQGroup);
-  float v[32];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 q = src[i];
-    v[4 * i] = q.x;
-    v[4 * i + 1] = q.y;
-    v[4 * i + 2] = q.z;
-    v[4 * i + 3] = q.w;
-  }
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) amax = fabsf(v[i]) > amax ? fabsf(v[i]) : amax;
-  if constexpr (kOfficial) {
-    // NaN never compares greater, as in the scan above
-    const float a1 = __shfl_xor(amax, 1);
-    amax = a1 > amax ? a1 : amax;
-    const float a2 = __shfl_xor(amax, 2);
-    amax = a2 > amax ? a2 : amax;
-  }
-  const uint32_t code = requant_code(amax);
-  const float inv = __uint_as_float((254u - code) << 23);  // 2^-(code-127)
-  uint32_t w[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) word |= e4m3_rne_sat(__fmul_rn(v[4 * i + j], inv)) << (8 * j);
-    w[i] = word;
-  }
-  uint8_t *dst = Q + size_t(t) * kHidden + kQGroup * g;
-  *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
-  *reinterpret_cast<uint4 *>(dst + 16u) = make_uint4(w[4], w[5], w[6], w[7]);
-  S[size_t(t) * groups + g] = uint8_t(code);
-}
+// The activation requant X [T, 4096] f32 -> Q [T, 4096] e4m3 + S [T, 128]
+// E8M0 (requant_x_group) runs in extra workgroups of the router's launch
+// (launch_router_scores), beside the scoring it does not depend on.
 
 // ---------------------------------------------------------------------------
 // routing and grouping
@@ -813,15 +768,10 @@ hipError_t launch_prefill(hipStream_t s, const PrefillArgs &a, const PrefillWork
   Workspace rws{};
   rws.scores = ws.scores;
   rws.biased = ws.biased;
-  hipError_t e = launch_router_scores(s, rws, a.r, T, a.x);
+  hipError_t e = launch_router_scores(s, rws, a.r, T, a.x, {}, a.official ? 2 : 1, ws.xq, ws.xs);
   if (e != hipSuccess) return e;
   k_prefill_topk<<<(T + 3) / 4, 256, 0, s>>>(a, ws);
   k_prefill_group<<<1, 1024, 0, s>>>(a, ws);
-  const uint32_t rq_blocks = (T * (kHidden / kQGroup) + 255) / 256;
-  if (a.official)
-    k_requant_x<true><<<rq_blocks, 256, 0, s>>>(T, a.x, ws.xq, ws.xs);
-  else
-    k_requant_x<false><<<rq_blocks, 256, 0, s>>>(T, a.x, ws.xq, ws.xs);
   const uint32_t max_items = prefill_max_items(T);
   k_tile_x<<<max_items * (kXTileBytes / 16 / 256), 256, 0, s>>>(ws);
   const uint32_t cb_blocks = (T * (kHidden / 4) + 255) / 256;
