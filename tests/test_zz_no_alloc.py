@@ -1,7 +1,7 @@
 """The no-allocation entry point (s14_moe_block_route_noalloc) against the
 context entry point it varies (s14_moe_block_route): same inputs, outputs,
 routes and weights bit for bit, on two calls in a row, the second with a
-smaller block, in both modes."""
+smaller block, in each mode (EXACT, FAST, official)."""
 
 from __future__ import annotations
 
@@ -48,7 +48,7 @@ def setup():
     ctx.destroy()
 
 
-@pytest.mark.parametrize("mode", [s14.EXACT, s14.FAST])
+@pytest.mark.parametrize("mode", [s14.EXACT, s14.FAST, s14.OFFICIAL])
 def test_noalloc_matches_context_entry(setup, mode):
     ctx, pages, table, router = setup
     assert N.lib().s14_noalloc_scratch_bytes() > 0
