@@ -499,9 +499,11 @@ int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, con
     if (e != hipSuccess) return hip_fail(e, "phase 2 launch");
     return S14_OK;
   }
-  hipError_t e = launch_route(st, ws, rs, x, ev ? ev[kStageRoute] : KernelEvents{});
+  const bool official = mode == S14_MODE_OFFICIAL;
+  // official: the route launch also writes x's act_quant for phase 1
+  hipError_t e = launch_route(st, ws, rs, x, ev ? ev[kStageRoute] : KernelEvents{}, official);
   if (e != hipSuccess) return hip_fail(e, "router launch");
-  if (tokens > 1 && mode == S14_MODE_EXACT) {
+  if (tokens > 1 && (mode == S14_MODE_EXACT || official)) {
     // blocks: one row per lane (enough (token, expert) chains to fill the
     // GPU).  With a side stream the pairs run as two halves, one per stream,
     // so that the SIMDs one half's phase-1 tail leaves idle (3.5 equal
@@ -514,13 +516,13 @@ int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, con
       if ((e = hipStreamWaitEvent(fork->side, fork->fork, 0)) != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
     }
     const char *failed = nullptr;
-    e = launch_block_phase1(st, ws, 0, na, mx, f8, x, ev ? ev[kStagePhase1] : KernelEvents{});
-    if (e == hipSuccess && nb) e = launch_block_phase1(fork->side, ws, na, nb, mx, f8, x);
+    e = launch_block_phase1(st, ws, 0, na, mx, f8, x, official, ev ? ev[kStagePhase1] : KernelEvents{});
+    if (e == hipSuccess && nb) e = launch_block_phase1(fork->side, ws, na, nb, mx, f8, x, official);
     if (e != hipSuccess) {
       failed = "phase 1 launch";
     } else {
-      e = launch_block_phase2(st, ws, 0, na, mx, f8, ev ? ev[kStagePhase2].start : nullptr);
-      if (e == hipSuccess && nb) e = launch_block_phase2(fork->side, ws, na, nb, mx, f8);
+      e = launch_block_phase2(st, ws, 0, na, mx, f8, official, ev ? ev[kStagePhase2].start : nullptr);
+      if (e == hipSuccess && nb) e = launch_block_phase2(fork->side, ws, na, nb, mx, f8, official);
       if (e != hipSuccess) failed = "phase 2 launch";
     }
     if (fork) {
@@ -535,7 +537,7 @@ int block_route_launch(hipStream_t st, const Workspace &ws, uint32_t tokens, con
       }
     }
     if (failed) return hip_fail(e, failed);
-    e = launch_block_combine(st, ws, tokens, y, ev ? ev[kStagePhase2].stop : nullptr);
+    e = launch_block_combine(st, ws, tokens, y, official, ev ? ev[kStagePhase2].stop : nullptr);
     if (e != hipSuccess) return hip_fail(e, "combine launch");
     return S14_OK;
   }

@@ -1,5 +1,8 @@
 // EXACT row engine for blocks of 2..8 tokens (the K <= 8 speculative-verify
-// block): one output row per lane.
+// block): one output row per lane.  The same kernels, instantiated with
+// kOfficial, run official blocks (the official expert semantics: the route
+// launch's act_quant of x, bf16 roundings, the route weight before w2, h's
+// act_quant at the end of phase 1).
 //
 // The reference CPU oracle's order is a dependent chain of adds per (row,
 // token): acc += (x_k * e2m1(w_k)) * s, k ascending
@@ -282,6 +285,14 @@ __device__ __forceinline__ void b_decode_id(uint32_t n_pairs, uint32_t p0, uint3
 
 // Phase 1: workgroup -> (pair, 128 rows of h), wavefront -> 32 rows of w1
 // (lanes 0-31) and the same rows of w3 (lanes 32-63); h = swiglu(g, u).
+// kOfficial (the official expert semantics, executor.py:705-731): x is the
+// route launch's act_quant of x (ws.xq, with its window in ws.xwin); g and
+// u are rounded to bf16, h = bf16(swiglu(g, u) * w) with w the pair's route
+// weight; then h's act_quant for w2 (group 128, l42_reference.py:390-403):
+// the workgroup's 128 rows are exactly one group, so the group's maximum is
+// one exchange through LDS and no separate requant launch is needed.
+static_assert(kBWaves * 32 == 128, "a phase-1 workgroup's rows are one act_quant group of h");
+template <bool kOfficial>
 __global__ __launch_bounds__(64 * kBWaves) void k_block_phase1(const PairTable *__restrict__ tab, Workspace ws,
                                                                const float *__restrict__ X, uint32_t p0,
                                                                uint32_t n_pairs, PageOffsets mx, PageOffsets f8) {
@@ -293,7 +304,7 @@ __global__ __launch_bounds__(64 * kBWaves) void k_block_phase1(const PairTable *
   const uint32_t xw_all = ws.xwin[lane & uint32_t(kMaxTokens - 1)];
   const uint8_t *page = reinterpret_cast<const uint8_t *>(tab->page[p]);
   const uint32_t fmt = tab->fmt[p], t = tab->token[p];
-  const float *x = X + size_t(t) * kHidden;
+  const float *x = (kOfficial ? ws.xq : X) + size_t(t) * kHidden;
   const uint32_t tile = q * kBWaves + wave;  // 32-row tile of h
   const uint32_t row0 = tile * 32u;
   const bool upper = lane >= 32;
@@ -321,7 +332,27 @@ __global__ __launch_bounds__(64 * kBWaves) void k_block_phase1(const PairTable *
   }
   const float u = lane_xor32(acc);
   int lo = 255, hi = 0;
-  if (!upper) {
+  if constexpr (kOfficial) {
+    __shared__ int b_amax[kBWaves];
+    float hv = 0.0f, m = 0.0f;
+    if (!upper) {
+      hv = bf16_round(__fmul_rn(swiglu_exact(bf16_round(acc), bf16_round(u)), tab->weight[p]));
+      m = fabsf(hv) > m ? fabsf(hv) : m;  // a NaN never compares greater, as in the oracle's scan
+    }
+    const int mw = wave_max_i(int(__float_as_uint(m)));  // m >= 0: bits order as values
+    if (lane == 0) b_amax[wave] = mw;
+    __syncthreads();
+    int mb = b_amax[0];
+#pragma unroll
+    for (int w = 1; w < kBWaves; ++w) mb = max(mb, b_amax[w]);
+    const uint32_t code = requant_code(__uint_as_float(uint32_t(mb)));
+    const float inv = __uint_as_float((254u - code) << 23), sc = __uint_as_float(code << 23);
+    if (!upper) {
+      const float q = __fmul_rn(e4m3_f32(s14x::e4m3_rne_sat(__fmul_rn(hv, inv))), sc);
+      ws.h[size_t(p) * kInter + row] = q;
+      exp_range_acc(q, lo, hi);
+    }
+  } else if (!upper) {
     // once per row: expf's table from constant memory
     const float hv = swiglu_exact(acc, u);
     ws.h[size_t(p) * kInter + row] = hv;
@@ -333,7 +364,9 @@ __global__ __launch_bounds__(64 * kBWaves) void k_block_phase1(const PairTable *
 }
 
 // Phase 2: workgroup -> (pair, 256 rows of w2), wavefront -> 64 rows, one
-// per lane; down[pair][row] without the route weight.
+// per lane; down[pair][row] without the route weight (kOfficial: the
+// weight is already in h, and the output is rounded to bf16).
+template <bool kOfficial>
 __global__ __launch_bounds__(64 * kBWaves) void k_block_phase2(const PairTable *__restrict__ tab, Workspace ws,
                                                                uint32_t p0, uint32_t n_pairs, PageOffsets mx,
                                                                PageOffsets f8) {
@@ -365,11 +398,15 @@ __global__ __launch_bounds__(64 * kBWaves) void k_block_phase2(const PairTable *
     acc = row_dot_fp8<kInter / 32>(r, uint32_t(f8.w2) + row * kInter, uint32_t(f8.s2) + (row / 128) * (kInter / 128),
                                    h);
   }
+  if constexpr (kOfficial) acc = bf16_round(acc);
   ws.down[size_t(p) * kHidden + row] = acc;
 }
 
 // y[t][r] = sum_j w_j down_j[r] (routed, route order) + down_shared[r]
-// (s14_vulkan_numeric.rs:929-946); 4 rows per thread.
+// (s14_vulkan_numeric.rs:929-946); 4 rows per thread.  kOfficial: each
+// slot's bf16 output already carries its weight; y = bf16(sum in route
+// order, shared last) (executor.py:712-739).
+template <bool kOfficial>
 __global__ __launch_bounds__(256) void k_block_combine(const PairTable *__restrict__ tab, Workspace ws,
                                                        float *__restrict__ Y, uint32_t tokens) {
   const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
@@ -395,7 +432,7 @@ __global__ __launch_bounds__(256) void k_block_combine(const PairTable *__restri
 #pragma unroll
   for (uint32_t j = 0; j < uint32_t(kSlots); ++j) {
     if (j >= np) break;
-    if (sh[j]) {
+    if (kOfficial || sh[j]) {
       acc.x = __fadd_rn(acc.x, d[j].x);
       acc.y = __fadd_rn(acc.y, d[j].y);
       acc.z = __fadd_rn(acc.z, d[j].z);
@@ -407,28 +444,33 @@ __global__ __launch_bounds__(256) void k_block_combine(const PairTable *__restri
       acc.w = __fadd_rn(acc.w, __fmul_rn(sw[j], d[j].w));
     }
   }
+  if constexpr (kOfficial) acc = make_float4(bf16_round(acc.x), bf16_round(acc.y), bf16_round(acc.z), bf16_round(acc.w));
   *reinterpret_cast<float4 *>(Y + size_t(t) * kHidden + r) = acc;
 }
 
 }  // namespace
 
 hipError_t launch_block_phase1(hipStream_t s, const Workspace &ws, uint32_t p0, uint32_t n_pairs,
-                               const PageOffsets &mx, const PageOffsets &fp8, const float *x, KernelEvents ev) {
-  hipExtLaunchKernelGGL(k_block_phase1, dim3(kBTileGroups * n_pairs), dim3(64 * kBWaves), 0, s, ev.start, ev.stop, 0,
-                        ws.table, ws, x, p0, n_pairs, mx, fp8);
+                               const PageOffsets &mx, const PageOffsets &fp8, const float *x, bool official,
+                               KernelEvents ev) {
+  hipExtLaunchKernelGGL(official ? k_block_phase1<true> : k_block_phase1<false>, dim3(kBTileGroups * n_pairs),
+                        dim3(64 * kBWaves), 0, s, ev.start, ev.stop, 0, ws.table, ws, x, p0, n_pairs, mx, fp8);
   return hipGetLastError();
 }
 
 hipError_t launch_block_phase2(hipStream_t s, const Workspace &ws, uint32_t p0, uint32_t n_pairs,
-                               const PageOffsets &mx, const PageOffsets &fp8, hipEvent_t ev_start) {
-  hipExtLaunchKernelGGL(k_block_phase2, dim3((kHidden / (kBRowsW * kBWaves)) * n_pairs), dim3(64 * kBWaves), 0, s,
-                        ev_start, nullptr, 0, ws.table, ws, p0, n_pairs, mx, fp8);
+                               const PageOffsets &mx, const PageOffsets &fp8, bool official, hipEvent_t ev_start) {
+  hipExtLaunchKernelGGL(official ? k_block_phase2<true> : k_block_phase2<false>,
+                        dim3((kHidden / (kBRowsW * kBWaves)) * n_pairs), dim3(64 * kBWaves), 0, s, ev_start, nullptr,
+                        0, ws.table, ws, p0, n_pairs, mx, fp8);
   return hipGetLastError();
 }
 
-hipError_t launch_block_combine(hipStream_t s, const Workspace &ws, uint32_t tokens, float *y, hipEvent_t ev_stop) {
-  hipExtLaunchKernelGGL(k_block_combine, dim3((tokens * (kHidden / 4) + 255) / 256), dim3(256), 0, s, nullptr, ev_stop,
-                        0, ws.table, ws, y, tokens);
+hipError_t launch_block_combine(hipStream_t s, const Workspace &ws, uint32_t tokens, float *y, bool official,
+                                hipEvent_t ev_stop) {
+  hipExtLaunchKernelGGL(official ? k_block_combine<true> : k_block_combine<false>,
+                        dim3((tokens * (kHidden / 4) + 255) / 256), dim3(256), 0, s, nullptr, ev_stop, 0, ws.table, ws,
+                        y, tokens);
   return hipGetLastError();
 }
 

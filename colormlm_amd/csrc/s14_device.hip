@@ -672,29 +672,76 @@ __device__ __forceinline__ void plan_publish(const RouteSpec &rs, PairTable *tab
 // workgroup of a routed pair then selects the top-k itself from the scores
 // (route_pair), so no workgroup waits for a last arrival.
 //
-// kRequantX (single-token official layers): one more workgroup, past the
-// scoring ones, requantises the token's x for the official expert (group
-// 128, l42_reference.py:390-403) into ws.xq, in parallel with the scoring;
-// the official phase 1 then stages those values as the exact phase 1
-// stages x, instead of every phase-1 workgroup requantising x itself.
+// kRequantX (official layers): one more column of workgroups, past the
+// scoring ones (one per token), requantises the token's x for the official
+// expert (group 128, l42_reference.py:390-403) into ws.xq, in parallel with
+// the scoring, and (blocks) records the exponent range of the requantised
+// values in ws.xwin (the block engine's decode window); phase 1 then reads those
+// values as the exact phase 1 reads x, instead of every phase-1 workgroup
+// requantising x itself.  These workgroups are not counted in the
+// last-arrival hand-off, so the plan never waits for them.
 constexpr uint32_t kRouteGroup = 16;
 constexpr uint32_t kSingleRouteWaves = 4;  // route_waves(1)
+
+// The requant workgroup of token t, NT = blockDim.x threads, x's loads all
+// in flight at once; kWindow: also x's window (the block engine's).
+// xs: LDS for kHidden floats, red: 2 NT / 64 ints.
+template <uint32_t NT, bool kWindow>
+__device__ __forceinline__ void route_requant_x(const Workspace &ws, const float *__restrict__ X, uint32_t t,
+                                                float *xs, int *red) {
+  static_assert(NT % 64 == 0 && NT <= 64 * kMaxTokens, "whole wavefronts, at most the route workgroup's");
+  // no bounds test on the loads: the compiler cannot prove threadIdx.x < NT,
+  // so a test would put each load behind a branch and a wait
+  static_assert((kHidden / 4) % NT == 0, "whole float4 sweeps");
+  constexpr uint32_t W = NT / 64, IT = kHidden / 4 / NT;
+  const uint32_t wave = threadIdx.x >> 6;
+  const float4 *src = reinterpret_cast<const float4 *>(X + size_t(t) * kHidden);
+  float4 v[IT];
+#pragma unroll
+  for (uint32_t it = 0; it < IT; ++it) v[it] = src[it * NT + threadIdx.x];
+#pragma unroll
+  for (uint32_t it = 0; it < IT; ++it) reinterpret_cast<float4 *>(xs)[it * NT + threadIdx.x] = v[it];
+  __syncthreads();
+  int lo = 255, hi = 0;
+  requant128_groups(xs, kHidden / 128, int(wave), int(W), lo, hi);
+  if constexpr (kWindow) {
+    lo = wave_min_i(lo);
+    hi = wave_max_i(hi);
+    if ((threadIdx.x & 63) == 0) {
+      red[2 * wave] = lo;
+      red[2 * wave + 1] = hi;
+    }
+  }
+  __syncthreads();
+  float4 *dst = reinterpret_cast<float4 *>(ws.xq + size_t(t) * kHidden);
+  for (uint32_t i = threadIdx.x; i < kHidden / 4; i += blockDim.x) dst[i] = reinterpret_cast<const float4 *>(xs)[i];
+  if (kWindow && threadIdx.x == 0) {
+    for (uint32_t w = 0; w < W; ++w) {
+      lo = min(lo, red[2 * w]);
+      hi = max(hi, red[2 * w + 1]);
+    }
+    ws.xwin[t] = uint32_t(lo) | (uint32_t(hi) << 16);
+  }
+}
+
 template <bool kScoresOnly, bool kRequantX = false>
 __global__ __launch_bounds__(64 * kMaxTokens) void k_route(RouteSpec rs, Workspace ws, const float *__restrict__ X) {
   if constexpr (kRequantX) {
-    static_assert(kScoresOnly, "the requant rides on the single-token launch");
-    if (blockIdx.x * kSingleRouteWaves >= rs.r.n_experts) {  // the requant workgroup (uniform)
-      __shared__ float xs[kHidden];
-      __shared__ int red[2 * kSingleRouteWaves];
-      const uint32_t t = blockIdx.y;
-      stage_x_block<kHidden, 64 * kSingleRouteWaves>(xs, X + size_t(t) * kHidden, red);
-      requant128_block<64 * kSingleRouteWaves>(xs, kHidden, red);  // ends with a barrier
-      float *dst = ws.xq + size_t(t) * kHidden;
-      for (uint32_t i = threadIdx.x; i < kHidden / 4; i += blockDim.x)
-        reinterpret_cast<float4 *>(dst)[i] = reinterpret_cast<const float4 *>(xs)[i];
+    // the requant column (uniform): past the scoring columns; tested with
+    // the values the scoring needs anyway (gridDim would be one more
+    // dependent scalar load ahead of every scoring workgroup's loads)
+    if (blockIdx.x * (blockDim.x >> 6) >= rs.r.n_experts) {
+      __shared__ float rq_xs[kHidden];
+      __shared__ int rq_red[2 * kMaxTokens];
+      if (blockDim.x == 256)
+        route_requant_x<256, !kScoresOnly>(ws, X, blockIdx.y, rq_xs, rq_red);
+      else
+        route_requant_x<64 * kMaxTokens, !kScoresOnly>(ws, X, blockIdx.y, rq_xs, rq_red);
       return;
     }
   }
+  // the scoring workgroups' grid (without the requant column)
+  const uint32_t gx = kRequantX ? gridDim.x - 1 : gridDim.x;
   __shared__ float sc[kMaxTokens][kMaxExperts];
   __shared__ float bs[kMaxTokens][kMaxExperts];
   __shared__ uint64_t pages[kMaxExperts];
@@ -707,8 +754,8 @@ __global__ __launch_bounds__(64 * kMaxTokens) void k_route(RouteSpec rs, Workspa
   const uint32_t e = blockIdx.x * W + wave;
   if (e < rs.r.n_experts) {
     // blocks: expert 0's wavefront also records the token's x window for
-    // the block engine's phase 1
-    const float2 s = router_score(rs.r, X, t, e, (!kScoresOnly && e == 0) ? ws.xwin + t : nullptr);
+    // the block engine's phase 1 (official: the requant column records xq's)
+    const float2 s = router_score(rs.r, X, t, e, (!kScoresOnly && !kRequantX && e == 0) ? ws.xwin + t : nullptr);
     if (lane == 0) {
       // device-coherent stores (no cache writeback needed to publish them)
       __hip_atomic_store(&ws.scores[t * kMaxExperts + e], s.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -734,7 +781,7 @@ __global__ __launch_bounds__(64 * kMaxTokens) void k_route(RouteSpec rs, Workspa
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t n = gridDim.x * gridDim.y, id = blockIdx.y * gridDim.x + blockIdx.x;
+    const uint32_t n = gx * gridDim.y, id = blockIdx.y * gx + blockIdx.x;
     const uint32_t g = id / kRouteGroup, ng = (n + kRouteGroup - 1) / kRouteGroup;
     const uint32_t gsize = min(kRouteGroup, n - g * kRouteGroup);
     uint32_t *grp = ws.route_count + kRouteCounterStride * (1 + g);
@@ -890,13 +937,14 @@ __device__ __forceinline__ uint32_t page_bytes(uint32_t fmt) {
 // pair), the pair's x staged in LDS once for all of them; each wavefront
 // takes one 16-row tile: lanes 0-31 its rows of w1, lanes 32-63 the same
 // rows of w3, one row per lane pair; h = swiglu(g, u) after a half swap.
-// kTier (1: single-token launch, 8: block launch) names the instantiation,
-// so traces and profiles keep the two workloads apart, and picks the code
-// check (per row at batch 1, per batch of groups for blocks).
+// Single-token layers only (blocks of 2..8 tokens run the block engine);
+// kTier = 1 keeps the kernel's name in line with the FAST kernels', whose
+// tier picks their shape.
 template <int kSrc, int kTier, bool kOfficial>
 __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable plan, RouteSpec rs, Workspace ws,
                                                                      const float *__restrict__ X, PageOffsets mx,
                                                                      PageOffsets f8) {
+  static_assert(kTier == 1, "blocks run the block engine");
   __shared__ float xs[kHidden];
   __shared__ double exptab[32];
   __shared__ int red[2 * kP1ExactWaves];
@@ -918,19 +966,12 @@ __global__ __launch_bounds__(64 * kP1ExactWaves) void k_phase1_exact(PairTable p
     const uint32_t soff = uint32_t(upper ? mx.s3 : mx.s1) + row * (kHidden / 32);
     MxBatch<kPF> ba;
     mx_load<kPF>(ba, src, woff, soff, 0);  // first weights in flight during the x copy
-    if constexpr (kTier == 1) {
-      // batch 1 (one wavefront per SIMD, issue-bound): one code check per row
-      RowCodes<kHidden / 32> rc;
-      load_row_codes<kHidden / 32>(rc, src, soff);
-      CodeWindow win = stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
-      if constexpr (kOfficial && !kXq) win = requant128_block<64 * kP1ExactWaves>(xs, kHidden, red);
-      acc = mx_row_pair_fixed<kPF, kHidden / 32>(0.0f, ba, src, woff, soff, xs + 16 * h, win, rc);
-    } else {
-      // blocks: per-batch code checks measured faster here
-      CodeWindow win = stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
-      if constexpr (kOfficial && !kXq) win = requant128_block<64 * kP1ExactWaves>(xs, kHidden, red);
-      acc = mx_row_pair_fixed<kPF, kHidden / 32>(0.0f, ba, src, woff, soff, xs + 16 * h, win);
-    }
+    // one wavefront per SIMD, issue-bound: one code check per row
+    RowCodes<kHidden / 32> rc;
+    load_row_codes<kHidden / 32>(rc, src, soff);
+    CodeWindow win = stage_x_block<kHidden, 64 * kP1ExactWaves>(xs, srcx, red);
+    if constexpr (kOfficial && !kXq) win = requant128_block<64 * kP1ExactWaves>(xs, kHidden, red);
+    acc = mx_row_pair_fixed<kPF, kHidden / 32>(0.0f, ba, src, woff, soff, xs + 16 * h, win, rc);
   } else {
     const uint32_t woff = uint32_t(upper ? f8.w3 : f8.w1) + row * kHidden + 16u * h;
     const uint32_t soff = uint32_t(upper ? f8.s3 : f8.s1) + (row / 128) * (kHidden / 128);
@@ -1145,6 +1186,7 @@ __global__ __launch_bounds__(64 * kP2ExactWaves) void k_phase2_exact(const PairT
                                                                      const uint32_t *__restrict__ hwin,
                                                                      float *__restrict__ Y, PageOffsets mx,
                                                                      PageOffsets f8) {
+  static_assert(kTier == 1, "blocks run the block engine");
   __shared__ float hs[kSlots][kHStride];
   __shared__ float part[kSlots][kP2ExactRows];
   const uint32_t t = blockIdx.y;
@@ -1463,13 +1505,19 @@ hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const Router
   return hipGetLastError();
 }
 
-hipError_t launch_route(hipStream_t s, const Workspace &ws, const RouteSpec &rs, const float *x, KernelEvents ev) {
+hipError_t launch_route(hipStream_t s, const Workspace &ws, const RouteSpec &rs, const float *x, KernelEvents ev,
+                        bool requant_x) {
   const uint32_t w = route_waves(rs.tokens);
-  const uint32_t blocks = (rs.r.n_experts + w - 1) / w * rs.tokens;
+  static_assert(kMaxTokens == 8, "the requant column runs 256 or 512 threads");
+  const uint32_t groups = (rs.r.n_experts + w - 1) / w, blocks = groups * rs.tokens;
   // the workspace holds counters for at most kRouteCounters / kRouteCounterStride - 1 groups
   if ((blocks + kRouteGroup - 1) / kRouteGroup > kRouteCounters / kRouteCounterStride - 1) return hipErrorInvalidValue;
-  hipExtLaunchKernelGGL(k_route<false>, dim3((rs.r.n_experts + w - 1) / w, rs.tokens), dim3(64 * w), 0, s, ev.start,
-                        ev.stop, 0, rs, ws, x);
+  if (requant_x)
+    hipExtLaunchKernelGGL(k_route<false, true>, dim3(groups + 1, rs.tokens), dim3(64 * w), 0, s, ev.start, ev.stop,
+                          0, rs, ws, x);
+  else
+    hipExtLaunchKernelGGL(k_route<false>, dim3(groups, rs.tokens), dim3(64 * w), 0, s, ev.start, ev.stop, 0, rs, ws,
+                          x);
   return hipGetLastError();
 }
 
@@ -1496,7 +1544,7 @@ void phase1_launch(hipStream_t s, const Workspace &ws, const PairTable &plan, co
     const dim3 grid(kInter / p1_fast_rows(kTier), n_pairs);
     hipExtLaunchKernelGGL(k_phase1_fast<kSrc, kTier>, grid, dim3(256), 0, s, ev.start, ev.stop, 0, plan, rs, ws, x,
                           mx, fp8);
-  } else {
+  } else if constexpr (kTier == 1) {  // blocks in these modes run the block engine
     const dim3 grid(kInter / (kP1ExactRows * kP1ExactWaves), n_pairs);
     const dim3 blk(64 * kP1ExactWaves);
     if (mode == S14_MODE_OFFICIAL) {
@@ -1533,15 +1581,17 @@ void phase2_tier(hipStream_t s, const Workspace &ws, uint32_t tokens, const Page
                  float *y, int mode, KernelEvents ev) {
   const PairTable *tab = ws.table;
   const float *h = ws.h;
-  if (mode == S14_MODE_FAST)
+  if (mode == S14_MODE_FAST) {
     hipExtLaunchKernelGGL(k_phase2_fast<kTier>, dim3(kHidden / kP2FastRows, tokens), dim3(64 * kP2FastWaves), 0, s,
                           ev.start, ev.stop, 0, tab, h, y, mx, fp8);
-  else if (mode == S14_MODE_OFFICIAL)
-    hipExtLaunchKernelGGL(k_phase2_exact<kTier, true>, dim3(kHidden / kP2ExactRows, tokens), dim3(64 * kP2ExactWaves),
-                          0, s, ev.start, ev.stop, 0, tab, h, ws.hwin, y, mx, fp8);
-  else
-    hipExtLaunchKernelGGL(k_phase2_exact<kTier, false>, dim3(kHidden / kP2ExactRows, tokens), dim3(64 * kP2ExactWaves),
-                          0, s, ev.start, ev.stop, 0, tab, h, ws.hwin, y, mx, fp8);
+  } else if constexpr (kTier == 1) {  // blocks in these modes run the block engine
+    if (mode == S14_MODE_OFFICIAL)
+      hipExtLaunchKernelGGL(k_phase2_exact<kTier, true>, dim3(kHidden / kP2ExactRows, tokens),
+                            dim3(64 * kP2ExactWaves), 0, s, ev.start, ev.stop, 0, tab, h, ws.hwin, y, mx, fp8);
+    else
+      hipExtLaunchKernelGGL(k_phase2_exact<kTier, false>, dim3(kHidden / kP2ExactRows, tokens),
+                            dim3(64 * kP2ExactWaves), 0, s, ev.start, ev.stop, 0, tab, h, ws.hwin, y, mx, fp8);
+  }
 }
 }  // namespace
 
@@ -1558,6 +1608,7 @@ hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *ho
                          uint32_t tokens, const PageOffsets &mx, const PageOffsets &fp8, const float *x, int mode,
                          KernelEvents ev, const RouteSpec *route) {
   if (route && (host_plan || tokens != 1)) return hipErrorInvalidValue;  // in-kernel planning: one routed token
+  if (tokens > 1 && mode != S14_MODE_FAST) return hipErrorInvalidValue;  // the block engine's
   if (tokens <= 1)
     phase1_tier<1>(s, ws, host_plan, route, n_pairs, mx, fp8, x, mode, ev);
   else
@@ -1567,6 +1618,7 @@ hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *ho
 
 hipError_t launch_phase2(hipStream_t s, const Workspace &ws, uint32_t tokens, const PageOffsets &mx,
                          const PageOffsets &fp8, float *y, int mode, KernelEvents ev) {
+  if (tokens > 1 && mode != S14_MODE_FAST) return hipErrorInvalidValue;  // the block engine's
   if (tokens <= 1)
     phase2_tier<1>(s, ws, tokens, mx, fp8, y, mode, ev);
   else

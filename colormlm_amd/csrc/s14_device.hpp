@@ -221,9 +221,12 @@ hipError_t launch_router_scores(hipStream_t s, const Workspace &ws, const Router
                                 uint8_t *q = nullptr, uint8_t *qs = nullptr);
 // Scores, then the top-k and weights of every token to rs.ids_out /
 // weights_out when given; with rs.expert_pages also the pair table in
-// ws.table.  One launch (the last workgroup plans).
+// ws.table.  One launch (the last workgroup plans).  requant_x: one more
+// workgroup per token writes the official act_quant of x (group 128,
+// dequantised) to ws.xq and its exponent range to ws.xwin, for the official
+// block engine.
 hipError_t launch_route(hipStream_t s, const Workspace &ws, const RouteSpec &rs, const float *x,
-                        KernelEvents ev = {});
+                        KernelEvents ev = {}, bool requant_x = false);
 // The same launch's scoring alone (no plan, no table): for one routed
 // token, whose phase 1 plans from the scores itself (launch_phase1 with
 // `route`).  official: one more workgroup writes the official act_quant of
@@ -236,6 +239,8 @@ hipError_t launch_route_scores(hipStream_t s, const Workspace &ws, const RouteSp
 // every workgroup of a routed pair selects the top-k from the scores of
 // launch_route_scores, and workgroup (0,0) reports the route and publishes
 // the table; otherwise the pairs are read from the table launch_route wrote.
+// More than one token: FAST only (EXACT and official blocks run the block
+// engine below); other modes return hipErrorInvalidValue.
 hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *host_plan,
                          uint32_t n_pairs, uint32_t tokens, const PageOffsets &mx,
                          const PageOffsets &fp8, const float *x, int mode, KernelEvents ev = {},
@@ -243,18 +248,23 @@ hipError_t launch_phase1(hipStream_t s, const Workspace &ws, const PairTable *ho
 // Blocks of 2..8 tokens in EXACT order, one row per lane (s14_block.hip):
 // phase 1 and phase 2 of the pairs [p0, p0 + n_pairs) of the table the route
 // kernel wrote, then each token's route-order accumulation of its pairs'
-// outputs into y [tokens][hidden].
+// outputs into y [tokens][hidden].  official: the official expert semantics
+// (x from ws.xq, which launch_route with requant_x wrote; bf16 g, u, h and
+// w2 outputs, the route weight before w2, h's act_quant inside phase 1).
 hipError_t launch_block_phase1(hipStream_t s, const Workspace &ws, uint32_t p0, uint32_t n_pairs,
-                               const PageOffsets &mx, const PageOffsets &fp8, const float *x, KernelEvents ev = {});
+                               const PageOffsets &mx, const PageOffsets &fp8, const float *x, bool official,
+                               KernelEvents ev = {});
 hipError_t launch_block_phase2(hipStream_t s, const Workspace &ws, uint32_t p0, uint32_t n_pairs,
-                               const PageOffsets &mx, const PageOffsets &fp8, hipEvent_t ev_start = nullptr);
-hipError_t launch_block_combine(hipStream_t s, const Workspace &ws, uint32_t tokens, float *y,
+                               const PageOffsets &mx, const PageOffsets &fp8, bool official,
+                               hipEvent_t ev_start = nullptr);
+hipError_t launch_block_combine(hipStream_t s, const Workspace &ws, uint32_t tokens, float *y, bool official,
                                 hipEvent_t ev_stop = nullptr);
 // The single-expert chain (one MXFP4 page, y = weight * down) in EXACT
 // order with lane quads: its phase 1 and phase 2.
 hipError_t launch_chain_quad(hipStream_t s, const Workspace &ws, const uint8_t *page, const PageOffsets &mx,
                              const float *x, float weight, float *y, KernelEvents ev1 = {}, KernelEvents ev2 = {});
-// w2 of every pair and the per-token accumulation into y [tokens][hidden].
+// w2 of every pair and the per-token accumulation into y [tokens][hidden]
+// (more than one token: FAST only, as launch_phase1).
 hipError_t launch_phase2(hipStream_t s, const Workspace &ws, uint32_t tokens,
                          const PageOffsets &mx, const PageOffsets &fp8, float *y, int mode,
                          KernelEvents ev = {});

@@ -1146,7 +1146,8 @@ def test_official_chain_weight_before_w2(ctx, oracle, bank):
 
 
 @pytest.mark.parametrize("score_fn,scale,tokens", [(N.S14_SCORE_SIGMOID, 1.0, 8),
-                                                   (N.S14_SCORE_SQRT_SOFTPLUS, 1.5, 3)])
+                                                   (N.S14_SCORE_SQRT_SOFTPLUS, 1.5, 3),
+                                                   (N.S14_SCORE_SIGMOID, 1.0, 2)])
 def test_official_block(ctx, oracle, bank, score_fn, scale, tokens):
     """Official blocks through the device router, token by token against the
     oracle: ids and weights bit for bit with the oracle's own route (both
@@ -1168,4 +1169,28 @@ def test_official_block(ctx, oracle, bank, score_fn, scale, tokens):
         assert_bit_exact(wts_h[t], w_o, f"weights t={t}")
         want = oracle.moe_layer_official(xs[t], [page_host(bank, int(e)) for e in i_o], w_o, shared)
         assert_bit_exact(got[t], want, f"official block t={t}")
+
+
+def test_official_block_fp8_shared(ctx, oracle, bank):
+    """Official block (T=5) with the reference's FP8 shared page: the FP8
+    rows of both phases read the requantised x and h, and phase-2 wavefronts
+    whose halves mix MXFP4 and FP8 rows round each to bf16; token by token
+    against the oracle's official layer on the device's route."""
+    tokens = 5
+    say(f"official block T={tokens} with FP8 shared page")
+    sh = synth.gen_fp8_page(0, 0)
+    xs = synth.block_tokens(seed=12, tokens=tokens)
+    router = s14.Router(bank["wr_d"], bank["bias_d"])
+    y = torch.empty((tokens, HIDDEN), dtype=torch.float32, device="cuda")
+    ids = torch.empty((tokens, 6), dtype=torch.int16, device="cuda")
+    wts = torch.empty((tokens, 6), dtype=torch.float32, device="cuda")
+    s14.moe_block_route(ctx, tokens, router, bank["table"], dev(sh), dev(xs), y, ids, wts,
+                        shared_format=N.S14_PAGE_FP8, mode=s14.OFFICIAL)
+    got, ids_h, wts_h = host(y), host(ids).astype(np.uint16), host(wts)
+    for t in range(tokens):
+        _, i_o, w_o = oracle.route(bank["wr"], bank["bias"], xs[t])
+        assert ids_h[t].tolist() == i_o.tolist()
+        assert_bit_exact(wts_h[t], w_o, f"weights t={t}")
+        want = oracle.moe_layer_official(xs[t], [page_host(bank, int(e)) for e in i_o], w_o, sh, shared_fmt="fp8")
+        assert_bit_exact(got[t], want, f"official block fp8-shared t={t}")
 
