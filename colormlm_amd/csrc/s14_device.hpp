@@ -88,12 +88,12 @@ struct Workspace {
   float *biased;  // [kMaxTokens][kMaxExperts]
   uint32_t *route_count;  // [kRouteCounters]: groups, then per-group workgroups, of the running route launch that are done (one per 128-byte line)
   uint32_t *hwin;         // [kMaxPairs][kInter / kP1ExactRows]: exponent range (lo | hi << 16) of each exact phase-1 tile's h
-  uint32_t *xwin;         // [kMaxTokens]: exponent range (lo | hi << 16) of each token's x, written by the block route
+  uint32_t *xwin;         // [kMaxTokens]: exponent range (lo | hi << 16) of each token's x (official: of its act_quant), written by the block route
   // kSyncLines lines of kRouteCounterStride words: the status word (kStatus*
   // bits) that launches leave for s14_launch_status.
   uint32_t *sync;
   float *down;  // [kMaxPairs][kHidden]: each pair's w2 output of a block launch (before its route weight)
-  float *xq;    // [kMaxTokens][kHidden]: official mode's act_quant of x (dequantised), written by the single-token route
+  float *xq;    // [kMaxTokens][kHidden]: official mode's act_quant of x (dequantised), written by the route launch
   size_t bytes;
 };
 constexpr uint32_t kSyncLines = 1;
@@ -104,7 +104,8 @@ inline uint32_t *status_word(const Workspace &ws) { return ws.sync + kSyncStatus
 enum : uint32_t { kStatusNullPage = 1u, kStatusBadRoute = 2u };
 
 // Layout of the workspace in one device allocation (each region 256-byte
-// aligned): table | h | scores | biased | route counters | h windows.
+// aligned): table | h | scores | biased | route counters | h windows | x
+// windows | status line | w2 rows | requantised x.
 struct WorkspaceLayout {
   size_t table, h, scores, biased, count, hwin, xwin, sync, down, xq, bytes;
 };

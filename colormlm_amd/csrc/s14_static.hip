@@ -3,8 +3,9 @@
 // loops, harnesses that forbid allocation).  It has no counterpart in the
 // reference.
 //
-// Its workspace (pair table, h, router scores, route completion counters, h
-// exponent windows: the same layout a context allocates) is the file-scope
+// Its workspace (pair table, h, per-pair w2 rows, router scores, the
+// official requantised x, route completion counters, x and h exponent
+// windows: the same layout a context allocates) is the file-scope
 // device array `scratch`, one copy per GPU, held until the process ends.  In
 // host code `scratch` names a host-side stand-in, not a device address, so
 // host code never passes it to a kernel: the first call on a device, with
