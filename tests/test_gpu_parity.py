@@ -499,12 +499,14 @@ def test_moe_block_fp8_shared_and_edge_codes(ctx, oracle, bank):
         assert np.max(np.abs(fast[t] - got[t])) <= 1e-3
 
 
-def test_moe_block_edge_scale_codes(ctx, oracle, bank):
+@pytest.mark.parametrize("mode", [s14.EXACT, s14.OFFICIAL])
+def test_moe_block_edge_scale_codes(ctx, oracle, bank, mode):
     """Block launches (T=3) whose routed pages carry scale codes outside the
     scaled-decode window in w1, w3 and w2 rows (copies of the chosen pages,
-    substituted in the page table), against the oracle on the same pages."""
+    substituted in the page table), against the oracle on the same pages, in
+    EXACT and official mode (whose windows come from the requantised x and h)."""
     tokens = 3
-    say(f"config 3 block T={tokens} with out-of-window scale codes, exact")
+    say(f"config 3 block T={tokens} with out-of-window scale codes, mode={mode}")
     xs = synth.block_tokens(seed=9, tokens=tokens)
     routes = [oracle.route(bank["wr"], bank["bias"], xs[t]) for t in range(tokens)]
     chosen = sorted({int(e) for _, i_o, _ in routes for e in i_o})
@@ -523,12 +525,13 @@ def test_moe_block_edge_scale_codes(ctx, oracle, bank):
         edited[e] = pg
     router = s14.Router(bank["wr_d"], bank["bias_d"])
     y = torch.empty((tokens, HIDDEN), dtype=torch.float32, device="cuda")
-    s14.moe_block_route(ctx, tokens, router, table, bank["pages"][256], dev(xs), y, mode=s14.EXACT)
+    s14.moe_block_route(ctx, tokens, router, table, bank["pages"][256], dev(xs), y, mode=mode)
     got = host(y)
     shared = page_host(bank, 256)
+    layer = oracle.moe_layer_official if mode == s14.OFFICIAL else oracle.moe_layer
     for t, (_, i_o, w_o) in enumerate(routes):
         pages = [edited[int(e)] if int(e) in edited else page_host(bank, int(e)) for e in i_o]
-        assert_bit_exact(got[t], oracle.moe_layer(xs[t], pages, w_o, shared), f"block edge codes token {t}")
+        assert_bit_exact(got[t], layer(xs[t], pages, w_o, shared), f"block edge codes token {t}")
 
 
 def test_pool_upload_publish_compute_release(ctx, oracle, bank):
