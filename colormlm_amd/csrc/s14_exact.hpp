@@ -174,6 +174,104 @@ __device__ __forceinline__ float pair_chain16(float acc, const float (&p)[16]) {
   return acc;
 }
 
+// pair_chain16 over p with the next group's scaled products (as
+// mx_products_scaled forms them: scale operand, eight conversions, sixteen
+// multiplies) placed one after each of the chain's adds.  An add waits
+// about 8 cycles for the one before it and issues in about 4.6, so an
+// independent instruction between two adds costs no time; the compiler's
+// own schedule bunches the adds together and the multiplies together.
+// Scheduling barriers around each (add, independent instruction) pair fix
+// this order.  sw: the 4-byte scale word holding the next group's code in
+// byte j (the converters read only their scale operand's exponent field,
+// so one shift forms it).
+__device__ __forceinline__ float pair_chain16_ilv(float acc, const float (&p)[16], float (&q)[16], uint2 w,
+                                                  uint32_t sw, int j, const X16 &x) {
+#define S14_ILV __builtin_amdgcn_sched_barrier(0)
+  v2f d[8];
+  float sc;
+  S14_ILV;
+  sc = __uint_as_float(j < 3 ? sw << (23 - 8 * j) : sw >> 1);
+  acc = __fadd_rn(from_odd(acc), p[0]);
+  S14_ILV;
+  d[0] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.x, sc, 0);
+  acc = __fadd_rn(acc, p[1]);
+  S14_ILV;
+  d[1] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.x, sc, 1);
+  acc = __fadd_rn(acc, p[2]);
+  S14_ILV;
+  d[2] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.x, sc, 2);
+  acc = __fadd_rn(acc, p[3]);
+  S14_ILV;
+  d[3] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.x, sc, 3);
+  acc = __fadd_rn(acc, p[4]);
+  S14_ILV;
+  q[0] = __fmul_rn(x.v[0], d[0].x);
+  acc = __fadd_rn(acc, p[5]);
+  S14_ILV;
+  q[1] = __fmul_rn(x.v[1], d[0].y);
+  acc = __fadd_rn(acc, p[6]);
+  S14_ILV;
+  d[4] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.y, sc, 0);
+  acc = __fadd_rn(acc, p[7]);
+  S14_ILV;
+  q[2] = __fmul_rn(x.v[2], d[1].x);
+  acc = __fadd_rn(acc, p[8]);
+  S14_ILV;
+  q[3] = __fmul_rn(x.v[3], d[1].y);
+  acc = __fadd_rn(acc, p[9]);
+  S14_ILV;
+  d[5] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.y, sc, 1);
+  acc = __fadd_rn(acc, p[10]);
+  S14_ILV;
+  q[4] = __fmul_rn(x.v[4], d[2].x);
+  acc = __fadd_rn(acc, p[11]);
+  S14_ILV;
+  q[5] = __fmul_rn(x.v[5], d[2].y);
+  acc = __fadd_rn(acc, p[12]);
+  S14_ILV;
+  d[6] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.y, sc, 2);
+  acc = __fadd_rn(acc, p[13]);
+  S14_ILV;
+  q[6] = __fmul_rn(x.v[6], d[3].x);
+  acc = __fadd_rn(acc, p[14]);
+  S14_ILV;
+  q[7] = __fmul_rn(x.v[7], d[3].y);
+  acc = __fadd_rn(acc, p[15]);
+  S14_ILV;
+  d[7] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.y, sc, 3);
+  acc = __fadd_rn(from_even(acc), p[0]);
+  S14_ILV;
+  q[8] = __fmul_rn(x.v[8], d[4].x);
+  acc = __fadd_rn(acc, p[1]);
+  S14_ILV;
+  q[9] = __fmul_rn(x.v[9], d[4].y);
+  acc = __fadd_rn(acc, p[2]);
+  S14_ILV;
+  q[10] = __fmul_rn(x.v[10], d[5].x);
+  acc = __fadd_rn(acc, p[3]);
+  S14_ILV;
+  q[11] = __fmul_rn(x.v[11], d[5].y);
+  acc = __fadd_rn(acc, p[4]);
+  S14_ILV;
+  q[12] = __fmul_rn(x.v[12], d[6].x);
+  acc = __fadd_rn(acc, p[5]);
+  S14_ILV;
+  q[13] = __fmul_rn(x.v[13], d[6].y);
+  acc = __fadd_rn(acc, p[6]);
+  S14_ILV;
+  q[14] = __fmul_rn(x.v[14], d[7].x);
+  acc = __fadd_rn(acc, p[7]);
+  S14_ILV;
+  q[15] = __fmul_rn(x.v[15], d[7].y);
+  acc = __fadd_rn(acc, p[8]);
+  S14_ILV;
+#pragma unroll
+  for (int k = 9; k < 16; ++k) acc = __fadd_rn(acc, p[k]);
+  S14_ILV;
+#undef S14_ILV
+  return acc;
+}
+
 // MXFP4 products of the lane's 8 code bytes (16 k, low nibble first).
 // Scaled: p = x * (e2m1 * 2^(c-127)) via the gfx950 scaled converter — equal
 // to the oracle's (x * e2m1) * 2^(c-127) for codes inside the window.
@@ -335,7 +433,25 @@ __device__ __forceinline__ float mx_consume(float acc, const MxBatch<PF> &b, con
 #pragma unroll
     for (int j = 0; j < PF / 4; ++j) ok = ok && codes_in(b.c[j], win);
   }
-  if (!kCheck || __builtin_amdgcn_ballot_w64(!ok) == 0) {
+  if constexpr (!kCheck) {
+    // the row's codes were checked once: each group's chain interleaved
+    // with the next group's products (pair_chain16_ilv)
+    X16 xa, xb;
+    float p[16], q[16];
+    load_x16(xa, xh + g0 * 32);
+    load_x16(xb, xh + (g0 + 1) * 32);
+    mx_products_scaled(p, b.w[0], batch_code(b, 0), xa);
+#pragma unroll
+    for (int i = 0; i < PF; i += 2) {
+      if (i + 2 < PF) load_x16(xa, xh + (g0 + i + 2) * 32);
+      acc = pair_chain16_ilv(acc, p, q, b.w[i + 1], b.c[(i + 1) >> 2], (i + 1) & 3, xb);
+      if (i + 3 < PF) load_x16(xb, xh + (g0 + i + 3) * 32);
+      if (i + 2 < PF)
+        acc = pair_chain16_ilv(acc, q, p, b.w[i + 2], b.c[(i + 2) >> 2], (i + 2) & 3, xa);
+      else
+        acc = pair_chain16(acc, q);
+    }
+  } else if (__builtin_amdgcn_ballot_w64(!ok) == 0) {
     X16 xa, xb;
     float p[16], q[16];
     load_x16(xa, xh + g0 * 32);
