@@ -820,6 +820,75 @@ __device__ __forceinline__ bool quad_codes_in(const QuadCodes<G> &qc, CodeWindow
   const bool ok = int(min(mn.x, mn.y)) >= win.cmin && int(max(mx.x, mx.y)) <= win.cmax;
   return __builtin_amdgcn_ballot_w64(!ok) == 0;
 }
+// quad_chain8 over p with the next group's scaled products (mx_products8:
+// scale operand, four conversions, eight multiplies) placed among its adds,
+// one before each hand-over add (which then needs no wait states of its
+// own) and the rest after the first adds of each step; scheduling barriers
+// around each (independent instruction, add) pair fix the order (the
+// compiler's own schedule bunches the adds).  cw: the scale word holding the
+// next group's code in byte j (one shift forms the converters' operand, of
+// which they read only the exponent field); xv: that group's x.
+__device__ __forceinline__ float quad_chain8_ilv(float acc, const float (&p)[8], float (&q)[8], uint32_t w,
+                                                 uint32_t cw, int j, const float (&xv)[8]) {
+#define S14_ILV __builtin_amdgcn_sched_barrier(0)
+  v2f d[4];
+  float sc;
+  S14_ILV;
+  sc = __uint_as_float(j < 3 ? cw << (23 - 8 * j) : cw >> 1);
+  acc = __fadd_rn(from_prev_in_quad(acc), p[0]);
+  S14_ILV;
+  d[0] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 0);
+  acc = __fadd_rn(acc, p[1]);
+  S14_ILV;
+  d[1] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 1);
+  acc = __fadd_rn(acc, p[2]);
+  S14_ILV;
+  d[2] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 2);
+  acc = __fadd_rn(acc, p[3]);
+  S14_ILV;
+  d[3] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 3);
+  acc = __fadd_rn(acc, p[4]);
+  S14_ILV;
+#pragma unroll
+  for (int k = 5; k < 8; ++k) acc = __fadd_rn(acc, p[k]);
+  S14_ILV;
+  q[0] = __fmul_rn(xv[0], d[0].x);
+  acc = __fadd_rn(from_prev_in_quad(acc), p[0]);
+  S14_ILV;
+  q[1] = __fmul_rn(xv[1], d[0].y);
+  acc = __fadd_rn(acc, p[1]);
+  S14_ILV;
+  q[2] = __fmul_rn(xv[2], d[1].x);
+  acc = __fadd_rn(acc, p[2]);
+  S14_ILV;
+#pragma unroll
+  for (int k = 3; k < 8; ++k) acc = __fadd_rn(acc, p[k]);
+  S14_ILV;
+  q[3] = __fmul_rn(xv[3], d[1].y);
+  acc = __fadd_rn(from_prev_in_quad(acc), p[0]);
+  S14_ILV;
+  q[4] = __fmul_rn(xv[4], d[2].x);
+  acc = __fadd_rn(acc, p[1]);
+  S14_ILV;
+  q[5] = __fmul_rn(xv[5], d[2].y);
+  acc = __fadd_rn(acc, p[2]);
+  S14_ILV;
+#pragma unroll
+  for (int k = 3; k < 8; ++k) acc = __fadd_rn(acc, p[k]);
+  S14_ILV;
+  q[6] = __fmul_rn(xv[6], d[3].x);
+  acc = __fadd_rn(from_prev_in_quad(acc), p[0]);
+  S14_ILV;
+  q[7] = __fmul_rn(xv[7], d[3].y);
+  acc = __fadd_rn(acc, p[1]);
+  S14_ILV;
+#pragma unroll
+  for (int k = 2; k < 8; ++k) acc = __fadd_rn(acc, p[k]);
+  S14_ILV;
+#undef S14_ILV
+  return acc;
+}
+
 // Dot of one MXFP4 row of G groups (G % (4 NB) == 0) with x in LDS, NB
 // batches of 4 groups in flight; the caller issued batches 0 .. NB-1.
 // Result in every lane of the quad.
@@ -840,9 +909,18 @@ __device__ __forceinline__ float mx_row_quad_as(MxQBatch (&b)[NB], Rsrc r, uint3
       const int j = n / 4, i = n % 4;
       if (n + 1 < 4 * NB) {
         const int jn = (n + 1) / 4, in = (n + 1) % 4;
-        mx_products8<kScaled>(pn, b[jn].w[in], (b[jn].c >> (8 * in)) & 255u, xq + 32 * (g0 + n + 1));
+        if constexpr (kScaled) {
+          const float *x = xq + 32 * (g0 + n + 1);
+          const float4 xa = *reinterpret_cast<const float4 *>(x), xb = *reinterpret_cast<const float4 *>(x + 4);
+          const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+          acc = quad_chain8_ilv(acc, pc, pn, b[jn].w[in], b[jn].c, in, xv);
+        } else {
+          mx_products8<kScaled>(pn, b[jn].w[in], (b[jn].c >> (8 * in)) & 255u, xq + 32 * (g0 + n + 1));
+          acc = quad_chain8(acc, pc);
+        }
+      } else {
+        acc = quad_chain8(acc, pc);
       }
-      acc = quad_chain8(acc, pc);
       if (i == 3 && refill) mxq_load(b[j], r, woff, soff, g0 + 4 * NB + 4 * j);
 #pragma unroll
       for (int k = 0; k < 8; ++k) pc[k] = pn[k];
