@@ -1,6 +1,6 @@
 // Prefill through the S14 MoE layer (config 4) on gfx950: T tokens, each
 // routed to its top-k experts plus the shared expert, computed per expert as
-// grouped GEMMs on the CDNA4 bf16 MFMA (v_mfma_f32_32x32x16_bf16): MXFP4
+// grouped GEMMs on the CDNA4 bf16 MFMA (v_mfma_f32_16x16x32_bf16): MXFP4
 // weights (A, E8M0 per 32 k) and e4m3-requantised activations (B, E8M0 per
 // 32 k) are decoded to bf16 in registers by the gfx950 scaled converters,
 // exactly (an e2m1 value has two significant bits, an e4m3 value four, the
@@ -19,14 +19,6 @@
 // internal precision (it returns 256 * 256 + 1 * 1 as 65,536 when the two
 // products share a step): GEMM results 5.7e-5 of the output's scale away
 // from the oracle's, against 8e-7 here.
-//
-// Operand layout of v_mfma_f32_32x32x16_bf16 (lane l, half h = l / 32):
-// A is row l % 32, B column l % 32, each 8 bf16 at k 8h..8h+7 of the MFMA's
-// 16; D element i of lane l is row 8(i/4) + 4h + i%4, column l % 32.  A 64-k
-// step is four MFMAs: in MFMA j, lane half h supplies k 32h + 8j .. +7 of
-// the step, so a lane's 16 weight bytes (k 32h..32h+31 of its row, one
-// E8M0 block) and its column's 32 activations at the same k (one E8M0
-// block) feed it.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
@@ -38,7 +30,7 @@
 namespace s14 {
 namespace {
 
-typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 constexpr uint32_t kQGroup = 32;  // requant group (k values per E8M0 scale)
@@ -223,39 +215,65 @@ __global__ __launch_bounds__(1024) void k_prefill_group(PrefillArgs a, PrefillWo
 // grouped GEMMs
 // ---------------------------------------------------------------------------
 
-// Each work item's x rows into the item's tile.
-// Columns past the item's count are not written: the GEMMs never read them.
-// One thread per 16 tile bytes; the thread holding part 0 of the first step
-// of a chunk also writes that chunk's scale word.
+// Both GEMMs run on v_mfma_f32_16x16x32_bf16 over 16-column halves of a work
+// item's (up to 32) columns, in super-steps of 128 k.  Operand layout, lane
+// l = c + 16 q (c = 0..15, q = 0..3): in MFMA j (0..3) of a super-step, lane
+// l supplies row c of A and column c of B at the super-step's k values 32 q
+// + 8 j .. +7 (8 bf16 each); D element v of lane l is row 4 q + v, column c.
+// A lane's 32 k of a super-step are one E8M0 block of A's row (16 weight
+// bytes, one LDS read) and of B's column.  Every column of every item goes
+// through the same MFMA sequence, so a token's outputs do not depend on the
+// item, or the item's width, the grouping gave it.  An item of at most
+// kNarrowTokens pairs runs one half: most experts get a few tokens, and one
+// half does half the MFMA work, activation loads and activation conversions
+// of a 32-column tile.  Wider items run two halves that share each decoded
+// A operand.
+constexpr uint32_t kSuperK = 128;                          // k per super-step
+constexpr uint32_t kChunkSupers = kChunkSteps * 64 / kSuperK;  // super-steps per chunk: 2
+
+// Each work item's x rows into the item's tile: tile[super-step][half][plane
+// p][lane][16 bytes], lane = c + 16 q holding the e4m3 codes of k 32 q + 16 p
+// .. +15 of the super-step for column 16 half + c; scales [chunk][half][lane]
+// u32, byte u = the E8M0 of super-step kChunkSupers * chunk + u for the
+// lane's block q.  Columns past the item's count are not written: the GEMMs
+// never read them.  One thread per 16 tile bytes; the plane-0 thread of a
+// chunk's first super-step also writes that chunk's scale word.
 __global__ __launch_bounds__(256) void k_tile_x(PrefillWorkspace ws) {
   constexpr uint32_t kPerItem = kXTileBytes / 16;
   const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
   const uint32_t i = gid / kPerItem;
   if (i >= ws.stats[0]) return;
   const uint32_t r = gid % kPerItem;
-  const uint32_t lane = r & 63u, part = (r >> 6) & 1u, s = r >> 7;
-  const uint32_t col = lane & 31u, h = lane >> 5;
+  const uint32_t lane = r & 63u, p = (r >> 6) & 1u, half = (r >> 7) & 1u, u = r >> 8;
+  const uint32_t col = 16u * half + (lane & 15u), q = lane >> 4;
   const PrefillItem it = ws.items[i];
   if (col >= it.count) return;
   const uint32_t t = ws.pair_token[it.first + col];
   *reinterpret_cast<uint4 *>(ws.xt + size_t(i) * kXTileBytes + 16u * r) =
-      *reinterpret_cast<const uint4 *>(ws.xq + size_t(t) * kHidden + 64u * s + 32u * h + 16u * part);
-  if (part == 0 && s % kChunkSteps == 0) {
+      *reinterpret_cast<const uint4 *>(ws.xq + size_t(t) * kHidden + kSuperK * u + 32u * q + 16u * p);
+  if (p == 0 && u % kChunkSupers == 0) {
     uint32_t word = 0;
-    const uint8_t *sc = ws.xs + size_t(t) * (kHidden / kQGroup) + 2u * s + h;  // group 2 (s + k) + h
+    const uint8_t *sc = ws.xs + size_t(t) * (kHidden / kQGroup) + 4u * u + q;  // group 4 (u + k) + q
 #pragma unroll
-    for (uint32_t k = 0; k < kChunkSteps; ++k) word |= uint32_t(sc[2u * k]) << (8u * k);
-    reinterpret_cast<uint32_t *>(ws.xts + size_t(i) * kXScaleBytes)[(s / kChunkSteps) * 64u + lane] = word;
+    for (uint32_t k = 0; k < kChunkSupers; ++k) word |= uint32_t(sc[4u * k]) << (8u * k);
+    reinterpret_cast<uint32_t *>(ws.xts + size_t(i) * kXScaleBytes)[((u / kChunkSupers) * 2u + half) * 64u + lane] =
+        word;
   }
 }
 
 // A page of 0 (an expert that is not resident) reads the shared page instead
 // (mapped memory); the top-k step gave its pairs a NaN weight and set the
 // status word.
+// The address is read back through readfirstlane: it is uniform, and with
+// the GEMMs' two column-half paths the compiler otherwise kept it in VGPRs
+// and wrapped every DMA load in a loop over its lanes' descriptors.
 __device__ __forceinline__ Rsrc page_rsrc(const PrefillArgs &a, uint32_t e) {
   const uint8_t *page = e < kMaxExperts ? reinterpret_cast<const uint8_t *>(a.expert_pages[e]) : a.shared_page;
   if (!page) page = a.shared_page;
-  return make_rsrc(page, uint32_t(S14_EXPERT_PAGE_BYTES));
+  const uint64_t pv = reinterpret_cast<uint64_t>(page);
+  const uint64_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(pv))));
+  const uint64_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(pv >> 32))));
+  return make_rsrc(reinterpret_cast<const uint8_t *>(lo | (hi << 32)), uint32_t(S14_EXPERT_PAGE_BYTES));
 }
 
 // E8M0 code c as the scale operand of the gfx950 scaled converters (they
@@ -280,26 +298,32 @@ __device__ __forceinline__ v8bf fp8x8_bf16(uint32_t w0, uint32_t w1, float s) {
                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, s, true))};
   return __builtin_bit_cast(v8bf, v);
 }
-// One 64-k step of a lane's activations (lo: k 32h..32h+15 of the step, hi:
-// k 32h+16..32h+31, one E8M0 block) as the B operands of the step's four
-// MFMAs: MFMA j takes k 32h+8j..32h+8j+7.
+// A lane's activations of one half and one super-step (k 32 q .. 32 q + 31
+// of its column: planes 0 and 1, one E8M0 block) as the B operands of MFMAs
+// j = 0..3.
 struct BStep {
   v8bf b[4];
 };
-__device__ __forceinline__ BStep b_step(uint4 lo, uint4 hi, uint32_t code) {
+__device__ __forceinline__ BStep b_step(uint4 p0, uint4 p1, uint32_t code) {
   const float s = e8m0_operand(code);
-  return BStep{{fp8x8_bf16(lo.x, lo.y, s), fp8x8_bf16(lo.z, lo.w, s), fp8x8_bf16(hi.x, hi.y, s),
-                fp8x8_bf16(hi.z, hi.w, s)}};
+  return BStep{{fp8x8_bf16(p0.x, p0.y, s), fp8x8_bf16(p0.z, p0.w, s), fp8x8_bf16(p1.x, p1.y, s),
+                fp8x8_bf16(p1.z, p1.w, s)}};
 }
-// acc += A . B over one 64-k step: the lane's 16 weight bytes (k 32h..32h+31
-// of its row, one E8M0 block) decoded exactly to bf16 against the step's
-// activations, four MFMAs (exact products, f32 accumulation).
-__device__ __forceinline__ v16f mfma_step(uint4 w, uint32_t code, const BStep &b, v16f acc) {
+// A lane's 16 weight bytes of one super-step (k 32 q .. 32 q + 31 of its
+// row, one E8M0 block) as the A operands of MFMAs j = 0..3.
+struct AStep {
+  v8bf a[4];
+};
+__device__ __forceinline__ AStep a_step(uint4 w, uint32_t code) {
   const float s = e8m0_operand(code);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp4x8_bf16(w.x, s), b.b[0], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp4x8_bf16(w.y, s), b.b[1], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp4x8_bf16(w.z, s), b.b[2], acc, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp4x8_bf16(w.w, s), b.b[3], acc, 0, 0, 0);
+  return AStep{{fp4x8_bf16(w.x, s), fp4x8_bf16(w.y, s), fp4x8_bf16(w.z, s), fp4x8_bf16(w.w, s)}};
+}
+// acc += A . B over one super-step of a 16x16 tile: exact products, f32
+// accumulation.
+__device__ __forceinline__ v4f mfma_step(const AStep &a, const BStep &b, v4f acc) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.a[j], b.b[j], acc, 0, 0, 0);
+  return acc;
 }
 
 // Pins the accumulators in uniform control flow.  The epilogues store only
@@ -308,31 +332,32 @@ __device__ __forceinline__ v16f mfma_step(uint4 w, uint32_t code, const BStep &b
 // EXEC mask does not take the inactive lanes' A rows and scales (their output
 // rows come back as garbage).
 template <int NT>
-__device__ __forceinline__ void mfma_settle(v16f (&acc)[NT]) {
+__device__ __forceinline__ void mfma_settle(v4f (&acc)[NT]) {
 #pragma unroll
   for (int j = 0; j < NT; ++j) asm volatile("" : "+a"(acc[j]));
 }
 
-// Weight operand through LDS.  A wavefront streams its 32-row weight tile in
-// chunks of kChunkSteps K steps (128 bytes of each row): the DMA form of the
+// Weight operand through LDS.  A wavefront streams its weight tile in chunks
+// of kChunkSteps 64-k steps (128 bytes of each row): the DMA form of the
 // buffer load (buffer_load_dwordx4 ... lds) writes each chunk into a ring
 // slot with 8 lanes per row, so every quarter-wave reads 256 contiguous bytes
-// of two rows; the MFMA then reads one 16-byte piece of 32 rows from LDS.
-// Loading the MFMA layout straight from HBM instead has each quarter-wave
-// touch 16 rows: the vector L1 then handles one 64-byte sector per 16 useful
-// bytes and, not HBM, bounds the kernel.  Row r's piece q sits at piece
-// q ^ swz(r) of its 128 bytes, so the 16 rows of a read pass land in
-// distinct banks.  Each slot is its own LDS array, which lets the compiler
-// wait for one slot's DMA loads without draining the others.
+// of two rows; each MFMA lane then reads its row's 16-byte piece of a
+// super-step from LDS.  Loading the MFMA layout straight from HBM instead
+// has each quarter-wave touch 16 rows: the vector L1 then handles one
+// 64-byte sector per 16 useful bytes and, not HBM, bounds the kernel.  Row
+// r's piece q sits at piece q ^ swz(r) of its 128 bytes, so the 16 rows of a
+// read pass land in distinct banks.  Each slot is its own LDS array, which
+// lets the compiler wait for one slot's DMA loads without draining the
+// others.
 __device__ __forceinline__ uint32_t swz(uint32_t r) { return (r + (r >> 3)) & 7u; }
 // The same for the phase-2 scale tile (64-byte rows, 4 pieces).
 __device__ __forceinline__ uint32_t swz4(uint32_t r) { return (r + (r >> 2)) & 3u; }
 
 constexpr uint32_t kUpSlotBytes = 2 * 32 * 128;  // w1 and w3 chunks
-// w2 rows per phase-2 wavefront: two 32-row MFMA tiles sharing each
-// activation operand (with one tile a wavefront read twice as many
-// activation bytes as weight bytes: 249 us for the down GEMM at 512 tokens
-// against 220 us; four tiles measured no faster)
+// w2 rows per phase-2 wavefront: four 16-row MFMA tiles sharing each
+// activation operand (with 32 rows a wavefront read twice as many activation
+// bytes as weight bytes: 249 us for the down GEMM at 512 tokens against 220
+// us with 64; 128 measured no faster)
 constexpr uint32_t kDnRows = 64;
 constexpr uint32_t kDnSlotBytes = kDnRows * 128;  // w2 chunk
 __shared__ __attribute__((aligned(16))) uint8_t up_slot0[kUpSlotBytes];
@@ -374,47 +399,70 @@ __device__ __forceinline__ void dma16(Rsrc r, uint8_t *lds, uint32_t off) {
 __device__ __forceinline__ void lds_reads_done() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
 // Activation operand: a VGPR ring of kRing chunks, each refilled right after
-// its last use, from the item tile (two coalesced 1 KiB loads per step).
+// its last use, from the item tile (two coalesced 1 KiB loads per super-step
+// and half).
 constexpr int kRing = 4;
+template <int NH>
 struct BChunk {
-  uint4 lo[kChunkSteps], hi[kChunkSteps];
-  uint32_t sc;  // byte k: scale of step k for this lane's half
+  uint4 v[NH][kChunkSupers][2];  // [half][super-step][plane]
+  uint32_t sc[NH];               // byte u: scale of super-step u for this lane's block
 };
 // Lanes of columns past the item's count read from past the descriptor's
 // range: the buffer load returns zeros without a memory access, so a work
-// item moves only its pairs' activations (items average ~13 of 32 columns).
+// item moves only its pairs' activations.
 constexpr uint32_t kOffRange = 0x40000000u;
-__device__ __forceinline__ uint32_t bcol_base(uint32_t lane, bool live) { return live ? 16u * lane : kOffRange; }
-__device__ __forceinline__ uint32_t bscale_base(uint32_t lane, bool live) { return live ? 4u * lane : kOffRange; }
-__device__ __forceinline__ void load_bchunk(BChunk &b, Rsrc tile, Rsrc scales, uint32_t c, uint32_t tbase,
-                                            uint32_t sbase) {
+template <int NH>
+struct BBase {
+  uint32_t tile[NH], scale[NH];
+};
+template <int NH>
+__device__ __forceinline__ BBase<NH> b_base(uint32_t lane, uint32_t count) {
+  BBase<NH> b;
 #pragma unroll
-  for (uint32_t k = 0; k < kChunkSteps; ++k) {
-    const uint32_t s = c * kChunkSteps + k;
-    b.lo[k] = ld16(tile, tbase + 2048u * s);
-    b.hi[k] = ld16(tile, tbase + 2048u * s + 1024u);
+  for (int h = 0; h < NH; ++h) {
+    const bool live = 16u * uint32_t(h) + (lane & 15u) < count;
+    b.tile[h] = live ? 2048u * uint32_t(h) + 16u * lane : kOffRange;
+    b.scale[h] = live ? 256u * uint32_t(h) + 4u * lane : kOffRange;
   }
-  b.sc = ld4(scales, sbase + c * 256u);
+  return b;
+}
+template <int NH>
+__device__ __forceinline__ void load_bchunk(BChunk<NH> &b, Rsrc tile, Rsrc scales, uint32_t c, const BBase<NH> &bb) {
+#pragma unroll
+  for (uint32_t u = 0; u < kChunkSupers; ++u)
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+      for (uint32_t p = 0; p < 2; ++p)
+        b.v[h][u][p] = ld16(tile, bb.tile[h] + 4096u * (c * kChunkSupers + u) + 1024u * p);
+#pragma unroll
+  for (int h = 0; h < NH; ++h) b.sc[h] = ld4(scales, bb.scale[h] + 512u * c);
+}
+
+// Phase 2's item tile (ht, hts) in the x tile's layout: the byte offset of
+// the codes of rows 16 p .. 16 p + 15 of block b of super-step u (phase 2's
+// K positions kSuperK u + 32 b + 16 p ..) for column col, and of the scale
+// byte of (u, b) for column col.
+__device__ __forceinline__ uint32_t h_tile_offset(uint32_t u, uint32_t b, uint32_t p, uint32_t col) {
+  return 4096u * u + 2048u * (col >> 4) + 1024u * p + 16u * ((col & 15u) + 16u * b);
+}
+__device__ __forceinline__ uint32_t h_scale_offset(uint32_t u, uint32_t b, uint32_t col) {
+  return (((u / kChunkSupers) * 2u + (col >> 4)) * 64u + (col & 15u) + 16u * b) * 4u + u % kChunkSupers;
 }
 
 // Phase 1: one wavefront per (32-row tile of w1/w3, work item of <= 32
-// pairs of one expert).  K = 4096 in 16 chunks; weights kRing - 1 chunks
-// ahead in LDS, activations kRing chunks ahead in VGPRs.  Then h =
-// swiglu(g, u), requantised per token over the tile's 32 rows (one E8M0
-// group of phase 2's K) and stored into the item's phase-2 tile.
+// pairs of one expert), NH column halves.  K = 4096 in 16 chunks; weights
+// kRing - 1 chunks ahead in LDS, activations kRing chunks ahead in VGPRs.
+// Then h = swiglu(g, u), requantised per token over the tile's 32 rows (one
+// E8M0 group of phase 2's K) and stored into the item's phase-2 tile.
 // kOfficial: h = bf16(swiglu(bf16(g), bf16(u)) * w), w the pair's route
 // weight (1 for the shared expert) (executor.py:717-731), stored in f32 for
 // k_requant_h128 (its group of 128 rows spans four of these workgroups).
-template <bool kOfficial>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_prefill_up(PrefillArgs a,
-                                                                                                PrefillWorkspace ws) {
-  const uint32_t n_items = ws.stats[0];
-  const uint32_t item = blockIdx.y;
-  if (item >= n_items) return;
-  const PrefillItem it = ws.items[item];
+template <bool kOfficial, int NH>
+__device__ __forceinline__ void prefill_up_item(const PrefillArgs &a, const PrefillWorkspace &ws,
+                                                const PrefillItem &it, uint32_t item, const Rsrc rp) {
   const uint32_t rt = blockIdx.x;
-  const uint32_t lane = threadIdx.x & 63, col = lane & 31, h = lane >> 5;
-  const Rsrc rp = page_rsrc(a, it.expert);
+  const uint32_t lane = threadIdx.x & 63, c16 = lane & 15u, q = lane >> 4;
   constexpr uint32_t kRowBytes = kHidden / 2, kScaleRow = kHidden / 32;
   constexpr uint32_t kChunks = kHidden / 64 / kChunkSteps;
   // DMA lane map: load j of a chunk covers rows 8j..8j+7 of the tile, lane
@@ -443,41 +491,52 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   }
   const Rsrc xt = make_rsrc(ws.xt + size_t(item) * kXTileBytes, kXTileBytes);
   const Rsrc xts = make_rsrc(ws.xts + size_t(item) * kXScaleBytes, kXScaleBytes);
-  const bool live = col < it.count;
-  const uint32_t tb = bcol_base(lane, live), sbb = bscale_base(lane, live);
-  // expf's table for the epilogue's 16 SwiGLUs per lane: one entry per lane
-  // now, written to a free ring slot after the K loop (an LDS array of its
-  // own would cost this kernel its fourth wavefront per CU)
+  const BBase<NH> bb = b_base<NH>(lane, it.count);
+  // expf's table for the epilogue's SwiGLUs: one entry per lane now, written
+  // to a free ring slot after the K loop (an LDS array of its own would cost
+  // this kernel its fourth wavefront per CU)
   const double exp_entry = s14x::exp_table_entry(lane & 31u);
-  BChunk rb[kRing];
+  BChunk<NH> rb[kRing];
   issue(Slot<0>{}, 0);
   issue(Slot<1>{}, 1);
   issue(Slot<2>{}, 2);
 #pragma unroll
   for (int j = 0; j < kRing; ++j) {
-    load_bchunk(rb[j], xt, xts, uint32_t(j), tb, sbb);
+    load_bchunk(rb[j], xt, xts, uint32_t(j), bb);
     __builtin_amdgcn_sched_barrier(0);  // chunk order, so the loop's waits count the ring right
   }
-  v16f g, u;
+  // acc[4 h + i]: g of column half h, rows 16 i .. 16 i + 15 of the tile;
+  // acc[4 h + 2 + i]: u of the same
+  v4f acc[4 * NH];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) g[i] = u[i] = 0.0f;
-  const uint32_t sw = swz(col);
+  for (int t = 0; t < 4 * NH; ++t) acc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t sw[2] = {swz(c16), swz(16u + c16)};  // the lane's A rows c16 and 16 + c16
   auto chunk = [&](auto slot_tag, uint32_t c, bool refill) {
     constexpr int S = decltype(slot_tag)::value;
-    const uint8_t *src = up_slot<S>() + 128u * col;
 #pragma unroll
-    for (uint32_t k = 0; k < kChunkSteps; ++k) {
-      const uint32_t q = (2u * k + h) ^ sw;
-      const uint4 a1 = *reinterpret_cast<const uint4 *>(src + 16u * q);
-      const uint4 a3 = *reinterpret_cast<const uint4 *>(src + 4096u + 16u * q);
-      const uint32_t sb = 2u * (c * kChunkSteps + k) + h;  // scale byte of this lane's weight block
-      const uint32_t sp = 128u * col + 16u * ((sb >> 4) ^ sw) + (sb & 15u);
-      const uint32_t c1 = up_scales[sp], c3 = up_scales[4096u + sp];
-      const BStep B = b_step(rb[S].lo[k], rb[S].hi[k], (rb[S].sc >> (8u * k)) & 0xffu);
-      g = mfma_step(a1, c1, B, g);
-      u = mfma_step(a3, c3, B, u);
+    for (uint32_t u = 0; u < kChunkSupers; ++u) {
+      const uint32_t pc = 4u * u + q;                  // the lane's piece of the chunk row
+      const uint32_t sb = kChunkSupers * 4u * c + pc;  // and its E8M0 block of the row
+      AStep a1[2], a3[2];
+#pragma unroll
+      for (uint32_t i = 0; i < 2; ++i) {
+        const uint32_t R = 16u * i + c16;
+        const uint8_t *src = up_slot<S>() + 128u * R + 16u * (pc ^ sw[i]);
+        const uint32_t sp = 128u * R + 16u * ((sb >> 4) ^ sw[i]) + (sb & 15u);
+        a1[i] = a_step(*reinterpret_cast<const uint4 *>(src), up_scales[sp]);
+        a3[i] = a_step(*reinterpret_cast<const uint4 *>(src + 4096u), up_scales[4096u + sp]);
+      }
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        const BStep B = b_step(rb[S].v[h][u][0], rb[S].v[h][u][1], (rb[S].sc[h] >> (8u * u)) & 0xffu);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          acc[4 * h + i] = mfma_step(a1[i], B, acc[4 * h + i]);
+          acc[4 * h + 2 + i] = mfma_step(a3[i], B, acc[4 * h + 2 + i]);
+        }
+      }
     }
-    if (refill) load_bchunk(rb[S], xt, xts, c + kRing, tb, sbb);
+    if (refill) load_bchunk(rb[S], xt, xts, c + kRing, bb);
     // keep the refill here: left free, the scheduler sinks loads to the end
     // of the loop body, and the next round's first wait then drains the ring
     __builtin_amdgcn_sched_barrier(0);
@@ -501,57 +560,78 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   chunk(Slot<1>{}, kChunks - 3, false);
   chunk(Slot<2>{}, kChunks - 2, false);
   chunk(Slot<3>{}, kChunks - 1, false);
-  v16f acc[2] = {g, u};
-  mfma_settle<2>(acc);
-  g = acc[0];
-  u = acc[1];
-  // epilogue: lane (col, h) holds rows 8q + 4h + v (q, v = 0..3) of column col
+  mfma_settle(acc);
   double *exptab = reinterpret_cast<double *>(up_slot0);  // slot 0's last chunk is consumed
   if (lane < 32) exptab[lane] = exp_entry;
   __syncthreads();  // one wavefront: orders the table writes before the lookups
+  // epilogue: lane (c16, q) holds rows 16 i + 4 q + v (i = 0, 1; v = 0..3)
+  // of column 16 h + c16 in element v of acc[4 h + i] (g) and acc[4 h + 2 + i] (u)
   if constexpr (kOfficial) {
-    if (col >= it.count) return;
-    const uint32_t pair = it.first + col;
-    const float w = ws.pair_weight[pair];
-    float *dst = ws.hf + size_t(pair) * kInter + rt * 32u;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      float o[4];
+    for (int h = 0; h < NH; ++h) {
+      const uint32_t col = 16u * uint32_t(h) + c16;
+      if (col >= it.count) continue;
+      const uint32_t pair = it.first + col;
+      const float w = ws.pair_weight[pair];
+      float *dst = ws.hf + size_t(pair) * kInter + rt * 32u;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int i = 4 * q4 + v;
-        o[v] = bf16_round(__fmul_rn(swiglu_exact(bf16_round(g[i]), bf16_round(u[i]), exptab), w));
+      for (int i = 0; i < 2; ++i) {
+        float o[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          o[v] = bf16_round(
+              __fmul_rn(swiglu_exact(bf16_round(acc[4 * h + i][v]), bf16_round(acc[4 * h + 2 + i][v]), exptab), w));
+        *reinterpret_cast<float4 *>(dst + 16u * uint32_t(i) + 4u * q) = make_float4(o[0], o[1], o[2], o[3]);
       }
-      *reinterpret_cast<float4 *>(dst + 8u * q4 + 4u * h) = make_float4(o[0], o[1], o[2], o[3]);
     }
     return;
   }
-  float hv[16];
-  float amax = 0.0f;
+  // this tile's 32 rows are block rt % 4 of phase 2's super-step rt / 4
+  // (one E8M0 group), read by lane (col % 16) + 16 (rt % 4) of the column's half
+  const uint32_t u2 = rt >> 2, b2 = rt & 3u;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    hv[i] = swiglu_exact(g[i], u[i], exptab);
-    amax = fabsf(hv[i]) > amax ? fabsf(hv[i]) : amax;
+  for (int h = 0; h < NH; ++h) {
+    float hv[8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      hv[e] = swiglu_exact(acc[4 * h + e / 4][e % 4], acc[4 * h + 2 + e / 4][e % 4], exptab);
+      amax = fabsf(hv[e]) > amax ? fabsf(hv[e]) : amax;
+    }
+    // the column's other 24 rows: the lanes of the other three blocks
+#pragma unroll
+    for (int m = 16; m < 64; m <<= 1) {
+      const float other = __shfl_xor(amax, m);
+      amax = other > amax ? other : amax;
+    }
+    const uint32_t code = requant_code(amax);
+    const float inv = __uint_as_float((254u - code) << 23);
+    const uint32_t col = 16u * uint32_t(h) + c16;
+    if (col >= it.count) continue;  // phase 2 never reads absent columns
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // rows 16 i + 4 q .. +3: plane i, bytes 4 q .. 4 q + 3
+      uint32_t word = 0;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) word |= e4m3_rne_sat(__fmul_rn(hv[4 * i + v], inv)) << (8 * v);
+      *reinterpret_cast<uint32_t *>(ws.ht + size_t(item) * kHTileBytes + h_tile_offset(u2, b2, uint32_t(i), col) +
+                                    4u * q) = word;
+    }
+    if (q == 0) ws.hts[size_t(item) * kHScaleBytes + h_scale_offset(u2, b2, col)] = uint8_t(code);
   }
-  const float other = __shfl_xor(amax, 32);  // the other 16 rows of the column
-  amax = other > amax ? other : amax;
-  const uint32_t code = requant_code(amax);
-  const float inv = __uint_as_float((254u - code) << 23);
-  if (col >= it.count) return;  // phase 2 never reads absent columns
-  // this tile's 32 rows are half blk of phase 2's K step s2 (group rt)
-  const uint32_t s2 = rt >> 1, blk = rt & 1u;
-  uint8_t *tile = ws.ht + size_t(item) * kHTileBytes + 2048u * s2;
-#pragma unroll
-  for (int q4 = 0; q4 < 4; ++q4) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) word |= e4m3_rne_sat(__fmul_rn(hv[4 * q4 + v], inv)) << (8 * v);
-    const uint32_t pos = 32u * blk + 8u * q4 + 4u * h;  // k in the step of the first of 4 consecutive rows
-    *reinterpret_cast<uint32_t *>(tile + 1024u * ((pos >> 4) & 1u) + 16u * (col + 32u * (pos >> 5)) + (pos & 15u)) =
-        word;
-  }
-  if (h == 0) ws.hts[size_t(item) * kHScaleBytes + ((s2 / kChunkSteps) * 64u + col + 32u * blk) * 4u + s2 % kChunkSteps] =
-      uint8_t(code);
+}
+
+template <bool kOfficial>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_prefill_up(PrefillArgs a,
+                                                                                                PrefillWorkspace ws) {
+  const uint32_t n_items = ws.stats[0];
+  const uint32_t item = blockIdx.y;
+  if (item >= n_items) return;
+  const PrefillItem it = ws.items[item];
+  const Rsrc rp = page_rsrc(a, it.expert);
+  if (uint32_t(__builtin_amdgcn_readfirstlane(int(it.count))) <= kNarrowTokens)
+    prefill_up_item<kOfficial, 1>(a, ws, it, item, rp);
+  else
+    prefill_up_item<kOfficial, 2>(a, ws, it, item, rp);
 }
 
 // Official mode: the w2 input's act_quant (group 128) of every work item's
@@ -593,32 +673,22 @@ __global__ __launch_bounds__(256) void k_requant_h128(PrefillWorkspace ws) {
   for (int i = 0; i < 4; ++i)
     w[i] = e4m3_rne_sat(__fmul_rn(q[i].x, inv)) | (e4m3_rne_sat(__fmul_rn(q[i].y, inv)) << 8) |
            (e4m3_rne_sat(__fmul_rn(q[i].z, inv)) << 16) | (e4m3_rne_sat(__fmul_rn(q[i].w, inv)) << 24);
-  const uint32_t rt = 4u * m + j / 2u, s2 = rt >> 1, blk = rt & 1u;
-  const uint32_t pos = 32u * blk + 16u * (j & 1u);  // k in the step of the piece's first row
-  uint8_t *tile = ws.ht + size_t(item) * kHTileBytes;
-  *reinterpret_cast<uint4 *>(tile + 2048u * s2 + 1024u * ((pos >> 4) & 1u) + 16u * (col + 32u * (pos >> 5))) =
+  // group m is phase 2's super-step m: piece j is plane j % 2 of block j / 2
+  *reinterpret_cast<uint4 *>(ws.ht + size_t(item) * kHTileBytes + h_tile_offset(m, j >> 1, j & 1u, col)) =
       make_uint4(w[0], w[1], w[2], w[3]);
-  if (j < 4u) {  // the scale byte of tile 4m + j
-    const uint32_t rs = 4u * m + j, ss = rs >> 1, bs = rs & 1u;
-    ws.hts[size_t(item) * kHScaleBytes + ((ss / kChunkSteps) * 64u + col + 32u * bs) * 4u + ss % kChunkSteps] =
-        uint8_t(code);
-  }
+  if ((j & 1u) == 0) ws.hts[size_t(item) * kHScaleBytes + h_scale_offset(m, j >> 1, col)] = uint8_t(code);
 }
 
 // Phase 2: one wavefront per (64-row tile of w2, work item): down rows of
-// every pair of the item, f32, route weight not applied, as two 32-row
-// MFMA tiles that share each activation operand.  K = 2048 in 8 chunks, the
+// every pair of the item, f32, route weight not applied, as four 16-row
+// MFMA tiles per column half, each decoded A operand shared by the halves
+// and each activation operand by the four tiles.  K = 2048 in 8 chunks, the
 // same rings as phase 1.  kOfficial: rounded to bf16.
-template <bool kOfficial>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_prefill_down(PrefillArgs a,
-                                                                                                  PrefillWorkspace ws) {
-  const uint32_t n_items = ws.stats[0];
-  const uint32_t item = blockIdx.y;
-  if (item >= n_items) return;
-  const PrefillItem it = ws.items[item];
+template <bool kOfficial, int NH>
+__device__ __forceinline__ void prefill_down_item(const PrefillArgs &a, const PrefillWorkspace &ws,
+                                                  const PrefillItem &it, uint32_t item, const Rsrc rp) {
   const uint32_t rt = blockIdx.x;  // 64-row tile
-  const uint32_t lane = threadIdx.x & 63, col = lane & 31, h = lane >> 5;
-  const Rsrc rp = page_rsrc(a, it.expert);
+  const uint32_t lane = threadIdx.x & 63, c16 = lane & 15u, q = lane >> 4;
   constexpr uint32_t kRowBytes = kInter / 2, kScaleRow = kInter / 32;
   constexpr uint32_t kChunks = kInter / 64 / kChunkSteps;
   constexpr uint32_t kDma = kDnRows / 8;  // DMA loads per chunk: 8 rows each
@@ -643,47 +713,47 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   }
   const Rsrc ht = make_rsrc(ws.ht + size_t(item) * kHTileBytes, kHTileBytes);
   const Rsrc hts = make_rsrc(ws.hts + size_t(item) * kHScaleBytes, kHScaleBytes);
-  const bool live = col < it.count;
-  const uint32_t tb = bcol_base(lane, live), sbb = bscale_base(lane, live);
-  BChunk rb[kRing];
+  const BBase<NH> bb = b_base<NH>(lane, it.count);
+  BChunk<NH> rb[kRing];
   issue(Slot<0>{}, 0);
   issue(Slot<1>{}, 1);
   issue(Slot<2>{}, 2);
 #pragma unroll
   for (int j = 0; j < kRing; ++j) {
-    load_bchunk(rb[j], ht, hts, uint32_t(j), tb, sbb);
+    load_bchunk(rb[j], ht, hts, uint32_t(j), bb);
     __builtin_amdgcn_sched_barrier(0);  // chunk order, so the loop's waits count the ring right
   }
-  constexpr int NT = int(kDnRows / 32);  // MFMA tiles
-  v16f d[NT];
+  constexpr int NT = int(kDnRows / 16);  // row tiles
+  v4f d[NH * NT];                        // d[NT h + tl]: column half h, rows 16 tl .. 16 tl + 15
 #pragma unroll
-  for (int tl = 0; tl < NT; ++tl)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) d[tl][i] = 0.0f;
-  // the lane's rows 32 tl + col, one per tile
+  for (int t = 0; t < NH * NT; ++t) d[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  // the lane's rows 16 tl + c16, one per tile
   uint32_t sw[NT], s4[NT];
 #pragma unroll
   for (int tl = 0; tl < NT; ++tl) {
-    sw[tl] = swz(32u * uint32_t(tl) + col);
-    s4[tl] = swz4(32u * uint32_t(tl) + col);
+    sw[tl] = swz(16u * uint32_t(tl) + c16);
+    s4[tl] = swz4(16u * uint32_t(tl) + c16);
   }
   auto chunk = [&](auto slot_tag, uint32_t c, bool refill) {
     constexpr int S = decltype(slot_tag)::value;
     const uint8_t *src = dn_slot<S>();
 #pragma unroll
-    for (uint32_t k = 0; k < kChunkSteps; ++k) {
-      const uint32_t p = 2u * k + h;
-      const uint32_t sb = 2u * (c * kChunkSteps + k) + h;
-      const BStep B = b_step(rb[S].lo[k], rb[S].hi[k], (rb[S].sc >> (8u * k)) & 0xffu);
+    for (uint32_t u = 0; u < kChunkSupers; ++u) {
+      const uint32_t pc = 4u * u + q;                  // the lane's piece of the chunk row
+      const uint32_t sb = kChunkSupers * 4u * c + pc;  // and its E8M0 block of the row
+      BStep B[NH];
+#pragma unroll
+      for (int h = 0; h < NH; ++h) B[h] = b_step(rb[S].v[h][u][0], rb[S].v[h][u][1], (rb[S].sc[h] >> (8u * u)) & 0xffu);
 #pragma unroll
       for (int tl = 0; tl < NT; ++tl) {
-        const uint32_t r = 32u * uint32_t(tl) + col;
-        const uint4 aw = *reinterpret_cast<const uint4 *>(src + 128u * r + 16u * (p ^ sw[tl]));
-        const uint32_t ca = dn_scales[64u * r + 16u * ((sb >> 4) ^ s4[tl]) + (sb & 15u)];
-        d[tl] = mfma_step(aw, ca, B, d[tl]);
+        const uint32_t r = 16u * uint32_t(tl) + c16;
+        const uint4 aw = *reinterpret_cast<const uint4 *>(src + 128u * r + 16u * (pc ^ sw[tl]));
+        const AStep A = a_step(aw, dn_scales[64u * r + 16u * ((sb >> 4) ^ s4[tl]) + (sb & 15u)]);
+#pragma unroll
+        for (int h = 0; h < NH; ++h) d[NT * h + tl] = mfma_step(A, B[h], d[NT * h + tl]);
       }
     }
-    if (refill) load_bchunk(rb[S], ht, hts, c + kRing, tb, sbb);
+    if (refill) load_bchunk(rb[S], ht, hts, c + kRing, bb);
     __builtin_amdgcn_sched_barrier(0);  // as in phase 1
   };
   static_assert(kRing == 4 && kChunks % 4 == 0 && kChunks >= 8, "four ring slots, whole rounds");
@@ -703,18 +773,35 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   chunk(Slot<1>{}, kChunks - 3, false);
   chunk(Slot<2>{}, kChunks - 2, false);
   chunk(Slot<3>{}, kChunks - 1, false);
-  mfma_settle<NT>(d);
-  if (col >= it.count) return;
+  mfma_settle(d);
+  // lane (c16, q) holds rows 16 tl + 4 q + v of column 16 h + c16 in element v of d[NT h + tl]
 #pragma unroll
-  for (int tl = 0; tl < NT; ++tl) {
-    float *dst = ws.down + size_t(it.first + col) * kHidden + rt * kDnRows + 32u * uint32_t(tl);
+  for (int h = 0; h < NH; ++h) {
+    const uint32_t col = 16u * uint32_t(h) + c16;
+    if (col >= it.count) continue;
+    float *dst = ws.down + size_t(it.first + col) * kHidden + rt * kDnRows + 4u * q;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      float4 o = make_float4(d[tl][4 * q4], d[tl][4 * q4 + 1], d[tl][4 * q4 + 2], d[tl][4 * q4 + 3]);
+    for (int tl = 0; tl < NT; ++tl) {
+      const v4f v = d[NT * h + tl];
+      float4 o = make_float4(v[0], v[1], v[2], v[3]);
       if constexpr (kOfficial) o = make_float4(bf16_round(o.x), bf16_round(o.y), bf16_round(o.z), bf16_round(o.w));
-      *reinterpret_cast<float4 *>(dst + 8u * q4 + 4u * h) = o;
+      *reinterpret_cast<float4 *>(dst + 16u * uint32_t(tl)) = o;
     }
   }
+}
+
+template <bool kOfficial>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_prefill_down(PrefillArgs a,
+                                                                                                  PrefillWorkspace ws) {
+  const uint32_t n_items = ws.stats[0];
+  const uint32_t item = blockIdx.y;
+  if (item >= n_items) return;
+  const PrefillItem it = ws.items[item];
+  const Rsrc rp = page_rsrc(a, it.expert);
+  if (uint32_t(__builtin_amdgcn_readfirstlane(int(it.count))) <= kNarrowTokens)
+    prefill_down_item<kOfficial, 1>(a, ws, it, item, rp);
+  else
+    prefill_down_item<kOfficial, 2>(a, ws, it, item, rp);
 }
 
 // y[t] = 0; y += w_s * down_s in route order; y += shared down

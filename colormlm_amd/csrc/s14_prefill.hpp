@@ -12,6 +12,7 @@ namespace s14 {
 constexpr uint32_t kMaxPrefillTokens = 1024;
 constexpr uint32_t kPrefillBitWords = kMaxPrefillTokens / 32;  // token bitmap words per expert
 constexpr uint32_t kItemTokens = 32;  // tokens of one expert per GEMM work item: one MFMA column tile
+constexpr uint32_t kNarrowTokens = 16;  // items of at most this many tokens run one 16-column half
 
 // One GEMM work item: `count` consecutive pairs of one expert, starting at
 // pair `first` (expert kMaxExperts is the shared expert).
@@ -22,17 +23,18 @@ struct PrefillItem {
 };
 
 // Item tiles: the activation operand (B) of one work item laid out so each
-// K step is two coalesced 1 KiB loads: tile[step][part][lane][16 bytes],
-// lane = column + 32 h holding the e4m3 codes of k 32 h + 16 part .. +15 of
-// the step for its column, one E8M0 block per lane (columns past the item's
-// count are neither written nor read).  Scales: [chunk of kChunkSteps
-// steps][lane] u32, byte k = the E8M0 of step kChunkSteps * chunk + k for
-// the lane's half.
+// 128-k super-step is two coalesced 1 KiB loads per 16-column half:
+// tile[super-step][half][plane p][lane][16 bytes], lane = c + 16 q holding
+// the e4m3 codes of k 32 q + 16 p .. +15 of the super-step for column 16 half
+// + c, one E8M0 block (q) per lane (columns past the item's count are
+// neither written nor read; an item of at most kNarrowTokens pairs has only
+// half 0).  Scales: [chunk of kChunkSteps 64-k steps][half][lane] u32, byte u
+// (0, 1) = the E8M0 of the chunk's super-step u for the lane's block.
 constexpr uint32_t kChunkSteps = 4;
 constexpr uint32_t kXTileBytes = (kHidden / 64) * 2048;                      // phase 1: 128 KiB
-constexpr uint32_t kXScaleBytes = (kHidden / 64 / kChunkSteps) * 64 * 4;     // 4 KiB
+constexpr uint32_t kXScaleBytes = (kHidden / 64 / kChunkSteps) * 2 * 64 * 4; // 8 KiB
 constexpr uint32_t kHTileBytes = (kInter / 64) * 2048;                       // phase 2: 64 KiB
-constexpr uint32_t kHScaleBytes = (kInter / 64 / kChunkSteps) * 64 * 4;      // 2 KiB
+constexpr uint32_t kHScaleBytes = (kInter / 64 / kChunkSteps) * 2 * 64 * 4;  // 4 KiB
 
 // Upper bound of the work items of T tokens: every expert contributes at
 // most one partial item beyond its full ones.

@@ -492,17 +492,19 @@ def last_prefill_view(ctx: Context) -> dict:
 
     n_items = int(v.n_items)
     items = grab(v.items, 3 * n_items, "<u4").reshape(n_items, 3)
-    steps = N.INTER // 64
-    tiles = grab(v.ht, n_items * steps * 2048, "|u1").reshape(n_items, steps, 2, 2, 32, 16)  # [i][s][part][h][col][b]
-    tscales = grab(v.hts, n_items * steps * 64, "|u1").reshape(n_items, steps // 4, 2, 32, 4)  # [i][c][h][col][k]
+    supers = N.INTER // 128
+    # tile [u][half][plane][b][c][byte]: k 128 u + 32 b + 16 plane + byte of
+    # column 16 half + c; scales [chunk][half][b][c][byte]: byte u' < 2 is
+    # the E8M0 of super-step 2 chunk + u', block b
+    tiles = grab(v.ht, n_items * supers * 4096, "|u1").reshape(n_items, supers, 2, 2, 4, 16, 16)
+    tscales = grab(v.hts, n_items * (supers // 2) * 512, "|u1").reshape(n_items, supers // 2, 2, 4, 16, 4)
     hq = np.zeros((P, N.INTER), np.uint8)
     hs = np.zeros((P, N.INTER // 32), np.uint8)
     for i, (_, first, count) in enumerate(items.tolist()):
-        # pair first + col, step s: value 32 h + 16 part + b
-        blk = tiles[i, :, :, :, :count].transpose(3, 0, 2, 1, 4)  # [col][s][h][part][b]
-        hq[first:first + count] = blk.reshape(count, N.INTER)
-        sc = tscales[i, :, :, :count].transpose(2, 0, 3, 1)  # [col][c][k][h] -> group 2 (4c + k) + h
-        hs[first:first + count] = sc.reshape(count, N.INTER // 32)
+        blk = tiles[i].transpose(1, 4, 0, 3, 2, 5).reshape(32, N.INTER)  # [half][c][u][b][plane][byte]
+        hq[first:first + count] = blk[:count]
+        sc = tscales[i][..., :2].transpose(1, 3, 0, 4, 2).reshape(32, N.INTER // 32)  # [half][c][chunk][u'][b]
+        hs[first:first + count] = sc[:count]
     return {
         "tokens": T,
         "n_pairs": P,
