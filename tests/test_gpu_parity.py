@@ -957,6 +957,73 @@ def test_prefill_ragged_and_max_tokens(ctx, oracle, bank, prefill_router, tokens
                         torch.empty(1, device="cuda"))
 
 
+def _boundary_routes(T: int, targets) -> np.ndarray:
+    """T rows of six distinct experts in which expert e appears exactly
+    targets[e] times (the rest of the 6T slots spread over the other
+    experts): each token takes the six experts with the most slots left."""
+    left = np.zeros(256, np.int64)
+    for e, c in targets.items():
+        left[e] = c
+    others = [e for e in range(256) if e not in targets]
+    rest, k = 6 * T - int(left.sum()), 0
+    while rest > 0:
+        left[others[k % len(others)]] += 1
+        rest -= 1
+        k += 1
+    rows = np.zeros((T, 6), np.int64)
+    for t in range(T):
+        order = np.lexsort((np.arange(256), -left))[:6]  # most slots left, lowest id first
+        rows[t] = np.sort(order)
+        left[order] -= 1
+    assert (left == 0).all()
+    return rows
+
+
+def test_prefill_item_width_boundaries(ctx, oracle, bank):
+    """The prefill GEMMs run a work item of at most 16 pairs as one 16-column
+    half and a wider one as two halves; an expert's tokens split into items
+    of 32.  Hash-routed tokens (tid2eid rows built here) give experts exactly
+    1, 15, 16, 17, 31, 32, 33, 47, 48 and 49 tokens, so items of 1, 15, 16,
+    17, 31 and 32 pairs and every split across the 32 and 16 boundaries
+    occur: routes as built, stage checks (h codes, w2 GEMM, combine) on every
+    pair of those experts, outputs within the prefill's gates, and the first
+    40 tokens of the run equal a 40-token run bit for bit although their
+    experts' items (and widths) differ between the two runs."""
+    T = 64
+    targets = {3: 1, 11: 15, 29: 16, 47: 17, 60: 31, 77: 32, 95: 33, 120: 47, 150: 48, 201: 49}
+    say(f"prefill item widths T={T}: expert token counts {sorted(targets.values())}")
+    rows = _boundary_routes(T, targets)
+    counts = np.bincount(rows.ravel(), minlength=256)
+    assert all(counts[e] == c for e, c in targets.items())
+    xs = synth.prefill_tokens(seed=3, tokens=T)
+    tok = np.arange(T, dtype=np.int32)
+    router = s14.Router(bank["wr_d"], bank["bias_d"], tid2eid=torch.from_numpy(rows).cuda(), token_ids=dev(tok))
+    y = torch.empty((T, HIDDEN), dtype=torch.float32, device="cuda")
+    ids = torch.empty((T, 6), dtype=torch.int16, device="cuda")
+    wts = torch.empty((T, 6), dtype=torch.float32, device="cuda")
+    s14.moe_prefill(ctx, T, router, bank["table"], bank["pages"][256], dev(xs), y, ids, wts)
+    got, ids_h, wts_h = host(y), host(ids).astype(np.int64), host(wts)
+    assert (ids_h == rows).all(), "hash routes"
+    st = s14.last_prefill_stats(ctx)
+    assert st["items"] == int(np.sum((counts + 31) // 32)) + (T + 31) // 32
+    view = s14.last_prefill_view(ctx)
+    widths = sorted({int(c) for c in view["items"][:, 2]})
+    for w in (1, 15, 16, 17, 31, 32):
+        assert w in widths, f"no item of {w} pairs: {widths}"
+    check = sorted(int(view["token_pair"][t][s_]) for t in range(T) for s_ in range(6) if int(rows[t, s_]) in targets)
+    _check_prefill_stages(oracle, bank, view, xs, ids_h, wts_h, got, check)
+    shared = page_host(bank, 256)
+    for t in (0, 37, 63):
+        want = oracle.moe_prefill_token(xs[t], [page_host(bank, int(e)) for e in rows[t]], wts_h[t], shared)
+        _prefill_close(oracle, got[t], want, f"token {t}")
+    # batch invariance across item widths
+    T2 = 40
+    y2 = torch.empty((T2, HIDDEN), dtype=torch.float32, device="cuda")
+    s14.moe_prefill(ctx, T2, router, bank["table"], bank["pages"][256], dev(np.ascontiguousarray(xs[:T2])), y2)
+    assert_bit_exact(host(y2), got[:T2], f"first {T2} tokens of T={T} vs T={T2}")
+    ctx.launch_status()
+
+
 def test_nonresident_page_is_reported_not_read(ctx, oracle, bank, prefill_router):
     """A routed expert whose page-table entry is 0 (not resident): the one-token
     single-launch kernel, a block launch and a prefill each read the shared
