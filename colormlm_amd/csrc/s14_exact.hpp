@@ -719,6 +719,78 @@ __device__ __forceinline__ void fp8q_load(Fp8QBatch &b, Rsrc w, Rsrc sc, uint32_
   for (int i = 0; i < 4; ++i) b.w[i] = ld8(w, woff + 32u * uint32_t(g0 + i));
   b.s = fp8_scale(sc, soff, uint32_t(g0) / 4u, scale_f32);
 }
+// quad_chain8 over p with the next group's FP8 products q = (x * e4m3) * s
+// formed in its gaps, written as one asm statement because the compiler
+// gathers such code into runs of its own whatever barriers stand between
+// (its instruction selection orders arithmetic by data dependence only):
+// each of the 32 dependent adds leaves room for one independent
+// instruction, and each hand-over add (0, 8, 16, 24: a DPP read of the sum
+// that the add before it has just written, which needs two wait states)
+// gets two.  Gap schedule: the eight conversions (one code each, byte b
+// chosen by op_sel), then the x products, then the scalings, each at least
+// one gap after what it reads.  The statement ends on an add of acc, so a
+// DPP read of acc by compiled code after it takes fp8_chain_end first.
+__device__ __forceinline__ float fp8_quad_chain8_asm(float acc, const float (&p)[8], float (&q)[8], uint2 w, float s,
+                                                     const float (&xv)[8]) {
+#define S14_DPP "quad_perm:[3,0,1,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+#define S14_A(k) "v_add_f32 %[acc], %[acc], %[p" #k "]\n\t"
+#define S14_AD "v_add_f32_dpp %[acc], %[acc], %[p0] " S14_DPP
+#define S14_C(k, w, sel) "v_cvt_scalef32_f32_fp8 %[q" #k "], %[" #w "], 1.0" sel "\n\t"
+#define S14_M(k) "v_mul_f32 %[q" #k "], %[x" #k "], %[q" #k "]\n\t"
+#define S14_S(k) "v_mul_f32 %[q" #k "], %[q" #k "], %[s]\n\t"
+  asm volatile(
+      // step 0
+      S14_C(0, wx, "") S14_C(1, wx, " op_sel:[1,0,0]") S14_AD
+      S14_C(2, wx, " op_sel:[0,1,0]") S14_A(1)
+      S14_C(3, wx, " op_sel:[1,1,0]") S14_A(2)
+      S14_C(4, wy, "") S14_A(3)
+      S14_C(5, wy, " op_sel:[1,0,0]") S14_A(4)
+      S14_C(6, wy, " op_sel:[0,1,0]") S14_A(5)
+      S14_C(7, wy, " op_sel:[1,1,0]") S14_A(6)
+      S14_M(0) S14_A(7)
+      // step 1
+      S14_M(1) S14_M(2) S14_AD
+      S14_M(3) S14_A(1)
+      S14_M(4) S14_A(2)
+      S14_M(5) S14_A(3)
+      S14_M(6) S14_A(4)
+      S14_M(7) S14_A(5)
+      S14_S(0) S14_A(6)
+      S14_S(1) S14_A(7)
+      // step 2
+      S14_S(2) S14_S(3) S14_AD
+      S14_S(4) S14_A(1)
+      S14_S(5) S14_A(2)
+      S14_A(3) S14_A(4) S14_A(5) S14_A(6) S14_A(7)
+      // step 3
+      S14_S(6) S14_S(7) S14_AD
+      S14_A(1) S14_A(2) S14_A(3) S14_A(4) S14_A(5) S14_A(6) S14_A(7)
+      : [acc] "+v"(acc), [q0] "=&v"(q[0]), [q1] "=&v"(q[1]), [q2] "=&v"(q[2]), [q3] "=&v"(q[3]),
+        [q4] "=&v"(q[4]), [q5] "=&v"(q[5]), [q6] "=&v"(q[6]), [q7] "=&v"(q[7])
+      : [p0] "v"(p[0]), [p1] "v"(p[1]), [p2] "v"(p[2]), [p3] "v"(p[3]), [p4] "v"(p[4]), [p5] "v"(p[5]),
+        [p6] "v"(p[6]), [p7] "v"(p[7]), [x0] "v"(xv[0]), [x1] "v"(xv[1]), [x2] "v"(xv[2]), [x3] "v"(xv[3]),
+        [x4] "v"(xv[4]), [x5] "v"(xv[5]), [x6] "v"(xv[6]), [x7] "v"(xv[7]), [wx] "v"(w.x), [wy] "v"(w.y),
+        [s] "v"(s));
+#undef S14_DPP
+#undef S14_A
+#undef S14_AD
+#undef S14_C
+#undef S14_M
+#undef S14_S
+  return acc;
+}
+// Two wait states after fp8_quad_chain8_asm's last write of acc, before
+// compiled code reads it through DPP (acc passes through the statement, so
+// that read cannot move above it).
+__device__ __forceinline__ float fp8_chain_end(float acc) {
+  asm volatile("s_nop 1" : "+v"(acc));
+  return acc;
+}
+// x of one group for a quad lane (8 values from LDS).
+__device__ __forceinline__ void fp8_x8(float (&xv)[8], const float *__restrict__ x) {
+  const float4 xa = *reinterpret_cast<const float4 *>(x), xb = *reinterpret_cast<const float4 *>(x + 4);
+  xv[0] = xa.x, xv[1] = xa.y, xv[2] = xa.z, xv[3] = xa.w, xv[4] = xb.x, xv[5] = xb.y, xv[6] = xb.z, xv[7] = xb.w;
+}
 // Dot of one FP8 row of G groups (G % (4 NB) == 0) with x in LDS (xq = x +
 // 8 q); NB batches in flight.  Result in every lane of the quad.
 template <int NB>
@@ -730,18 +802,25 @@ __device__ __forceinline__ float fp8_row_quad(Rsrc w, Rsrc sc, uint32_t woff, ui
   float acc = 0.0f;
   for (int g0 = 0; g0 < G; g0 += 4 * NB) {
     const bool refill = g0 + 4 * NB < G;  // uniform
-    // software-pipelined as mx_row_quad: group n+1's products ahead of group
-    // n's chain
-    float pc[8], pn[8];
+    // software-pipelined: group n+1's products formed in the gaps of group
+    // n's chain, from x read from LDS a group before that
+    float pc[8], pn[8], xn[8];
     fp8_products8(pc, b[0].w[0], b[0].s, xq + 32 * g0);
+    fp8_x8(xn, xq + 32 * (g0 + 1));
 #pragma unroll
     for (int n = 0; n < 4 * NB; ++n) {
       const int j = n / 4, i = n % 4;
       if (n + 1 < 4 * NB) {
         const int jn = (n + 1) / 4, in = (n + 1) % 4;
-        fp8_products8(pn, b[jn].w[in], b[jn].s, xq + 32 * (g0 + n + 1));
+        float xa[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) xa[k] = xn[k];
+        if (n + 2 < 4 * NB) fp8_x8(xn, xq + 32 * (g0 + n + 2));
+        acc = fp8_quad_chain8_asm(acc, pc, pn, b[jn].w[in], b[jn].s, xa);
+        if (n + 2 == 4 * NB) acc = fp8_chain_end(acc);
+      } else {
+        acc = quad_chain8(acc, pc);
       }
-      acc = quad_chain8(acc, pc);
       if (i == 3 && refill) fp8q_load(b[j], w, sc, woff, soff, scale_f32, g0 + 4 * NB + 4 * j);
 #pragma unroll
       for (int k = 0; k < 8; ++k) pc[k] = pn[k];

@@ -202,6 +202,43 @@ def test_fp8_ue8m0_reference_variant_exact(pipes, oracle, n, k):
     assert_bit_exact(host(y), oracle.fp8_matvec_ue8m0(x, w, s), "fp8 ue8m0 exact")
 
 
+def test_fp8_quad_exact_every_code(pipes, oracle):
+    """The lane-quad EXACT FP8 matvec (k % 1024 == 0) over every finite e4m3
+    code in every byte position of a lane's words, with zeros, -0 and
+    subnormal x, and scales small enough that products fall into the f32
+    subnormal range: both scale kinds and both x kinds."""
+    say("fp8 quad exact: every code, subnormal products")
+    n, k = 256, 2048
+    w = ((np.arange(n)[:, None] * 5 + np.arange(k)[None, :]) % 256).astype(np.uint8)
+    w[(w & 0x7F) == 0x7F] = 0x7E  # the NaN codes
+    tiles = (n // 128, k // 128)
+    # f32 x with zeros, -0 and subnormals; UE8M0 codes down to 2^-126
+    x = synth.gen_normal(16, 1, k)
+    x[::97] = 0.0
+    x[5::97] = -0.0
+    x[11::53] = np.float32(1e-40)
+    x[13::61] = np.float32(-3e-39)
+    s = (np.arange(tiles[0] * tiles[1]).reshape(tiles) * 17 % 140 + 1).astype(np.uint8)
+    s_words = np.zeros(-(-s.size // 4) * 4, dtype=np.uint8)
+    s_words[: s.size] = s.reshape(-1)
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    d = pipes.bind_fp8(s14.S14MatvecShape.new(n, k).validate_fp8(), dev(x), dev(w), dev(s_words), y, mode=s14.EXACT)
+    pipes.cmd_fp8_matvec(d)
+    assert_bit_exact(host(y), oracle.fp8_matvec_ue8m0(x, w, s), "fp8 quad ue8m0 every code")
+    # bf16 x with zeros, -0 and subnormals; f32 scales from 2^-120 to 1
+    xb = (synth.gen_bytes(16, 2, 2 * k).view(np.uint16) & 0x3FFF) | ((np.arange(k) % 2) << 15).astype(np.uint16)
+    xb[::89] = 0x0000
+    xb[7::89] = 0x8000
+    xb[3::41] = 0x0001 | ((np.arange(k)[3::41] % 2) << 15).astype(np.uint16)
+    sf = np.exp2(-(np.arange(tiles[0] * tiles[1]) * 29 % 121)).astype(np.float32).reshape(tiles)
+    y2 = torch.empty(n, dtype=torch.float32, device="cuda")
+    d2 = pipes.bind_fp8(
+        s14.S14MatvecShape.new(n, k).validate_fp8(), dev(xb).view(torch.bfloat16), dev(w), dev(sf), y2, mode=s14.EXACT
+    )
+    pipes.cmd_fp8_matvec(d2)
+    assert_bit_exact(host(y2), oracle.fp8_matvec_f32scale_bf16x(xb, w, sf), "fp8 quad f32-scale bf16-x every code")
+
+
 def test_swiglu_route_mix_accumulate_bit_exact(pipes, oracle):
     say("swiglu / route_mix / moe_accumulate")
     n = 1 << 20
