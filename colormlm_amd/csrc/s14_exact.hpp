@@ -174,102 +174,83 @@ __device__ __forceinline__ float pair_chain16(float acc, const float (&p)[16]) {
   return acc;
 }
 
-// pair_chain16 over p with the next group's scaled products (as
-// mx_products_scaled forms them: scale operand, eight conversions, sixteen
-// multiplies) placed one after each of the chain's adds.  An add waits
-// about 8 cycles for the one before it and issues in about 4.6, so an
-// independent instruction between two adds costs no time; the compiler's
-// own schedule bunches the adds together and the multiplies together.
-// Scheduling barriers around each (add, independent instruction) pair fix
-// this order.  sw: the 4-byte scale word holding the next group's code in
-// byte j (the converters read only their scale operand's exponent field,
-// so one shift forms it).
-__device__ __forceinline__ float pair_chain16_ilv(float acc, const float (&p)[16], float (&q)[16], uint2 w,
-                                                  uint32_t sw, int j, const X16 &x) {
-#define S14_ILV __builtin_amdgcn_sched_barrier(0)
-  v2f d[8];
-  float sc;
-  S14_ILV;
-  sc = __uint_as_float(j < 3 ? sw << (23 - 8 * j) : sw >> 1);
-  acc = __fadd_rn(from_odd(acc), p[0]);
-  S14_ILV;
-  d[0] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.x, sc, 0);
-  acc = __fadd_rn(acc, p[1]);
-  S14_ILV;
-  d[1] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.x, sc, 1);
-  acc = __fadd_rn(acc, p[2]);
-  S14_ILV;
-  d[2] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.x, sc, 2);
-  acc = __fadd_rn(acc, p[3]);
-  S14_ILV;
-  d[3] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.x, sc, 3);
-  acc = __fadd_rn(acc, p[4]);
-  S14_ILV;
-  q[0] = __fmul_rn(x.v[0], d[0].x);
-  acc = __fadd_rn(acc, p[5]);
-  S14_ILV;
-  q[1] = __fmul_rn(x.v[1], d[0].y);
-  acc = __fadd_rn(acc, p[6]);
-  S14_ILV;
-  d[4] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.y, sc, 0);
-  acc = __fadd_rn(acc, p[7]);
-  S14_ILV;
-  q[2] = __fmul_rn(x.v[2], d[1].x);
-  acc = __fadd_rn(acc, p[8]);
-  S14_ILV;
-  q[3] = __fmul_rn(x.v[3], d[1].y);
-  acc = __fadd_rn(acc, p[9]);
-  S14_ILV;
-  d[5] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.y, sc, 1);
-  acc = __fadd_rn(acc, p[10]);
-  S14_ILV;
-  q[4] = __fmul_rn(x.v[4], d[2].x);
-  acc = __fadd_rn(acc, p[11]);
-  S14_ILV;
-  q[5] = __fmul_rn(x.v[5], d[2].y);
-  acc = __fadd_rn(acc, p[12]);
-  S14_ILV;
-  d[6] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.y, sc, 2);
-  acc = __fadd_rn(acc, p[13]);
-  S14_ILV;
-  q[6] = __fmul_rn(x.v[6], d[3].x);
-  acc = __fadd_rn(acc, p[14]);
-  S14_ILV;
-  q[7] = __fmul_rn(x.v[7], d[3].y);
-  acc = __fadd_rn(acc, p[15]);
-  S14_ILV;
-  d[7] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.y, sc, 3);
-  acc = __fadd_rn(from_even(acc), p[0]);
-  S14_ILV;
-  q[8] = __fmul_rn(x.v[8], d[4].x);
-  acc = __fadd_rn(acc, p[1]);
-  S14_ILV;
-  q[9] = __fmul_rn(x.v[9], d[4].y);
-  acc = __fadd_rn(acc, p[2]);
-  S14_ILV;
-  q[10] = __fmul_rn(x.v[10], d[5].x);
-  acc = __fadd_rn(acc, p[3]);
-  S14_ILV;
-  q[11] = __fmul_rn(x.v[11], d[5].y);
-  acc = __fadd_rn(acc, p[4]);
-  S14_ILV;
-  q[12] = __fmul_rn(x.v[12], d[6].x);
-  acc = __fadd_rn(acc, p[5]);
-  S14_ILV;
-  q[13] = __fmul_rn(x.v[13], d[6].y);
-  acc = __fadd_rn(acc, p[6]);
-  S14_ILV;
-  q[14] = __fmul_rn(x.v[14], d[7].x);
-  acc = __fadd_rn(acc, p[7]);
-  S14_ILV;
-  q[15] = __fmul_rn(x.v[15], d[7].y);
-  acc = __fadd_rn(acc, p[8]);
-  S14_ILV;
-#pragma unroll
-  for (int k = 9; k < 16; ++k) acc = __fadd_rn(acc, p[k]);
-  S14_ILV;
-#undef S14_ILV
+// pair_chain16 over p with the next group's scaled products q = x * (e2m1
+// * 2^(c-127)) (as mx_products_scaled forms them) in its gaps.  An add
+// waits about 8 cycles for the one before it and issues in about 4.6, so
+// an independent instruction between two adds costs no time; the
+// compiler gathers such code into runs of its own whatever barriers stand
+// between (its instruction selection orders arithmetic by data dependence
+// only), so the group is one asm statement: one independent instruction
+// before each add, two before each hand-over add (0 and 16, a DPP read of
+// the sum the add before it has just written, which needs two wait
+// states).  The eight converters (byte b of a code word chosen by op_sel)
+// write three register pairs in turn, v[0:1], v[2:3] and v[4:5], named in
+// the statement (an operand cannot name one half of a pair) and so listed
+// as clobbered; each pair's two multiplies follow its converter a gap or
+// more later.  sc: the converters' scale operand (2^(c-127); they read its
+// exponent field only).  The statement ends on an add of acc, so a DPP
+// read of acc by compiled code after it takes asm_chain_end first.
+__device__ __forceinline__ float pair_chain16_asm(float acc, const float (&p)[16], float (&q)[16], uint2 w, float sc,
+                                                  const X16 &x) {
+#define S14_A(k) "v_add_f32 %[acc], %[acc], %[p" #k "]\n\t"
+#define S14_AD(sel) "v_add_f32_dpp %[acc], %[acc], %[p0] quad_perm:" sel " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+#define S14_C(t, w, sel) "v_cvt_scalef32_pk_f32_fp4 v[" t "], %[" #w "], %[sc]" sel "\n\t"
+#define S14_M(k, r) "v_mul_f32 %[q" #k "], %[x" #k "], v" r "\n\t"
+  asm volatile(
+      // the even lane's half: the sum from the odd lane, then 16 products
+      S14_C("0:1", wx, "") S14_C("2:3", wx, " op_sel:[1,0,0]") S14_AD("[1,1,3,3]")
+      S14_C("4:5", wx, " op_sel:[0,1,0]") S14_A(1)
+      S14_M(0, "0") S14_A(2)
+      S14_M(1, "1") S14_A(3)
+      S14_C("0:1", wx, " op_sel:[1,1,0]") S14_A(4)
+      S14_M(2, "2") S14_A(5)
+      S14_M(3, "3") S14_A(6)
+      S14_C("2:3", wy, "") S14_A(7)
+      S14_M(4, "4") S14_A(8)
+      S14_M(5, "5") S14_A(9)
+      S14_C("4:5", wy, " op_sel:[1,0,0]") S14_A(10)
+      S14_M(6, "0") S14_A(11)
+      S14_M(7, "1") S14_A(12)
+      S14_C("0:1", wy, " op_sel:[0,1,0]") S14_A(13)
+      S14_M(8, "2") S14_A(14)
+      S14_M(9, "3") S14_A(15)
+      // the odd lane's half: the sum from the even lane
+      S14_C("2:3", wy, " op_sel:[1,1,0]") S14_M(10, "4") S14_AD("[0,0,2,2]")
+      S14_M(11, "5") S14_A(1)
+      S14_M(12, "0") S14_A(2)
+      S14_M(13, "1") S14_A(3)
+      S14_M(14, "2") S14_A(4)
+      S14_M(15, "3") S14_A(5)
+      S14_A(6) S14_A(7) S14_A(8) S14_A(9) S14_A(10) S14_A(11) S14_A(12) S14_A(13) S14_A(14) S14_A(15)
+      : [acc] "+v"(acc), [q0] "=&v"(q[0]), [q1] "=&v"(q[1]), [q2] "=&v"(q[2]), [q3] "=&v"(q[3]),
+        [q4] "=&v"(q[4]), [q5] "=&v"(q[5]), [q6] "=&v"(q[6]), [q7] "=&v"(q[7]), [q8] "=&v"(q[8]),
+        [q9] "=&v"(q[9]), [q10] "=&v"(q[10]), [q11] "=&v"(q[11]), [q12] "=&v"(q[12]), [q13] "=&v"(q[13]),
+        [q14] "=&v"(q[14]), [q15] "=&v"(q[15])
+      : [p0] "v"(p[0]), [p1] "v"(p[1]), [p2] "v"(p[2]), [p3] "v"(p[3]), [p4] "v"(p[4]), [p5] "v"(p[5]),
+        [p6] "v"(p[6]), [p7] "v"(p[7]), [p8] "v"(p[8]), [p9] "v"(p[9]), [p10] "v"(p[10]), [p11] "v"(p[11]),
+        [p12] "v"(p[12]), [p13] "v"(p[13]), [p14] "v"(p[14]), [p15] "v"(p[15]), [x0] "v"(x.v[0]),
+        [x1] "v"(x.v[1]), [x2] "v"(x.v[2]), [x3] "v"(x.v[3]), [x4] "v"(x.v[4]), [x5] "v"(x.v[5]),
+        [x6] "v"(x.v[6]), [x7] "v"(x.v[7]), [x8] "v"(x.v[8]), [x9] "v"(x.v[9]), [x10] "v"(x.v[10]),
+        [x11] "v"(x.v[11]), [x12] "v"(x.v[12]), [x13] "v"(x.v[13]), [x14] "v"(x.v[14]), [x15] "v"(x.v[15]),
+        [wx] "v"(w.x), [wy] "v"(w.y), [sc] "v"(sc)
+      : "v0", "v1", "v2", "v3", "v4", "v5");
+#undef S14_A
+#undef S14_AD
+#undef S14_C
+#undef S14_M
   return acc;
+}
+// Two wait states after an asm chain statement's last write of acc
+// (pair_chain16_asm, fp8_quad_chain8_asm, mx_quad_chain8_asm), before
+// compiled code reads it through DPP (acc passes through the statement, so
+// that read cannot move above it).
+__device__ __forceinline__ float asm_chain_end(float acc) {
+  asm volatile("s_nop 1" : "+v"(acc));
+  return acc;
+}
+// The converters' scale operand for byte j of scale word sw.
+__device__ __forceinline__ float pair_scale_operand(uint32_t sw, int j) {
+  return __uint_as_float(j < 3 ? sw << (23 - 8 * j) : sw >> 1);
 }
 
 // MXFP4 products of the lane's 8 code bytes (16 k, low nibble first).
@@ -435,7 +416,7 @@ __device__ __forceinline__ float mx_consume(float acc, const MxBatch<PF> &b, con
   }
   if constexpr (!kCheck) {
     // the row's codes were checked once: each group's chain interleaved
-    // with the next group's products (pair_chain16_ilv)
+    // with the next group's products (pair_chain16_asm)
     X16 xa, xb;
     float p[16], q[16];
     load_x16(xa, xh + g0 * 32);
@@ -444,12 +425,13 @@ __device__ __forceinline__ float mx_consume(float acc, const MxBatch<PF> &b, con
 #pragma unroll
     for (int i = 0; i < PF; i += 2) {
       if (i + 2 < PF) load_x16(xa, xh + (g0 + i + 2) * 32);
-      acc = pair_chain16_ilv(acc, p, q, b.w[i + 1], b.c[(i + 1) >> 2], (i + 1) & 3, xb);
+      acc = pair_chain16_asm(acc, p, q, b.w[i + 1], pair_scale_operand(b.c[(i + 1) >> 2], (i + 1) & 3), xb);
       if (i + 3 < PF) load_x16(xb, xh + (g0 + i + 3) * 32);
-      if (i + 2 < PF)
-        acc = pair_chain16_ilv(acc, q, p, b.w[i + 2], b.c[(i + 2) >> 2], (i + 2) & 3, xa);
-      else
-        acc = pair_chain16(acc, q);
+      if (i + 2 < PF) {
+        acc = pair_chain16_asm(acc, q, p, b.w[i + 2], pair_scale_operand(b.c[(i + 2) >> 2], (i + 2) & 3), xa);
+      } else {
+        acc = pair_chain16(asm_chain_end(acc), q);
+      }
     }
   } else if (__builtin_amdgcn_ballot_w64(!ok) == 0) {
     X16 xa, xb;
@@ -729,7 +711,7 @@ __device__ __forceinline__ void fp8q_load(Fp8QBatch &b, Rsrc w, Rsrc sc, uint32_
 // gets two.  Gap schedule: the eight conversions (one code each, byte b
 // chosen by op_sel), then the x products, then the scalings, each at least
 // one gap after what it reads.  The statement ends on an add of acc, so a
-// DPP read of acc by compiled code after it takes fp8_chain_end first.
+// DPP read of acc by compiled code after it takes asm_chain_end first.
 __device__ __forceinline__ float fp8_quad_chain8_asm(float acc, const float (&p)[8], float (&q)[8], uint2 w, float s,
                                                      const float (&xv)[8]) {
 #define S14_DPP "quad_perm:[3,0,1,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
@@ -779,15 +761,8 @@ __device__ __forceinline__ float fp8_quad_chain8_asm(float acc, const float (&p)
 #undef S14_S
   return acc;
 }
-// Two wait states after fp8_quad_chain8_asm's last write of acc, before
-// compiled code reads it through DPP (acc passes through the statement, so
-// that read cannot move above it).
-__device__ __forceinline__ float fp8_chain_end(float acc) {
-  asm volatile("s_nop 1" : "+v"(acc));
-  return acc;
-}
 // x of one group for a quad lane (8 values from LDS).
-__device__ __forceinline__ void fp8_x8(float (&xv)[8], const float *__restrict__ x) {
+__device__ __forceinline__ void quad_x8(float (&xv)[8], const float *__restrict__ x) {
   const float4 xa = *reinterpret_cast<const float4 *>(x), xb = *reinterpret_cast<const float4 *>(x + 4);
   xv[0] = xa.x, xv[1] = xa.y, xv[2] = xa.z, xv[3] = xa.w, xv[4] = xb.x, xv[5] = xb.y, xv[6] = xb.z, xv[7] = xb.w;
 }
@@ -806,7 +781,7 @@ __device__ __forceinline__ float fp8_row_quad(Rsrc w, Rsrc sc, uint32_t woff, ui
     // n's chain, from x read from LDS a group before that
     float pc[8], pn[8], xn[8];
     fp8_products8(pc, b[0].w[0], b[0].s, xq + 32 * g0);
-    fp8_x8(xn, xq + 32 * (g0 + 1));
+    quad_x8(xn, xq + 32 * (g0 + 1));
 #pragma unroll
     for (int n = 0; n < 4 * NB; ++n) {
       const int j = n / 4, i = n % 4;
@@ -815,9 +790,9 @@ __device__ __forceinline__ float fp8_row_quad(Rsrc w, Rsrc sc, uint32_t woff, ui
         float xa[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) xa[k] = xn[k];
-        if (n + 2 < 4 * NB) fp8_x8(xn, xq + 32 * (g0 + n + 2));
+        if (n + 2 < 4 * NB) quad_x8(xn, xq + 32 * (g0 + n + 2));
         acc = fp8_quad_chain8_asm(acc, pc, pn, b[jn].w[in], b[jn].s, xa);
-        if (n + 2 == 4 * NB) acc = fp8_chain_end(acc);
+        if (n + 2 == 4 * NB) acc = asm_chain_end(acc);
       } else {
         acc = quad_chain8(acc, pc);
       }
@@ -899,72 +874,49 @@ __device__ __forceinline__ bool quad_codes_in(const QuadCodes<G> &qc, CodeWindow
   const bool ok = int(min(mn.x, mn.y)) >= win.cmin && int(max(mx.x, mx.y)) <= win.cmax;
   return __builtin_amdgcn_ballot_w64(!ok) == 0;
 }
-// quad_chain8 over p with the next group's scaled products (mx_products8:
-// scale operand, four conversions, eight multiplies) placed among its adds,
-// one before each hand-over add (which then needs no wait states of its
-// own) and the rest after the first adds of each step; scheduling barriers
-// around each (independent instruction, add) pair fix the order (the
-// compiler's own schedule bunches the adds).  cw: the scale word holding the
-// next group's code in byte j (one shift forms the converters' operand, of
-// which they read only the exponent field); xv: that group's x.
-__device__ __forceinline__ float quad_chain8_ilv(float acc, const float (&p)[8], float (&q)[8], uint32_t w,
-                                                 uint32_t cw, int j, const float (&xv)[8]) {
-#define S14_ILV __builtin_amdgcn_sched_barrier(0)
-  v2f d[4];
-  float sc;
-  S14_ILV;
-  sc = __uint_as_float(j < 3 ? cw << (23 - 8 * j) : cw >> 1);
-  acc = __fadd_rn(from_prev_in_quad(acc), p[0]);
-  S14_ILV;
-  d[0] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 0);
-  acc = __fadd_rn(acc, p[1]);
-  S14_ILV;
-  d[1] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 1);
-  acc = __fadd_rn(acc, p[2]);
-  S14_ILV;
-  d[2] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 2);
-  acc = __fadd_rn(acc, p[3]);
-  S14_ILV;
-  d[3] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 3);
-  acc = __fadd_rn(acc, p[4]);
-  S14_ILV;
-#pragma unroll
-  for (int k = 5; k < 8; ++k) acc = __fadd_rn(acc, p[k]);
-  S14_ILV;
-  q[0] = __fmul_rn(xv[0], d[0].x);
-  acc = __fadd_rn(from_prev_in_quad(acc), p[0]);
-  S14_ILV;
-  q[1] = __fmul_rn(xv[1], d[0].y);
-  acc = __fadd_rn(acc, p[1]);
-  S14_ILV;
-  q[2] = __fmul_rn(xv[2], d[1].x);
-  acc = __fadd_rn(acc, p[2]);
-  S14_ILV;
-#pragma unroll
-  for (int k = 3; k < 8; ++k) acc = __fadd_rn(acc, p[k]);
-  S14_ILV;
-  q[3] = __fmul_rn(xv[3], d[1].y);
-  acc = __fadd_rn(from_prev_in_quad(acc), p[0]);
-  S14_ILV;
-  q[4] = __fmul_rn(xv[4], d[2].x);
-  acc = __fadd_rn(acc, p[1]);
-  S14_ILV;
-  q[5] = __fmul_rn(xv[5], d[2].y);
-  acc = __fadd_rn(acc, p[2]);
-  S14_ILV;
-#pragma unroll
-  for (int k = 3; k < 8; ++k) acc = __fadd_rn(acc, p[k]);
-  S14_ILV;
-  q[6] = __fmul_rn(xv[6], d[3].x);
-  acc = __fadd_rn(from_prev_in_quad(acc), p[0]);
-  S14_ILV;
-  q[7] = __fmul_rn(xv[7], d[3].y);
-  acc = __fadd_rn(acc, p[1]);
-  S14_ILV;
-#pragma unroll
-  for (int k = 2; k < 8; ++k) acc = __fadd_rn(acc, p[k]);
-  S14_ILV;
-#undef S14_ILV
+// quad_chain8 over p with the next group's scaled products q = x * (e2m1 *
+// 2^(c-127)) (as mx_products8 forms them) in its gaps, one asm statement
+// as pair_chain16_asm: the four converters write v[0:1], v[2:3] and
+// v[4:5] in turn (clobbered), each pair's multiplies a gap or more later;
+// each hand-over add gets two independent instructions before it, or,
+// once those run out, two wait states.  sc: the converters' scale operand;
+// xv: that group's x.  Ends on an add of acc (asm_chain_end before a DPP
+// read by compiled code).
+__device__ __forceinline__ float mx_quad_chain8_asm(float acc, const float (&p)[8], float (&q)[8], uint32_t w,
+                                                    float sc, const float (&xv)[8]) {
+#define S14_A(k) "v_add_f32 %[acc], %[acc], %[p" #k "]\n\t"
+#define S14_AD "v_add_f32_dpp %[acc], %[acc], %[p0] quad_perm:[3,0,1,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+#define S14_C(t, sel) "v_cvt_scalef32_pk_f32_fp4 v[" t "], %[w], %[sc]" sel "\n\t"
+#define S14_M(k, r) "v_mul_f32 %[q" #k "], %[x" #k "], v" r "\n\t"
+  asm volatile(
+      // step 0
+      S14_C("0:1", "") S14_C("2:3", " op_sel:[1,0,0]") S14_AD
+      S14_C("4:5", " op_sel:[0,1,0]") S14_A(1)
+      S14_M(0, "0") S14_A(2)
+      S14_M(1, "1") S14_A(3)
+      S14_C("0:1", " op_sel:[1,1,0]") S14_A(4)
+      S14_M(2, "2") S14_A(5)
+      S14_A(6) S14_A(7)
+      // step 1
+      S14_M(3, "3") S14_M(4, "4") S14_AD
+      S14_M(5, "5") S14_A(1)
+      S14_A(2) S14_A(3) S14_A(4) S14_A(5) S14_A(6) S14_A(7)
+      // step 2
+      S14_M(6, "0") S14_M(7, "1") S14_AD
+      S14_A(1) S14_A(2) S14_A(3) S14_A(4) S14_A(5) S14_A(6) S14_A(7)
+      // step 3
+      "s_nop 1\n\t" S14_AD
+      S14_A(1) S14_A(2) S14_A(3) S14_A(4) S14_A(5) S14_A(6) S14_A(7)
+      : [acc] "+v"(acc), [q0] "=&v"(q[0]), [q1] "=&v"(q[1]), [q2] "=&v"(q[2]), [q3] "=&v"(q[3]),
+        [q4] "=&v"(q[4]), [q5] "=&v"(q[5]), [q6] "=&v"(q[6]), [q7] "=&v"(q[7])
+      : [p0] "v"(p[0]), [p1] "v"(p[1]), [p2] "v"(p[2]), [p3] "v"(p[3]), [p4] "v"(p[4]), [p5] "v"(p[5]),
+        [p6] "v"(p[6]), [p7] "v"(p[7]), [x0] "v"(xv[0]), [x1] "v"(xv[1]), [x2] "v"(xv[2]), [x3] "v"(xv[3]),
+        [x4] "v"(xv[4]), [x5] "v"(xv[5]), [x6] "v"(xv[6]), [x7] "v"(xv[7]), [w] "v"(w), [sc] "v"(sc)
+      : "v0", "v1", "v2", "v3", "v4", "v5");
+#undef S14_A
+#undef S14_AD
+#undef S14_C
+#undef S14_M
   return acc;
 }
 
@@ -979,20 +931,23 @@ __device__ __forceinline__ float mx_row_quad_as(MxQBatch (&b)[NB], Rsrc r, uint3
 #pragma unroll 1
   for (int g0 = 0; g0 < G; g0 += 4 * NB) {
     const bool refill = g0 + 4 * NB < G;  // uniform
-    // software-pipelined: group n+1's x reads and products are issued ahead
-    // of group n's chain, so they fill the gaps between its dependent adds
-    float pc[8], pn[8];
+    // software-pipelined: group n+1's products are formed in the gaps of
+    // group n's chain (scaled decode), from x read from LDS a group before
+    float pc[8], pn[8], xn[8];
     mx_products8<kScaled>(pc, b[0].w[0], b[0].c & 255u, xq + 32 * g0);
+    if constexpr (kScaled) quad_x8(xn, xq + 32 * (g0 + 1));
 #pragma unroll
     for (int n = 0; n < 4 * NB; ++n) {
       const int j = n / 4, i = n % 4;
       if (n + 1 < 4 * NB) {
         const int jn = (n + 1) / 4, in = (n + 1) % 4;
         if constexpr (kScaled) {
-          const float *x = xq + 32 * (g0 + n + 1);
-          const float4 xa = *reinterpret_cast<const float4 *>(x), xb = *reinterpret_cast<const float4 *>(x + 4);
-          const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-          acc = quad_chain8_ilv(acc, pc, pn, b[jn].w[in], b[jn].c, in, xv);
+          float xa[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) xa[k] = xn[k];
+          if (n + 2 < 4 * NB) quad_x8(xn, xq + 32 * (g0 + n + 2));
+          acc = mx_quad_chain8_asm(acc, pc, pn, b[jn].w[in], pair_scale_operand(b[jn].c, in), xa);
+          if (n + 2 == 4 * NB) acc = asm_chain_end(acc);
         } else {
           mx_products8<kScaled>(pn, b[jn].w[in], (b[jn].c >> (8 * in)) & 255u, xq + 32 * (g0 + n + 1));
           acc = quad_chain8(acc, pc);
