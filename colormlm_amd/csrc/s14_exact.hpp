@@ -708,51 +708,54 @@ __device__ __forceinline__ void fp8q_load(Fp8QBatch &b, Rsrc w, Rsrc sc, uint32_
 // each of the 32 dependent adds leaves room for one independent
 // instruction, and each hand-over add (0, 8, 16, 24: a DPP read of the sum
 // that the add before it has just written, which needs two wait states)
-// gets two.  Gap schedule: the eight conversions (one code each, byte b
-// chosen by op_sel), then the x products, then the scalings, each at least
-// one gap after what it reads.  The statement ends on an add of acc, so a
-// DPP read of acc by compiled code after it takes asm_chain_end first.
+// gets two (or, once the independent work runs out, two wait states).
+// Gap schedule: the four conversions (two codes each, the word's low or
+// high half chosen by op_sel) write three register pairs in turn, v[0:1],
+// v[2:3] and v[4:5], named in the statement (an operand cannot name one
+// half of a pair) and so listed as clobbered; then the x products, then
+// the scalings, each at least one gap after what it reads.  The statement
+// ends on an add of acc, so a DPP read of acc by compiled code after it
+// takes asm_chain_end first.
 __device__ __forceinline__ float fp8_quad_chain8_asm(float acc, const float (&p)[8], float (&q)[8], uint2 w, float s,
                                                      const float (&xv)[8]) {
 #define S14_DPP "quad_perm:[3,0,1,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
 #define S14_A(k) "v_add_f32 %[acc], %[acc], %[p" #k "]\n\t"
 #define S14_AD "v_add_f32_dpp %[acc], %[acc], %[p0] " S14_DPP
-#define S14_C(k, w, sel) "v_cvt_scalef32_f32_fp8 %[q" #k "], %[" #w "], 1.0" sel "\n\t"
-#define S14_M(k) "v_mul_f32 %[q" #k "], %[x" #k "], %[q" #k "]\n\t"
+#define S14_C(t, w, sel) "v_cvt_scalef32_pk_f32_fp8 v[" t "], %[" #w "], 1.0" sel "\n\t"
+#define S14_M(k, r) "v_mul_f32 %[q" #k "], %[x" #k "], v" r "\n\t"
 #define S14_S(k) "v_mul_f32 %[q" #k "], %[q" #k "], %[s]\n\t"
   asm volatile(
       // step 0
-      S14_C(0, wx, "") S14_C(1, wx, " op_sel:[1,0,0]") S14_AD
-      S14_C(2, wx, " op_sel:[0,1,0]") S14_A(1)
-      S14_C(3, wx, " op_sel:[1,1,0]") S14_A(2)
-      S14_C(4, wy, "") S14_A(3)
-      S14_C(5, wy, " op_sel:[1,0,0]") S14_A(4)
-      S14_C(6, wy, " op_sel:[0,1,0]") S14_A(5)
-      S14_C(7, wy, " op_sel:[1,1,0]") S14_A(6)
-      S14_M(0) S14_A(7)
+      S14_C("0:1", wx, "") S14_C("2:3", wx, " op_sel:[1,0,0]") S14_AD
+      S14_C("4:5", wy, "") S14_A(1)
+      S14_M(0, "0") S14_A(2)
+      S14_M(1, "1") S14_A(3)
+      S14_C("0:1", wy, " op_sel:[1,0,0]") S14_A(4)
+      S14_M(2, "2") S14_A(5)
+      S14_M(3, "3") S14_A(6)
+      S14_M(4, "4") S14_A(7)
       // step 1
-      S14_M(1) S14_M(2) S14_AD
-      S14_M(3) S14_A(1)
-      S14_M(4) S14_A(2)
-      S14_M(5) S14_A(3)
-      S14_M(6) S14_A(4)
-      S14_M(7) S14_A(5)
-      S14_S(0) S14_A(6)
-      S14_S(1) S14_A(7)
+      S14_M(5, "5") S14_M(6, "0") S14_AD
+      S14_M(7, "1") S14_A(1)
+      S14_S(0) S14_A(2)
+      S14_S(1) S14_A(3)
+      S14_S(2) S14_A(4)
+      S14_S(3) S14_A(5)
+      S14_S(4) S14_A(6)
+      S14_S(5) S14_A(7)
       // step 2
-      S14_S(2) S14_S(3) S14_AD
-      S14_S(4) S14_A(1)
-      S14_S(5) S14_A(2)
-      S14_A(3) S14_A(4) S14_A(5) S14_A(6) S14_A(7)
-      // step 3
       S14_S(6) S14_S(7) S14_AD
+      S14_A(1) S14_A(2) S14_A(3) S14_A(4) S14_A(5) S14_A(6) S14_A(7)
+      // step 3
+      "s_nop 1\n\t" S14_AD
       S14_A(1) S14_A(2) S14_A(3) S14_A(4) S14_A(5) S14_A(6) S14_A(7)
       : [acc] "+v"(acc), [q0] "=&v"(q[0]), [q1] "=&v"(q[1]), [q2] "=&v"(q[2]), [q3] "=&v"(q[3]),
         [q4] "=&v"(q[4]), [q5] "=&v"(q[5]), [q6] "=&v"(q[6]), [q7] "=&v"(q[7])
       : [p0] "v"(p[0]), [p1] "v"(p[1]), [p2] "v"(p[2]), [p3] "v"(p[3]), [p4] "v"(p[4]), [p5] "v"(p[5]),
         [p6] "v"(p[6]), [p7] "v"(p[7]), [x0] "v"(xv[0]), [x1] "v"(xv[1]), [x2] "v"(xv[2]), [x3] "v"(xv[3]),
         [x4] "v"(xv[4]), [x5] "v"(xv[5]), [x6] "v"(xv[6]), [x7] "v"(xv[7]), [wx] "v"(w.x), [wy] "v"(w.y),
-        [s] "v"(s));
+        [s] "v"(s)
+      : "v0", "v1", "v2", "v3", "v4", "v5");
 #undef S14_DPP
 #undef S14_A
 #undef S14_AD
